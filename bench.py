@@ -1,0 +1,348 @@
+"""Benchmark of the MoE-HLM expert layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5] [--no-cpu-baseline]
+
+A step is one forward pass of the layer over one batch of synthetic input
+(inputs resident in HBM before timing starts).  The headline workload is
+the bf16 prefill-shape layer, N=8192 tokens, d=128
+multivectors, E=32 experts, top-4, expert FFN 128 -> 512 -> 128 with the
+grade-wise GELU, Zipf(1.2) expert load.  Configs 1, 2, 4 and 5 are timed in
+the same run and reported under "configs".
+
+One JSON line is printed.  ``roofline`` covers the dominant kernel, the
+grouped CliffordLinear MFMA kernel (both expert products), from HIP events
+around its launches on the stream it runs on; ``cpu_baseline`` times the
+reference's own compiled CPU geometric matmul (``oracle/_ref``, built from
+the reference sources) -- or the C restatement if that is absent -- plus the
+NumPy restatement of routing / dispatch / combine, on a bounded sample of
+the same workload, extrapolated linearly in FLOPs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16 = 2.5e15  # dense bf16 MFMA, FLOP/s
+PEAK_F32 = 157.3e12  # fp32 MFMA
+PEAK_HBM = 8.0e12  # bytes/s
+SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c4": 4, "c5": 5}
+
+CONFIGS = {
+    # name: N, d, E, k, F, dtype, weight format, logits kind, layers
+    "c1": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="f32", logits="energy", layers=1),
+    "c2": dict(N=16384, d=128, E=16, k=2, F=0, dtype="f32", fmt=None, logits="normal", layers=1),
+    "c3": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="bf16", logits="zipf", layers=1),
+    "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1),
+    "c5": dict(N=4096, d=256, E=64, k=2, F=1024, dtype="bf16", fmt="bf16", logits="normal_bias", layers=12),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="c3,c1,c2,c4,c5")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-rows", type=int, default=256)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# synthetic inputs (on the device, seeded)
+# ---------------------------------------------------------------------------
+
+
+def make_inputs(torch, c, seed=0):
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    dt = torch.float32 if c["dtype"] == "f32" else torch.bfloat16
+    rn = lambda *s: torch.randn(*s, generator=g, device=dev, dtype=torch.float32)
+    x = rn(N, d, 8).to(dt)
+    layers = []
+    for _ in range(c["layers"]):
+        L = {}
+        if F:
+            L["w_up"] = rn(E, F, d, 8) / (8.0 * d) ** 0.5
+            L["w_down"] = rn(E, d, F, 8) / (8.0 * F) ** 0.5
+            if dt == torch.bfloat16:
+                L["w_up"] = L["w_up"].bfloat16().float()
+                L["w_down"] = L["w_down"].bfloat16().float()
+        if c["logits"] == "normal":
+            L["logits"] = rn(N, E)
+        elif c["logits"] == "normal_bias":
+            L["logits"] = rn(N, E) + 0.5 * rn(E)[None, :]
+        elif c["logits"] == "zipf":
+            ranking = torch.randperm(E, generator=g, device=dev)
+            p = torch.arange(1, E + 1, device=dev, dtype=torch.float64) ** -1.2
+            chosen = torch.multinomial((p / p.sum()).float().expand(N, E), k, replacement=False, generator=g)
+            lg = 0.1 * rn(N, E)
+            bonus = (k - torch.arange(k, device=dev, dtype=torch.float32)).expand(N, k)
+            lg.scatter_add_(1, ranking[chosen], bonus)
+            L["logits"] = lg.contiguous()
+        else:  # energy router
+            L["router_w"] = 0.1 * rn(E, 4)
+            L["router_b"] = torch.zeros(E, device=dev)
+        layers.append(L)
+    return x, layers
+
+
+# ---------------------------------------------------------------------------
+# GPU timing
+# ---------------------------------------------------------------------------
+
+
+def time_fn(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps  # ms
+
+
+def run_layer_config(torch, ops, name, c, steps, warmup):
+    x, layers = make_inputs(torch, c, seed=SEEDS[name])
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    prepared = []
+    for L in layers:
+        prepared.append(dict(
+            w_up=ops.prepare_weights(L["w_up"], c["fmt"]), w_down=ops.prepare_weights(L["w_down"], c["fmt"]),
+            logits=L.get("logits"), router_w=L.get("router_w"), router_b=L.get("router_b")))
+        del L["w_up"], L["w_down"]
+    torch.cuda.synchronize()
+    ws = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype), device="cuda", dtype=torch.uint8)
+    bufs = [torch.empty_like(x), torch.empty_like(x)]
+    resid = c["layers"] > 1
+    info = {}
+
+    def step():
+        cur = x
+        for li, P in enumerate(prepared):
+            out = bufs[li % 2]
+            _, rt = ops.moe_forward(cur, k, P["w_up"], P["w_down"], None, None, "gelu", logits=P["logits"],
+                                    router_weight=P["router_w"], router_bias=P["router_b"],
+                                    residual=cur if resid else None, workspace=ws, out=out)
+            cur = out
+        info["rt"] = rt
+
+    ms = time_fn(torch, step, steps, warmup)
+    counts = info["rt"]["counts"].cpu()
+    # the dominant kernel: both grouped expert products of layer 0, timed alone
+    P0 = prepared[0]
+    logits = P0["logits"] if P0["logits"] is not None else ops.router_energy_logits(x, P0["router_w"], P0["router_b"])
+    r = ops.route(logits, k)
+    xs = ops.dispatch(x, r, mask_order=True)
+    h = torch.empty((N * k, F, 8), device="cuda", dtype=x.dtype)
+    ys = torch.empty((N * k, d, 8), device="cuda", dtype=x.dtype)
+    fmt_code = ops.WFORMAT_CODE[c["fmt"]]
+    L = ops.lib()
+    st = ops.stream_handle()
+
+    def up():
+        ops.check(L.ygg_grouped_clifford_linear(xs.data_ptr(), N * k, P0["w_up"].data.data_ptr(), fmt_code,
+                                                ops.ptr(P0["w_up"].scales), None, r.offsets.data_ptr(), E, d, F, 1,
+                                                h.data_ptr(), ops.DTYPE_CODE[x.dtype], 0, st))
+
+    def down():
+        ops.check(L.ygg_grouped_clifford_linear(h.data_ptr(), N * k, P0["w_down"].data.data_ptr(), fmt_code,
+                                                ops.ptr(P0["w_down"].scales), None, r.offsets.data_ptr(), E, F, d,
+                                                0, ys.data_ptr(), ops.DTYPE_CODE[x.dtype], 1, st))
+
+    ms_up = time_fn(torch, up, steps, warmup)
+    ms_down = time_fn(torch, down, steps, warmup)
+    ms_route = time_fn(torch, lambda: ops.route(logits, k), steps, warmup)
+    ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, mask_order=True), steps, warmup)
+    ms_comb = time_fn(torch, lambda: ops.combine(ys, r), steps, warmup)
+
+    P = N * k
+    flops_proj = 128.0 * d * F * P  # per projection (algorithmic)
+    es = 4 if c["dtype"] == "f32" else 2
+    R = d * 8 * es
+    rdc_bytes = (4 * N * E + 8 * N * k + 4 * N * k) + (N * R + P * R + 4 * P) + (P * R + 8 * P + N * R)
+    n_touched = int((counts > 0).sum())
+    wbytes_expert = {"bf16": 2 * 2 * 8 * d * F, "int8": 2 * 8 * d * F + 4 * (d + F), "f32": 2 * 4 * 8 * d * F}[c["fmt"]]
+    layer_flops = 2 * flops_proj
+    res = dict(
+        workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"], layers=c["layers"],
+        ms_per_step=ms, tokens_per_s=N / (ms * 1e-3),
+        kernels_ms=dict(route=ms_route, dispatch=ms_disp, expert_up=ms_up, expert_down=ms_down, combine=ms_comb),
+        expert_tflops=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
+        expert_mfma_frac=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / (PEAK_F32 if c["dtype"] == "f32" else PEAK_BF16),
+        layer_tflops=c["layers"] * layer_flops / (ms * 1e-3) / 1e12,
+        route_dispatch_combine_hbm_frac=rdc_bytes / ((ms_route + ms_disp + ms_comb) * 1e-3) / PEAK_HBM,
+        expert_counts_max=int(counts.max()), expert_counts_min=int(counts.min()), experts_touched=n_touched,
+    )
+    if name == "c4":
+        moved = n_touched * wbytes_expert + 2 * N * R + 4 * N * E
+        res["decode_bytes"] = moved
+        res["decode_hbm_frac"] = moved / (ms * 1e-3) / PEAK_HBM
+    res["_flops_per_launch"] = flops_proj
+    res["_ms_per_launch"] = (ms_up + ms_down) / 2
+    return res
+
+
+def run_c2(torch, ops, c, steps, warmup):
+    x, layers = make_inputs(torch, c, seed=2)
+    logits = layers[0]["logits"]
+    N, E, k, d = c["N"], c["E"], c["k"], c["d"]
+    r = ops.route(logits, k)
+    xs = ops.dispatch(x, r)
+
+    def step():
+        rr = ops.route(logits, k)
+        xx = ops.dispatch(x, rr)
+        ops.combine(xx, rr)
+
+    ms = time_fn(torch, step, steps, warmup)
+    ms_route = time_fn(torch, lambda: ops.route(logits, k), steps, warmup)
+    ms_disp = time_fn(torch, lambda: ops.dispatch(x, r), steps, warmup)
+    ms_comb = time_fn(torch, lambda: ops.combine(xs, r), steps, warmup)
+    R = d * 8 * 4
+    P = N * k
+    b_route = 4 * N * E + 8 * N * k + 4 * N * k
+    b_disp = N * R + P * R + 4 * P
+    b_comb = P * R + 8 * P + N * R
+    return dict(workload="c2", N=N, E=E, k=k, d=d, ms_per_step=ms, tokens_per_s=N / (ms * 1e-3),
+                kernels_ms=dict(route=ms_route, dispatch=ms_disp, combine=ms_comb),
+                bytes=b_route + b_disp + b_comb,
+                hbm_frac_step=(b_route + b_disp + b_comb) / (ms * 1e-3) / PEAK_HBM,
+                dispatch_hbm_frac=b_disp / (ms_disp * 1e-3) / PEAK_HBM,
+                combine_hbm_frac=b_comb / (ms_comb * 1e-3) / PEAK_HBM)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (bounded sample)
+# ---------------------------------------------------------------------------
+
+
+def cpu_baseline(c, sample_rows):
+    """Reference CPU path on a bounded sample of config c, extrapolated to the full layer."""
+    import numpy as np
+
+    from oracle import moe, native
+
+    g = np.random.default_rng(11)
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    x = g.standard_normal((N, d, 8), dtype=np.float32)
+    # routing + dispatch + combine over all tokens (NumPy restatement of the reference)
+    t0 = time.perf_counter()
+    probs = moe.softmax(logits)
+    idx, w = moe.topk_reference(probs, k)
+    flat = idx.reshape(-1)
+    tok = np.repeat(np.arange(N), k)
+    out = np.zeros_like(x)
+    for e in range(E):
+        m = flat == e
+        if m.any():
+            rows = x[tok[m]]
+            np.add.at(out, tok[m], w.reshape(-1)[m][:, None, None] * rows)
+    t_rdc = time.perf_counter() - t0
+    # expert FFN on `sample_rows` rows of one expert
+    wu = (g.standard_normal((F, d, 8)) / np.sqrt(8 * d)).astype(np.float32)
+    wd = (g.standard_normal((d, F, 8)) / np.sqrt(8 * F)).astype(np.float32)
+    xs = x[:sample_rows]
+    if native.ref_lib() is not None:
+        gm, kind, what = native.ref_geom_matmul, "reference", "oracle/_ref cl3_geom_matmul_flat (reference C, 1 thread)"
+    else:
+        gm, kind, what = native.c_geom_matmul, "port", "oracle C restatement of cl3_batch_geom_matmul (1 thread)"
+    t0 = time.perf_counter()
+    xt = np.ascontiguousarray(np.transpose(xs, (1, 0, 2)))
+    h = np.transpose(gm(wu, xt), (1, 0, 2))
+    h = moe.gelu(h)
+    ht = np.ascontiguousarray(np.transpose(h, (1, 0, 2)))
+    y = np.transpose(gm(wd, ht), (1, 0, 2))
+    t_ffn = time.perf_counter() - t0
+    del y
+    per_row = t_ffn / sample_rows
+    t_layer = t_rdc + per_row * N * k
+    return dict(value=N / t_layer, unit="tokens/s", cores=1, kind=kind,
+                sample=(f"{config_label(c)}: expert FFN on {sample_rows} of {N * k} token-expert rows via {what}, "
+                        f"extrapolated linearly in FLOPs; NumPy routing/dispatch/combine over all {N} tokens "
+                        f"({t_rdc:.2f} s); measured {t_ffn:.1f} s"))
+
+
+def config_label(c):
+    return f"N={c['N']} d={c['d']} E={c['E']} k={c['k']} F={c['F']} {c['dtype']}"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU is design-only: "
+                                   "see DESIGN.md, 'How the path would shard')"}))
+        sys.exit(2)
+    import torch
+
+    from yggdrasil_amd import ops
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        sys.exit(1)
+    names = [s.strip() for s in args.configs.split(",") if s.strip()]
+    results = {}
+    for name in names:
+        c = CONFIGS[name]
+        print(f"[bench] {name} {config_label(c)}", file=sys.stderr, flush=True)
+        if name == "c2":
+            results[name] = run_c2(torch, ops, c, args.steps, args.warmup)
+        else:
+            results[name] = run_layer_config(torch, ops, name, c, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    head_name = "c3" if "c3" in results else names[0]
+    head = results[head_name]
+    cpu = None
+    if not args.no_cpu_baseline and head_name != "c2":
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(CONFIGS[head_name], args.cpu_sample_rows)
+    roof = None
+    if "_flops_per_launch" in head:
+        ach = head["_flops_per_launch"] / (head["_ms_per_launch"] * 1e-3)
+        peak = PEAK_F32 if CONFIGS[head_name]["dtype"] == "f32" else PEAK_BF16
+        roof = dict(bound="mfma", kernel="grouped_cl_mfma (expert up + down projections)",
+                    achieved=ach / 1e12, peak=peak / 1e12, unit="TFLOP/s", frac=ach / peak, traffic=None)
+    for r in results.values():
+        r.pop("_flops_per_launch", None)
+        r.pop("_ms_per_launch", None)
+    c = CONFIGS[head_name]
+    line = {
+        "metric": "MoE-HLM layer tokens/sec (prefill+decode) at 1 GPU; % of MFMA/HBM roofline",
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if c["dtype"] == "bf16" else "f32",
+        "data": "synthetic (seeded; random-init weights ~N(0, 1/sqrt(8 fan_in)))",
+        "config": {"workload": f"BASELINE config {head_name[1]}: MoE-HLM layer, " + config_label(c)
+                   + (", Zipf(1.2) expert load" if c["logits"] == "zipf" else ""),
+                   "tokens": c["N"], "d": c["d"], "experts": c["E"], "top_k": c["k"], "d_ff": c["F"],
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "configs": results,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,142 @@
+/*
+ * ygg_moe.h -- C ABI of the MI355X (gfx950) MoE-HLM expert layer.
+ *
+ * Library: yggdrasil_amd/lib/libygg_moe.so (hipcc, gfx950 code objects).
+ *
+ * Conventions (every entry point):
+ *  - plain C types only; every pointer is a DEVICE pointer owned by the caller
+ *    (the library allocates nothing and keeps no state between calls);
+ *  - the work is enqueued on `stream` (a hipStream_t; pass the caller's
+ *    current stream, e.g. torch.cuda.current_stream().cuda_stream);
+ *  - the return value is 0 on success and -1 on a rejected argument or a
+ *    failed launch; ygg_last_error() then describes it (per host thread).
+ *    Nothing aborts and nothing falls back silently.  (The reference's
+ *    launchers return void and its Python wrappers swallow every exception,
+ *    rune/ops/batched.py:329-343.)
+ *  - multivectors are 8 contiguous values in the reference's blade order
+ *    1, e1, e2, e3, e12, e13, e23, e123 (rune/types/multivector.py:7), except
+ *    where an argument says "mask order" (1, e1, e2, e12, e3, e13, e23, e123,
+ *    i.e. e3 and e12 exchanged), the layout the expert products consume.
+ *  - dtype codes: 0 = fp32, 1 = bf16 (activations); weight formats:
+ *    0 = fp32, 1 = bf16 (dual, sign-folded), 2 = int8 per-output-channel.
+ *    activation codes: 0 none, 1 gelu, 2 relu, 3 sigmoid
+ *    (holograph/models/hlm_block.py:28-32).
+ */
+#ifndef YGG_MOE_H
+#define YGG_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ygg_stream_t; /* == hipStream_t */
+
+/* Message for the last non-zero status returned on this host thread. */
+const char* ygg_last_error(void);
+/* ABI version of the library (1). */
+int ygg_version(void);
+
+/* ---- operator boundary ---------------------------------------------------
+ * out[m, n] = sum_k gp(a[m, k], b[k, n]); a: (M, K, 8), b: (K, N, 8),
+ * out: (M, N, 8), fp32, blade order, weight operand on the left.
+ * Replaces cl3_geom_matmul_launch (mjolnir/src/cuda/batch_ops.cu:389-401,
+ * bound at rune/bindings/mjolnir_cuda_ffi.py:127-128,505-525) and
+ * cl3_geom_matmul_flat (mjolnir/src/cpu/batch_ops.c:165-172, declared
+ * mjolnir/include/cl3_ops.h:210, bound at rune/bindings/mjolnir_ffi.py:208-209).
+ * Unlike those, it reports errors and takes the stream explicitly. */
+int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K, int N, ygg_stream_t stream);
+
+/* ---- router --------------------------------------------------------------
+ * Grade-energy logits of CliffordRouter (holograph/layers/clifford_router.py:
+ * 54-90): energy[t, g] = sum over d and the blades of grade g of x^2,
+ * logits[t, e] = sum_g energy[t, g] / (sum energy + 1e-12) * W_r[e, g] + b_r[e].
+ * x: (N, d, 8) of x_dtype; router_w (E, 4), router_b (E); logits (N, E);
+ * energy (N, 4) or NULL. */
+int ygg_router_energy_logits(const void* x, int x_dtype, int N, int d, const float* router_w,
+                             const float* router_b, int E, float* logits, float* energy, ygg_stream_t stream);
+
+/* Workspace bytes needed by ygg_route. */
+size_t ygg_route_workspace_bytes(int N, int E, int k);
+
+/* Softmax, top-k and the expert counting sort.
+ * Replaces clifford_router.py:18-21,93-104 and the slot grouping of
+ * hlm_block.py:165-177.  logits (N, E) fp32, E <= 64, k <= 8.
+ * Outputs: topk_idx (N, k) -- slot 0 most probable, equal probabilities
+ *   ordered by lower expert index (the reference's ascending argsort order
+ *   is reversed, clifford_router.py:97); topk_w (N, k) renormalised
+ *   (sum + 1e-12, summed from the least probable slot); counts (E);
+ *   offsets (E + 1, exclusive scan); perm (N*k): token of each expert-grouped
+ *   row, ascending token order within an expert; slot_pos (N*k): the row of
+ *   slot (t, s).  Deterministic; bit-exact integer outputs. */
+int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
+              int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
+              ygg_stream_t stream);
+
+/* ---- dispatch / combine ----------------------------------------------------
+ * x_sorted[slot_pos[t, s]] = x[t]  (rows of d multivectors, dtype 0/1);
+ * to_mask_order != 0 stores the rows in mask order.
+ * Replaces expert_input = flat_x[token_ids] (hlm_block.py:178). */
+int ygg_dispatch(const void* x, int dtype, int N, int k, int d, const int32_t* slot_pos, void* x_sorted,
+                 int to_mask_order, ygg_stream_t stream);
+
+/* out[t] = (residual[t] +) sum over the token's slots in ascending expert
+ * order of topk_w[t, s] * y_sorted[slot_pos[t, s]], each product rounded
+ * before its add.  y_mask_order != 0: y rows are in mask order (out is
+ * always blade order).  residual may be NULL.
+ * Replaces weighted = w * y; np.add.at(output, token_ids, weighted)
+ * (hlm_block.py:180-181) and the residual add x + ffn_out (hlm_block.py:151). */
+int ygg_combine(const void* y_sorted, int y_dtype, int y_mask_order, int N, int k, int d, const int32_t* topk_idx,
+                const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
+                ygg_stream_t stream);
+
+/* ---- grouped CliffordLinear expert products --------------------------------
+ * Bytes of the prepared weights for E experts of a CliffordLinear d_in -> d_out. */
+size_t ygg_prepared_weight_bytes(int E, int d_out, int d_in, int format);
+
+/* Prepare expert weights W (E, d_out, d_in, 8) fp32 blade order -- the
+ * reference's CliffordLinear.weight layout (clifford_linear.py:95-96) stacked
+ * over experts -- into `format`.  int8: scales (E, d_out) fp32 are written,
+ * s = max(absmax over (d_in, 8), 1e-12) / 127, q = clip(rint(w / s), -127, 127)
+ * (conventions of bifrost/quantization/grade_quantize.py:85-117,198-203). */
+int ygg_prepare_weights(const float* W, int E, int d_out, int d_in, int format, void* out, float* scales,
+                        ygg_stream_t stream);
+
+/* Bias (E, d_out, 8) blade order -> mask order fp32 (clifford_linear.py:99). */
+int ygg_prepare_bias(const float* b, int E, int d_out, float* out, ygg_stream_t stream);
+
+/* For every expert e, rows [offsets[e], offsets[e+1]) of x (P_max >= offsets[E]
+ * rows of d_in multivectors, mask order; fp32 for format 0, bf16 otherwise):
+ *   y[m, j] = act( sum_i W_e[j, i] * x[m, i] + b_e[j] )
+ * act is the grade-wise activation (holograph/layers/activations.py:15-128).
+ * y: rows of d_out multivectors, fp32 (format 0) or y_dtype, blade order if
+ * y_blade_order else mask order.  bias: prepared (mask order) or NULL.
+ * Replaces CliffordLinear.forward (clifford_linear.py:101-123) of every
+ * expert inside CliffordFFN.forward (hlm_block.py:55-61). */
+int ygg_grouped_clifford_linear(const void* x, int P_max, const void* w_prepared, int format, const float* scales,
+                                const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out,
+                                int act, void* y, int y_dtype, int y_blade_order, ygg_stream_t stream);
+
+/* ---- the whole layer ---------------------------------------------------------
+ * Workspace bytes of ygg_moe_forward. */
+size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype);
+
+/* HLMBlock._moe_forward (hlm_block.py:154-183): x (N, d, 8) of dtype ->
+ * out (N, d, 8) of dtype (+ residual if not NULL).  logits (N, E) or NULL
+ * (then router_w/router_b give the grade-energy logits).  Expert weights
+ * prepared with ygg_prepare_weights (format 0 for fp32, 1 or 2 for bf16),
+ * biases prepared with ygg_prepare_bias or NULL.  topk_idx/topk_w/counts/
+ * offsets as in ygg_route. */
+int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act, const float* logits,
+                    const float* router_w, const float* router_b, const void* w_up, const float* s_up,
+                    const float* b_up, const void* w_down, const float* s_down, const float* b_down, int w_format,
+                    const void* residual, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                    int32_t* offsets, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YGG_MOE_H */

@@ -1,0 +1,119 @@
+"""CPU checks of the C-ABI library and of the host-side logic (no GPU calls).
+
+* the library loads and exports exactly what ``include/ygg_moe.h`` declares,
+  and the ctypes table in ``yggdrasil_amd/_native.py`` matches the header;
+* pure host-side functions (sizes, argument validation) behave;
+* the product path has no CPU fallback: CPU tensors are refused.
+"""
+
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "ygg_moe.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ygg_\w+)\s*\(", text)))
+
+
+def test_header_matches_ctypes_table():
+    from yggdrasil_amd import _native
+
+    assert header_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _native.lib()  # loads without touching a GPU
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (ygg_\w+)", out))
+    assert exported == set(header_functions()), exported ^ set(header_functions())
+
+
+def test_host_side_sizes():
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    assert L.ygg_version() == 1
+    # route workspace: slot ranks + two per-block histograms, 256-byte aligned
+    nb = (16384 + 255) // 256
+    assert L.ygg_route_workspace_bytes(16384, 16, 2) == ((16384 * 2 * 4 + 2 * nb * 16 * 4) + 255) // 256 * 256
+    # prepared weights: bf16 dual layout pads d_out to 32 and d_in to 2
+    assert L.ygg_prepared_weight_bytes(32, 512, 128, 1) == 32 * 16 * 64 * 64 * 32
+    assert L.ygg_prepared_weight_bytes(2, 5, 7, 1) == 2 * 1 * 4 * 64 * 32
+    assert L.ygg_prepared_weight_bytes(2, 5, 7, 2) == 2 * 1 * 4 * 64 * 8
+    assert L.ygg_prepared_weight_bytes(2, 5, 7, 0) == 2 * 5 * 7 * 32
+    assert L.ygg_prepared_weight_bytes(2, 5, 7, 9) == 0
+
+
+def test_argument_errors_are_reported_not_aborted():
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    # rejected before any launch: E > 64
+    assert L.ygg_route(None, 10, 65, 2, None, None, None, None, None, None, None, 0, None) == -1
+    assert b"E=65" in L.ygg_last_error()
+    assert L.ygg_dispatch(None, 7, 1, 1, 1, None, None, 0, None) == -1
+    assert b"dtype" in L.ygg_last_error()
+    assert L.ygg_prepare_weights(None, 1, 1, 1, 5, None, None, None) == -1
+    assert L.ygg_grouped_clifford_linear(None, 1, None, 2, None, None, None, 1, 1, 1, 1, None, 1, 0, None) == -1
+    assert b"scales" in L.ygg_last_error()
+
+
+def test_config_validation():
+    from yggdrasil_amd import MoEHLMConfig
+
+    c = MoEHLMConfig(d_model=8, d_ff=16)
+    assert c.weight_format == "f32"
+    assert MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.bfloat16).weight_format == "bf16"
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, activation="swish")
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.float32, weight_format="int8")
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, n_experts=65)
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, n_experts=4, top_k=5)
+
+
+def test_no_cpu_fallback():
+    from yggdrasil_amd import ops
+
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.route(torch.zeros(4, 8), 2)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.geom_matmul(torch.zeros(2, 3, 8), torch.zeros(3, 4, 8))
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from yggdrasil_amd import _native
+
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(_native, "_lib", None)
+    with pytest.raises(_native.NativeLibraryError, match="no CPU fallback"):
+        _native.lib()
+
+
+def test_product_never_imports_oracle():
+    pkg = os.path.join(ROOT, "yggdrasil_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                src = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", src, flags=re.M), f

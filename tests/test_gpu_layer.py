@@ -1,0 +1,189 @@
+"""GPU parity: expert products and the whole MoE-HLM layer against the reference.
+
+Reference goldens (``tests/golden``, written by the reference's own NumPy
+path) and the oracle.  Routing is compared bit-exactly; outputs normwise
+(fp32 <= 1e-5, bf16 / int8 weights <= 2e-2; see ``_gpu_helpers``).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import _inputs
+from _fixtures import LAYER_CASES, load_case
+from _gpu_helpers import TOL_BF16, TOL_F32, normwise_err, say
+from oracle import moe
+
+pytestmark = pytest.mark.gpu
+
+
+def _mods():
+    import yggdrasil_amd
+    from yggdrasil_amd import ops
+
+    return yggdrasil_amd, ops
+
+
+@pytest.mark.parametrize("name", ["gm_small", "gm_rect"])
+def test_geom_matmul_operator(name):
+    _, ops = _mods()
+    _, inp, ref = load_case(name)
+    say(f"geom_matmul {name}")
+    out = ops.geom_matmul(torch.from_numpy(inp["a"]).cuda(), torch.from_numpy(inp["b"]).cuda()).cpu().numpy()
+    assert normwise_err(out, ref["out"]) < TOL_F32
+
+
+@pytest.mark.parametrize("fmt,act,d_in,d_out,E,P", [
+    ("f32", "none", 8, 16, 3, 50), ("f32", "gelu", 64, 256, 8, 512), ("f32", "relu", 7, 5, 2, 33),
+    ("bf16", "none", 16, 64, 4, 200), ("bf16", "gelu", 128, 512, 3, 300), ("bf16", "sigmoid", 9, 40, 5, 77),
+    ("int8", "gelu", 32, 64, 4, 100), ("int8", "none", 128, 96, 2, 70)])
+def test_grouped_clifford_linear(fmt, act, d_in, d_out, E, P):
+    _, ops = _mods()
+    g = np.random.default_rng(d_in * 7 + d_out + E)
+    W = (g.standard_normal((E, d_out, d_in, 8), dtype=np.float32) / np.sqrt(8 * d_in)).astype(np.float32)
+    b = (0.3 * g.standard_normal((E, d_out, 8))).astype(np.float32)
+    x = g.standard_normal((P, d_in, 8), dtype=np.float32)
+    counts = np.bincount(g.integers(0, E, P), minlength=E)
+    counts[0] = 0 if E > 2 else counts[0]  # an empty expert
+    counts[-1] += P - counts.sum()
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    Wref = W
+    if fmt in ("bf16", "int8"):
+        x = _inputs.bf16_round(x)
+    if fmt == "bf16":
+        Wref = _inputs.bf16_round(W)
+    if fmt == "int8":
+        q, s = moe.quantize_int8(W)
+        Wref = moe.dequantize_int8(q, s)
+    dt = torch.float32 if fmt == "f32" else torch.bfloat16
+    say(f"grouped_clifford_linear fmt={fmt} act={act} d_in={d_in} d_out={d_out} E={E} P={P}")
+    pw = ops.prepare_weights(torch.from_numpy(W).cuda(), fmt)
+    pb = ops.prepare_bias(torch.from_numpy(b).cuda())
+    xs = ops.to_mask_order(torch.from_numpy(x).cuda().to(dt))
+    y = ops.grouped_clifford_linear(xs, pw, torch.from_numpy(offsets).cuda(), pb, act, out_dtype=torch.float32)
+    y = y.cpu().numpy()
+    if fmt == "int8":
+        assert np.array_equal(pw.scales.cpu().numpy(), s)
+    for e in range(E):
+        rows = slice(offsets[e], offsets[e + 1])
+        if offsets[e] == offsets[e + 1]:
+            continue
+        ref = moe.ACTIVATIONS[act](moe.clifford_linear(x[rows], Wref[e], b[e]))
+        tol = TOL_F32 if fmt == "f32" else 5e-3
+        assert normwise_err(y[rows], ref) < tol, e
+
+
+def _run_layer_case(name):
+    yggdrasil_amd, ops = _mods()
+    p, inp, ref = load_case(name)
+    bf16 = bool(p.get("bf16"))
+    dt = torch.bfloat16 if bf16 else torch.float32
+    fmt = "int8" if p.get("int8") else ("bf16" if bf16 else "f32")
+    router = {None: "energy", "clifford_head": "clifford_head"}.get(p.get("logits"), "logits")
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=p["d"], d_ff=p["F"], n_experts=p["E"], top_k=p["k"],
+                                     activation=p["act"], dtype=dt, weight_format=fmt, router=router)
+    x = torch.from_numpy(inp["x"]).cuda().to(dt)
+    for li in range(p.get("layers", 1)):
+        pre = f"l{li}_" if p["kind"] == "stack" else ""
+        layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+        layer.load_reference_weights(router_weight=inp[pre + "router_w"], router_bias=inp[pre + "router_b"],
+                                     w_up=inp[pre + "w_up"], b_up=inp[pre + "b_up"], w_down=inp[pre + "w_down"],
+                                     b_down=inp[pre + "b_down"], head_weight=inp.get(pre + "head_w"))
+        logits = torch.from_numpy(inp[pre + "logits"]).cuda() if router == "logits" else None
+        say(f"layer {name} {pre} N={x.shape[0] * x.shape[1]} d={p['d']} E={p['E']} k={p['k']} F={p['F']} {fmt}")
+        y = layer.moe_forward(x, logits=logits, residual=x if p["kind"] == "stack" else None)
+        torch.cuda.synchronize()
+        rt = layer.last_routing
+        assert np.array_equal(rt["topk_idx"].cpu().numpy(), ref[pre + "idx"][:, ::-1]), "routing indices"
+        assert np.array_equal(rt["counts"].cpu().numpy(), ref[pre + "counts"]), "expert counts"
+        assert np.allclose(rt["topk_w"].cpu().numpy(), ref[pre + "w"][:, ::-1], rtol=1e-5, atol=1e-6)
+        x = y
+    got = x.float().cpu().numpy()
+    err = normwise_err(got, ref["out"])
+    tol = TOL_BF16 if bf16 else TOL_F32
+    assert err < tol, f"{name}: normwise error {err:.3e} >= {tol}"
+    return err
+
+
+@pytest.mark.parametrize("name", LAYER_CASES)
+def test_layer_against_reference_golden(name):
+    _run_layer_case(name)
+
+
+def test_geoformer_interface_flat_input():
+    yggdrasil_amd, _ = _mods()
+    p, inp, ref = load_case("c1_layer")
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=p["d"], d_ff=p["F"], n_experts=p["E"], top_k=p["k"])
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(router_weight=inp["router_w"], router_bias=inp["router_b"], w_up=inp["w_up"],
+                                 b_up=inp["b_up"], w_down=inp["w_down"], b_down=inp["b_down"])
+    B, T = p["B"], p["T"]
+    xf = torch.from_numpy(inp["x"]).cuda().reshape(B, T, 8 * p["d"])
+    say("geoformer flat interface c1")
+    out, aux = layer(xf)
+    assert out.shape == xf.shape and aux.dim() == 0
+    assert normwise_err(out.cpu().numpy().reshape(ref["out"].shape), ref["out"]) < TOL_F32
+    c = ref["counts"].astype(np.float64)
+    f = c / c.sum()
+    assert abs(aux.item() - ((f - 1 / p["E"]) ** 2).sum()) < 1e-6
+
+
+def _sampled_layer_check(N, d, F, E, k, fmt, logits, seed, n_sample=12):
+    """Full-size layer on the GPU; the oracle recomputes a sample of tokens."""
+    yggdrasil_amd, _ = _mods()
+    g = np.random.default_rng(seed)
+    x = _inputs.bf16_round(g.standard_normal((N, d, 8), dtype=np.float32))
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F)
+    wu, wd = _inputs.bf16_round(wu), _inputs.bf16_round(wd)
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, dtype=torch.bfloat16,
+                                     weight_format=fmt, router="logits")
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    xt = torch.from_numpy(x).cuda().bfloat16().reshape(1, N, d, 8)
+    lt = torch.from_numpy(logits).cuda()
+    say(f"full layer N={N} d={d} F={F} E={E} k={k} {fmt}")
+    y = layer.moe_forward(xt, logits=lt).float().cpu().numpy().reshape(N, d, 8)
+    rt = layer.last_routing
+    idx = rt["topk_idx"].cpu().numpy()
+    w = rt["topk_w"].cpu().numpy()
+    idx_o, w_o = moe.route_topk(moe.softmax(logits), k)
+    assert np.array_equal(idx, idx_o)
+    if fmt == "int8":
+        wu = moe.dequantize_int8(*moe.quantize_int8(wu))
+        wd = moe.dequantize_int8(*moe.quantize_int8(wd))
+    sample = g.choice(N, size=n_sample, replace=False)
+    errs = []
+    for t in sample:
+        ref = np.zeros((d, 8), np.float32)
+        for s in np.argsort(idx[t]):
+            e = idx[t, s]
+            ye = moe.clifford_ffn(x[t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+            ref = ref + w_o[t, s] * ye
+        errs.append(normwise_err(y[t], ref))
+    assert max(errs) < TOL_BF16, max(errs)
+    # token permutation equivariance: every row is computed independently of its tile position
+    pi = g.permutation(N)
+    say(f"full layer permuted N={N}")
+    y2 = layer.moe_forward(xt[:, pi], logits=lt[pi]).float().cpu().numpy().reshape(N, d, 8)
+    assert np.array_equal(y2, y[pi])
+    return max(errs)
+
+
+def test_full_c3_prefill_bf16_sampled():
+    g = np.random.default_rng(303)
+    logits = _inputs.zipf_logits(g, 8192, 32, 4)
+    _sampled_layer_check(8192, 128, 512, 32, 4, "bf16", logits, 33)
+
+
+def test_full_c4_decode_int8_sampled():
+    g = np.random.default_rng(404)
+    logits = g.standard_normal((64, 32), dtype=np.float32)
+    _sampled_layer_check(64, 128, 512, 32, 2, "int8", logits, 44, n_sample=16)
+
+
+def test_module_rejects_cpu_tensors():
+    yggdrasil_amd, _ = _mods()
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=8, d_ff=16, n_experts=4, top_k=2)
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    with pytest.raises(ValueError):
+        layer.moe_forward(torch.zeros(1, 4, 8, 8))

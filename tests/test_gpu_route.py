@@ -1,0 +1,139 @@
+"""GPU parity: routing (softmax / top-k / counting sort), dispatch and combine.
+
+Integer outputs (indices, counts, offsets, permutation, slot rows) must be
+bit-exact against the reference goldens and the oracle; the combine must be
+bit-exact given the same routing weights (same order, no fused multiply-add).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _fixtures import load_case
+from _gpu_helpers import normwise_err, say
+from oracle import moe
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from yggdrasil_amd import ops
+
+    return ops
+
+
+def _check_route(logits_np, k, E, tag):
+    ops = _ops()
+    say(f"route {tag} N={logits_np.shape[0]} E={E} k={k}")
+    r = ops.route(torch.from_numpy(logits_np).cuda(), k)
+    torch.cuda.synchronize()
+    probs = moe.softmax(logits_np)
+    idx_o, w_o = moe.route_topk(probs, k)
+    counts_o, offsets_o, perm_o, slot_o = moe.dispatch_plan(idx_o, E)
+    assert np.array_equal(r.topk_idx.cpu().numpy(), idx_o)
+    assert np.array_equal(r.counts.cpu().numpy(), counts_o)
+    assert np.array_equal(r.offsets.cpu().numpy(), offsets_o)
+    assert np.array_equal(r.perm.cpu().numpy(), perm_o)
+    assert np.array_equal(r.slot_pos.cpu().numpy(), slot_o)
+    w = r.topk_w.cpu().numpy()
+    assert np.allclose(w, w_o, rtol=2e-6, atol=1e-7)
+    return r
+
+
+def test_route_dispatch_combine_against_reference_golden():
+    ops = _ops()
+    p, inp, ref = load_case("c2_route")
+    r = _check_route(inp["logits"], p["k"], p["E"], "c2 golden")
+    # reference selection, reversed to the build's descending order
+    assert np.array_equal(r.topk_idx.cpu().numpy(), ref["idx"][:, ::-1])
+    assert np.array_equal(r.counts.cpu().numpy(), ref["counts"])
+    assert np.array_equal(r.perm.cpu().numpy(), ref["perm"])
+    assert np.allclose(r.topk_w.cpu().numpy(), ref["w"][:, ::-1], rtol=2e-6, atol=1e-7)
+    x = torch.from_numpy(inp["x"]).cuda()
+    say("dispatch c2 golden")
+    xs = ops.dispatch(x, r)
+    assert np.array_equal(xs.cpu().numpy(), inp["x"][ref["perm"]])
+    xm = ops.dispatch(x, r, mask_order=True)
+    assert np.array_equal(xm.cpu().numpy(), inp["x"][ref["perm"]][..., [0, 1, 2, 4, 3, 5, 6, 7]])
+    say("combine c2 golden (identity experts)")
+    out = ops.combine(xs, r).cpu().numpy()
+    assert normwise_err(out, ref["out"]) < 1e-6
+    # bit-exact against the oracle's combine given the GPU's own weights
+    o2 = moe.combine(inp["x"][ref["perm"]], r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy(),
+                     r.slot_pos.cpu().numpy())
+    assert np.array_equal(out, o2)
+    out_m = ops.combine(xm, r, y_mask_order=True).cpu().numpy()
+    assert np.array_equal(out_m, out)
+
+
+@pytest.mark.parametrize("N,E,k,seed", [(1, 4, 1, 0), (255, 8, 2, 1), (257, 16, 4, 2), (1000, 64, 8, 3),
+                                        (16384, 16, 2, 4), (8192, 32, 4, 5), (4096, 64, 2, 6)])
+def test_route_random_sizes(N, E, k, seed):
+    r = np.random.default_rng(seed)
+    _check_route(r.standard_normal((N, E), dtype=np.float32), k, E, f"random seed={seed}")
+
+
+@pytest.mark.parametrize("E,k", [(4, 2), (16, 2), (32, 4), (64, 8)])
+def test_route_ties_lowest_index_wins(E, k):
+    r = np.random.default_rng(E + k)
+    logits = r.integers(0, 3, size=(700, E)).astype(np.float32)  # exact ties everywhere
+    _check_route(logits, k, E, f"ties E={E} k={k}")
+
+
+def test_route_zipf_skew_and_empty_experts():
+    r = np.random.default_rng(9)
+    N, E, k = 3000, 32, 4
+    logits = np.full((N, E), -30.0, np.float32)
+    logits[:, :4] = r.standard_normal((N, 4), dtype=np.float32)  # only experts 0..3 ever chosen
+    rt = _check_route(logits, k, E, "empty experts")
+    c = rt.counts.cpu().numpy()
+    assert c[4:].sum() == 0 and c[:4].sum() == N * k
+
+
+def test_full_c2_route_dispatch_combine():
+    """BASELINE C2: N=16384, E=16, k=2, d=128 fp32; identity expert."""
+    ops = _ops()
+    g = np.random.default_rng(2024)
+    N, E, k, d = 16384, 16, 2, 128
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    x = g.standard_normal((N, d, 8), dtype=np.float32)
+    r = _check_route(logits, k, E, "C2 full")
+    xt = torch.from_numpy(x).cuda()
+    say("dispatch C2 full")
+    xs = ops.dispatch(xt, r)
+    perm = r.perm.cpu().numpy()
+    assert np.array_equal(xs.cpu().numpy(), x[perm])
+    say("combine C2 full")
+    out = ops.combine(xs, r).cpu().numpy()
+    o2 = moe.combine(x[perm], r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy(), r.slot_pos.cpu().numpy())
+    assert np.array_equal(out, o2)
+    # identity experts with renormalised weights return the token itself
+    assert normwise_err(out, x) < 1e-6
+
+
+def test_combine_residual_and_bf16():
+    ops = _ops()
+    g = np.random.default_rng(5)
+    N, E, k, d = 300, 8, 3, 16
+    r = ops.route(torch.from_numpy(g.standard_normal((N, E), dtype=np.float32)).cuda(), k)
+    y = torch.from_numpy(g.standard_normal((N * k, d, 8), dtype=np.float32)).cuda()
+    res = torch.from_numpy(g.standard_normal((N, d, 8), dtype=np.float32)).cuda()
+    say("combine residual fp32")
+    out = ops.combine(y, r, residual=res).cpu().numpy()
+    ref = moe.combine(y.cpu().numpy(), r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy(), r.slot_pos.cpu().numpy())
+    assert np.array_equal(out, (res.cpu().numpy() + ref).astype(np.float32))
+    say("combine bf16")
+    outb = ops.combine(y.bfloat16(), r).float().cpu().numpy()
+    refb = moe.combine(y.bfloat16().float().cpu().numpy(), r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy(),
+                       r.slot_pos.cpu().numpy())
+    assert normwise_err(outb, refb) < 8e-3
+
+
+def test_route_rejects_bad_arguments():
+    ops = _ops()
+    from yggdrasil_amd._native import NativeLibraryError
+
+    with pytest.raises(NativeLibraryError):
+        ops.route(torch.zeros((4, 65), device="cuda"), 2)  # E > 64
+    with pytest.raises(NativeLibraryError):
+        ops.route(torch.zeros((4, 8), device="cuda"), 9)  # k > 8

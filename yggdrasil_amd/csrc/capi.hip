@@ -1,0 +1,115 @@
+// capi.hip -- error reporting and the composed MoE-HLM layer entry point.
+//
+// ygg_moe_forward replaces HLMBlock._moe_forward (holograph/models/hlm_block.py:
+// 154-183) end to end: router logits (or given logits), softmax / top-k /
+// counting sort, dispatch, the two grouped CliffordLinear products with the
+// grade-wise activation fused, and the weighted combine -- all enqueued on
+// the caller's stream, all buffers caller-owned (one workspace, sized by
+// ygg_moe_workspace_bytes), no host synchronisation.
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "ygg_common.h"
+
+namespace ygg {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return -1;
+  }
+  return 0;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace ygg
+
+using namespace ygg;
+
+YGG_API const char* ygg_last_error(void) { return g_err; }
+
+YGG_API int ygg_version(void) { return 1; }
+
+// declared in the other translation units
+extern "C" size_t ygg_route_workspace_bytes(int N, int E, int k);
+extern "C" int ygg_route(const float*, int, int, int, int32_t*, float*, int32_t*, int32_t*, int32_t*, int32_t*, void*,
+                         size_t, hipStream_t);
+extern "C" int ygg_router_energy_logits(const void*, int, int, int, const float*, const float*, int, float*, float*,
+                                        hipStream_t);
+extern "C" int ygg_dispatch(const void*, int, int, int, int, const int32_t*, void*, int, hipStream_t);
+extern "C" int ygg_combine(const void*, int, int, int, int, int, const int32_t*, const float*, const int32_t*,
+                           const void*, void*, int, hipStream_t);
+extern "C" int ygg_grouped_clifford_linear(const void*, int, const void*, int, const float*, const float*,
+                                           const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
+
+YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype) {
+  const size_t P = (size_t)N * k;
+  const size_t es = (dtype == kF32) ? 4 : 2;
+  size_t b = 0;
+  b += align256((size_t)N * E * 4);       // logits
+  b += align256(P * 4) * 2;               // perm, slot_pos
+  b += align256(ygg_route_workspace_bytes(N, E, k));
+  b += align256(P * d * 8 * es);          // x_sorted
+  b += align256(P * F * 8 * es);          // h
+  b += align256(P * d * 8 * es);          // y_sorted
+  return b;
+}
+
+YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
+                            const float* logits, const float* router_w, const float* router_b, const void* w_up,
+                            const float* s_up, const float* b_up, const void* w_down, const float* s_down,
+                            const float* b_down, int w_format, const void* residual, void* out, int32_t* topk_idx,
+                            float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+  YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
+  YGG_CHECK_ARG(dtype == kF32 ? w_format == 0 : (w_format == 1 || w_format == 2),
+                "ygg_moe_forward: weight format %d does not match dtype %d", w_format, dtype);
+  YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype),
+                "ygg_moe_forward: workspace of %zu bytes, need %zu", workspace_bytes,
+                ygg_moe_workspace_bytes(N, d, F, E, k, dtype));
+  YGG_CHECK_ARG(logits || (router_w && router_b), "ygg_moe_forward: need logits or router parameters");
+  if (N == 0) return 0;
+  const size_t P = (size_t)N * k;
+  const size_t es = (dtype == kF32) ? 4 : 2;
+  char* p = static_cast<char*>(workspace);
+  float* lg = reinterpret_cast<float*>(p);
+  p += align256((size_t)N * E * 4);
+  int32_t* perm = reinterpret_cast<int32_t*>(p);
+  p += align256(P * 4);
+  int32_t* slot_pos = reinterpret_cast<int32_t*>(p);
+  p += align256(P * 4);
+  void* rws = p;
+  const size_t rws_bytes = align256(ygg_route_workspace_bytes(N, E, k));
+  p += rws_bytes;
+  void* xs = p;
+  p += align256(P * d * 8 * es);
+  void* h = p;
+  p += align256(P * F * 8 * es);
+  void* ys = p;
+
+  if (!logits) {
+    if (ygg_router_energy_logits(x, dtype, N, d, router_w, router_b, E, lg, nullptr, stream)) return -1;
+    logits = lg;
+  }
+  if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
+  if (ygg_dispatch(x, dtype, N, k, d, slot_pos, xs, /*to_mask_order=*/1, stream)) return -1;
+  if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
+                                  /*blade=*/0, stream))
+    return -1;
+  if (ygg_grouped_clifford_linear(h, (int)P, w_down, w_format, s_down, b_down, offsets, E, F, d, kActNone, ys, dtype,
+                                  /*blade=*/1, stream))
+    return -1;
+  return ygg_combine(ys, dtype, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
+}

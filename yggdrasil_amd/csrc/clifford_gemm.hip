@@ -1,0 +1,531 @@
+// clifford_gemm.hip -- grouped CliffordLinear expert products on gfx950.
+//
+// Replaces, for every expert e of the MoE-HLM layer, CliffordLinear.forward
+// (holograph/layers/clifford_linear.py:101-123) on that expert's rows,
+//     y[m, j] = sum_i  W[j, i] * x[m, i]  (+ b[j])      (* = geometric product)
+// which the reference computes with rune.ops.batched.geom_matmul
+// (rune/ops/batched.py:320-344), followed by the grade-wise activation
+// (holograph/layers/activations.py:15-128) for the up projection.
+//
+// As a dense contraction:  Y[m, (j,r)] = sum_{(i,q)} X[m, (i,q)] L(W[j,i])[r, q],
+// K = 8 d_in, N = 8 d_out, 128 d_in d_out FLOPs per row -- L(w) has no zeros.
+//
+// MFMA mapping (bf16 / int8 weights, v_mfma_f32_32x32x16_bf16)
+// ------------------------------------------------------------
+// * K is walked two input multivectors at a time: lane l of a wave holds
+//   the 8 components (mask order) of multivector i0 + l/32 of row l%32 --
+//   exactly one A fragment.  No activation expansion is needed.
+// * One accumulator per output blade r: the B fragment for blade r holds,
+//   in lane (j = l%32, i = i0 + l/32), row r of L(W[j,i]):  in mask order
+//   L[r, q] = s(q^r, q) W[q^r], i.e. W permuted by XOR with r plus signs.
+//   The prepared weights store each multivector twice (plain and with every
+//   aligned pair swapped) with signs folded in (ygg_common.h), so B for
+//   blade r is a static choice of 32-bit registers plus one XOR.
+// * All 8 components of output multivector (m, j) land in the same lane, so
+//   bias, grade-wise activation, int8 scale and the output layout are fused
+//   into the epilogue with no shuffles.
+//
+// Row tiles never straddle experts: tile t of the launch maps to (expert,
+// first row) by walking the device-side offsets, so the grid is sized from
+// host-known bounds (ceil(P/BM) + E tiles) with no host synchronisation.
+
+#include "ygg_common.h"
+
+namespace ygg {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2 };
+
+// ---------------------------------------------------------------------------
+// activations (mask order: grade = popcount of the component index)
+// ---------------------------------------------------------------------------
+__device__ inline float gelu_f(float v) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  return 0.5f * v * (1.0f + tanhf(k0 * (v + 0.044715f * v * v * v)));
+}
+__device__ inline float sigmoid_f(float v) {
+  return v >= 0.f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+}
+
+template <int ACT>
+__device__ inline void activate_mask_order(float* y) {
+  if constexpr (ACT == kActNone) {
+    return;
+  } else {
+    // grade 0 (scalar): component 0
+    if constexpr (ACT == kActGelu) y[0] = gelu_f(y[0]);
+    if constexpr (ACT == kActRelu) y[0] = fmaxf(y[0], 0.f);
+    if constexpr (ACT == kActSigmoid) y[0] = sigmoid_f(y[0]);
+    // grades 1 {1,2,4} and 2 {3,5,6}: direction times activated magnitude
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int c0 = g == 0 ? 1 : 3, c1 = g == 0 ? 2 : 5, c2 = g == 0 ? 4 : 6;
+      const float mag = sqrtf(y[c0] * y[c0] + y[c1] * y[c1] + y[c2] * y[c2] + 1e-12f);
+      float gm;
+      if constexpr (ACT == kActGelu) gm = gelu_f(mag);
+      if constexpr (ACT == kActRelu) gm = fmaxf(mag, 0.f);
+      if constexpr (ACT == kActSigmoid) gm = sigmoid_f(mag);
+      const float f = gm / mag;
+      y[c0] *= f;
+      y[c1] *= f;
+      y[c2] *= f;
+    }
+    // grade 3: tanh for gelu and sigmoid; relu keeps sign(t) * max(|t|, 0) = t
+    if constexpr (ACT != kActRelu) y[7] = tanhf(y[7]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// row-tile -> expert mapping
+// ---------------------------------------------------------------------------
+__device__ inline bool find_tile(const int32_t* __restrict__ offsets, int E, int BM, int tile, int& e, int& row0,
+                                 int& row_end) {
+  int acc = 0;
+  int beg = offsets[0];
+  for (int x = 0; x < E; ++x) {
+    const int end = offsets[x + 1];
+    const int nt = (end - beg + BM - 1) / BM;
+    if (tile < acc + nt) {
+      e = x;
+      row0 = beg + (tile - acc) * BM;
+      row_end = end;
+      return true;
+    }
+    acc += nt;
+    beg = end;
+  }
+  return false;
+}
+
+// ---------------------------------------------------------------------------
+// weight preparation
+// ---------------------------------------------------------------------------
+// Quantisation scale per (expert, output channel): max(absmax, 1e-12) / 127,
+// computed in float64 and rounded to fp32.
+__global__ __launch_bounds__(256) void quant_scale_kernel(const float* __restrict__ W, int d_in,
+                                                          float* __restrict__ scales) {
+  __shared__ float red[256];
+  const size_t base = (size_t)blockIdx.x * d_in * 8;
+  float m = 0.f;
+  for (int i = threadIdx.x; i < d_in * 8; i += 256) m = fmaxf(m, fabsf(W[base + i]));
+  red[threadIdx.x] = m;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) scales[blockIdx.x] = (float)(fmax((double)red[0], 1e-12) / 127.0);
+}
+
+__device__ inline int quantize_one(float w, float s) {
+  double q = rint((double)w / (double)s);
+  q = fmin(fmax(q, -127.0), 127.0);
+  return (int)q;
+}
+
+// One thread per prepared multivector slot (padding included).
+__global__ __launch_bounds__(256) void prep_weights_kernel(const float* __restrict__ W, int E, int d_out, int d_in,
+                                                           int fmt, const float* __restrict__ scales,
+                                                           void* __restrict__ out) {
+  const int JB = (d_out + 31) / 32, IP = (d_in + 1) / 2;
+  const size_t total = (fmt == kWF32) ? (size_t)E * d_out * d_in : (size_t)E * JB * IP * 64;
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= total) return;
+  int e, j, i;
+  if (fmt == kWF32) {
+    i = (int)(n % d_in);
+    j = (int)((n / d_in) % d_out);
+    e = (int)(n / ((size_t)d_in * d_out));
+  } else {
+    const int ih = (int)(n & 1), jj = (int)((n >> 1) & 31);
+    size_t rest = n >> 6;
+    const int ip = (int)(rest % IP);
+    rest /= IP;
+    const int jb = (int)(rest % JB);
+    e = (int)(rest / JB);
+    j = jb * 32 + jj;
+    i = ip * 2 + ih;
+  }
+  float v[8];  // mask order, folded
+  const bool valid = (j < d_out) && (i < d_in);
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+    v[p] = valid ? (float)kWFold(p) * W[(((size_t)e * d_out + j) * d_in + i) * 8 + mask_to_blade(p)] : 0.f;
+  if (fmt == kWF32) {
+    float* o = static_cast<float*>(out) + n * 8;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) o[p] = v[p];
+  } else if (fmt == kWBF16) {
+    uint16_t* o = static_cast<uint16_t*>(out) + n * 16;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      o[p] = f32_to_bf16_bits(v[p]);
+      o[8 + p] = f32_to_bf16_bits(v[p ^ 1]);
+    }
+  } else {
+    int8_t* o = static_cast<int8_t*>(out) + n * 8;
+    const float s = valid ? scales[(size_t)e * d_out + j] : 1.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) o[p] = (int8_t)(valid ? quantize_one(v[p], s) : 0);
+  }
+}
+
+__global__ __launch_bounds__(256) void prep_bias_kernel(const float* __restrict__ b, size_t n_mv,
+                                                        float* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= n_mv) return;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) out[n * 8 + p] = b[n * 8 + mask_to_blade(p)];
+}
+
+// ---------------------------------------------------------------------------
+// bf16 / int8-weight MFMA kernel
+// ---------------------------------------------------------------------------
+template <int R>
+__device__ inline bf16x8_t blade_operand(const uint32_t (&raw)[4], const uint32_t (&sw)[4]) {
+  constexpr int tneg = neg_pair(R) ^ (R >> 1);  // negative pair in k (input component) order
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    d[t] = (R & 1) ? sw[t ^ (R >> 1)] : raw[t ^ (R >> 1)];
+    if (t == tneg) d[t] ^= 0x80008000u;
+  }
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+__device__ inline uint32_t i8pair_to_bf16x2(int lo, int hi) {
+  // |q| <= 127 has at most 7 significant bits: the top 16 bits of the fp32
+  // value are the exact bf16 value.
+  const uint32_t a = __builtin_bit_cast(uint32_t, (float)lo);
+  const uint32_t b = __builtin_bit_cast(uint32_t, (float)hi);
+  return (a >> 16) | (b & 0xffff0000u);
+}
+
+template <int OUT_DT>
+__device__ inline void store_out8(void* Y, size_t mv, const float* y, bool blade_order) {
+  float o[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = y[c];
+  if (blade_order) {
+    o[3] = y[4];
+    o[4] = y[3];
+  }
+  if constexpr (OUT_DT == kF32) {
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(Y) + mv * 8);
+    p[0] = make_float4(o[0], o[1], o[2], o[3]);
+    p[1] = make_float4(o[4], o[5], o[6], o[7]);
+  } else {
+    uint4 q;
+    q.x = pack_bf16x2(o[0], o[1]);
+    q.y = pack_bf16x2(o[2], o[3]);
+    q.z = pack_bf16x2(o[4], o[5]);
+    q.w = pack_bf16x2(o[6], o[7]);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(Y) + mv * 8) = q;
+  }
+}
+
+constexpr int kMfmaBM = 64;  // rows per workgroup (2 waves x 32)
+constexpr int kMfmaBN = 64;  // output multivectors per workgroup (2 waves x 32)
+
+template <int ACT, bool OUT_BLADE, bool WI8, int OUT_DT>
+__global__ __launch_bounds__(256, 2) void grouped_cl_mfma(const uint16_t* __restrict__ A, const void* __restrict__ Wp,
+                                                          const float* __restrict__ wscale,
+                                                          const float* __restrict__ bias,
+                                                          const int32_t* __restrict__ offsets, int E, int d_in,
+                                                          int d_out, void* __restrict__ Y) {
+  int e, row0, row_end;
+  if (!find_tile(offsets, E, kMfmaBM, blockIdx.x, e, row0, row_end)) return;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int JB = (d_out + 31) >> 5, IP = (d_in + 1) >> 1;
+  const int jb = blockIdx.y * 2 + wn;
+  if (jb >= JB) return;
+  const int ih = lane >> 5, l32 = lane & 31;
+  const int arow = row0 + wm * 32 + l32;
+  const bool arow_ok = arow < row_end;
+  const uint16_t* aptr = A + ((size_t)(arow_ok ? arow : row0) * d_in + ih) * 8;
+  const size_t wslot0 = (((size_t)e * JB + jb) * IP) * 64 + l32 * 2 + ih;
+
+  f32x16_t acc[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[r][v] = 0.f;
+
+  for (int ip = 0; ip < IP; ++ip) {
+    const int i = 2 * ip + ih;
+    uint4 a = make_uint4(0, 0, 0, 0);
+    if (arow_ok && i < d_in) a = *reinterpret_cast<const uint4*>(aptr + (size_t)ip * 16);
+    uint32_t raw[4], sw[4];
+    if constexpr (!WI8) {
+      const uint4* wp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(Wp) + (wslot0 + (size_t)ip * 64) * 16);
+      const uint4 w0 = wp[0], w1 = wp[1];
+      raw[0] = w0.x; raw[1] = w0.y; raw[2] = w0.z; raw[3] = w0.w;
+      sw[0] = w1.x; sw[1] = w1.y; sw[2] = w1.z; sw[3] = w1.w;
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(Wp) + (wslot0 + (size_t)ip * 64) * 8);
+      int c[8];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        c[p] = (int)(int8_t)((q.x >> (8 * p)) & 0xff);
+        c[4 + p] = (int)(int8_t)((q.y >> (8 * p)) & 0xff);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        raw[t] = i8pair_to_bf16x2(c[2 * t], c[2 * t + 1]);
+        sw[t] = (raw[t] >> 16) | (raw[t] << 16);
+      }
+    }
+    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<0>(raw, sw), acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<1>(raw, sw), acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<2>(raw, sw), acc[2], 0, 0, 0);
+    acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<3>(raw, sw), acc[3], 0, 0, 0);
+    acc[4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<4>(raw, sw), acc[4], 0, 0, 0);
+    acc[5] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<5>(raw, sw), acc[5], 0, 0, 0);
+    acc[6] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<6>(raw, sw), acc[6], 0, 0, 0);
+    acc[7] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, blade_operand<7>(raw, sw), acc[7], 0, 0, 0);
+  }
+
+  const int j = jb * 32 + l32;
+  if (j >= d_out) return;
+  const float sc = WI8 ? wscale[(size_t)e * d_out + j] : 1.f;
+  float bv[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) bv[r] = bias ? bias[((size_t)e * d_out + j) * 8 + r] : 0.f;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int row = row0 + wm * 32 + 8 * (v >> 2) + 4 * ih + (v & 3);
+    if (row >= row_end) continue;
+    float y[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = (float)kOutFold(r) * acc[r][v] * sc + bv[r];
+    activate_mask_order<ACT>(y);
+    store_out8<OUT_DT>(Y, (size_t)row * d_out + j, y, OUT_BLADE);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 kernel (VALU fused multiply-adds; LDS-staged tiles)
+// ---------------------------------------------------------------------------
+constexpr int kF32BM = 32, kF32BN = 32, kF32KI = 8;
+
+template <int ACT, bool OUT_BLADE>
+__global__ __launch_bounds__(256) void grouped_cl_f32(const float* __restrict__ A, const float* __restrict__ Wm,
+                                                      const float* __restrict__ bias,
+                                                      const int32_t* __restrict__ offsets, int E, int d_in,
+                                                      int d_out, float* __restrict__ Y) {
+  __shared__ float As[kF32BM][kF32KI * 8 + 4];
+  __shared__ float Ws[kF32BN][kF32KI * 8 + 4];
+  int e, row0, row_end;
+  if (!find_tile(offsets, E, kF32BM, blockIdx.x, e, row0, row_end)) return;
+  const int col0 = blockIdx.y * kF32BN;
+  const int tid = threadIdx.x;
+  const int tj = tid & 31, tm = tid >> 5;  // rows tm*4 .. tm*4+3
+  float acc[4][8];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[a][r] = 0.f;
+
+  const int lr = tid >> 3, lm = tid & 7;  // loader: row/col lr, multivector lm of the K slice
+  for (int i0 = 0; i0 < d_in; i0 += kF32KI) {
+    {
+      const int row = row0 + lr, i = i0 + lm;
+      float4 p0 = make_float4(0, 0, 0, 0), p1 = p0;
+      if (row < row_end && i < d_in) {
+        const float4* s = reinterpret_cast<const float4*>(A + ((size_t)row * d_in + i) * 8);
+        p0 = s[0];
+        p1 = s[1];
+      }
+      float* d = &As[lr][lm * 8];
+      d[0] = p0.x; d[1] = p0.y; d[2] = p0.z; d[3] = p0.w; d[4] = p1.x; d[5] = p1.y; d[6] = p1.z; d[7] = p1.w;
+      const int j = col0 + lr;
+      float4 q0 = make_float4(0, 0, 0, 0), q1 = q0;
+      if (j < d_out && i < d_in) {
+        const float4* s = reinterpret_cast<const float4*>(Wm + (((size_t)e * d_out + j) * d_in + i) * 8);
+        q0 = s[0];
+        q1 = s[1];
+      }
+      float* w = &Ws[lr][lm * 8];
+      w[0] = q0.x; w[1] = q0.y; w[2] = q0.z; w[3] = q0.w; w[4] = q1.x; w[5] = q1.y; w[6] = q1.z; w[7] = q1.w;
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int mv = 0; mv < kF32KI; ++mv) {
+      float w[8];
+#pragma unroll
+      for (int p = 0; p < 8; ++p) w[p] = Ws[tj][mv * 8 + p];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        float x[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = As[tm * 4 + a][mv * 8 + q];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float s = (float)folded_sign(r, q ^ r);
+            acc[a][r] = fmaf(s * w[q ^ r], x[q], acc[a][r]);
+          }
+      }
+    }
+    __syncthreads();
+  }
+  const int j = col0 + tj;
+  if (j >= d_out) return;
+  float bv[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) bv[r] = bias ? bias[((size_t)e * d_out + j) * 8 + r] : 0.f;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int row = row0 + tm * 4 + a;
+    if (row >= row_end) continue;
+    float y[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) y[r] = (float)kOutFold(r) * acc[a][r] + bv[r];
+    activate_mask_order<ACT>(y);
+    store_out8<kF32>(Y, (size_t)row * d_out + j, y, OUT_BLADE);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// plain geometric matmul operator (blade order, fp32)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void geom_matmul_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ out, int M, int K, int N) {
+  const int n = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (m >= M || n >= N) return;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int k = 0; k < K; ++k) {
+    const float4* pa = reinterpret_cast<const float4*>(a + ((size_t)m * K + k) * 8);
+    const float4* pb = reinterpret_cast<const float4*>(b + ((size_t)k * N + n) * 8);
+    const float4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
+    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int mp = blade_to_mask(p), mq = blade_to_mask(q);
+        const int o = mask_to_blade(mp ^ mq);
+        acc[o] = fmaf((float)mask_product_sign(mp, mq) * av[p], bv[q], acc[o]);
+      }
+  }
+  float4* po = reinterpret_cast<float4*>(out + ((size_t)m * N + n) * 8);
+  po[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  po[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+}  // namespace ygg
+
+using namespace ygg;
+
+YGG_API size_t ygg_prepared_weight_bytes(int E, int d_out, int d_in, int format) {
+  const size_t JB = (size_t)(d_out + 31) / 32, IP = (size_t)(d_in + 1) / 2;
+  switch (format) {
+    case kWF32: return (size_t)E * d_out * d_in * 8 * 4;
+    case kWBF16: return (size_t)E * JB * IP * 64 * 16 * 2;
+    case kWI8: return (size_t)E * JB * IP * 64 * 8;
+    default: return 0;
+  }
+}
+
+YGG_API int ygg_prepare_weights(const float* W, int E, int d_out, int d_in, int format, void* out, float* scales,
+                                hipStream_t stream) {
+  YGG_CHECK_ARG(format == kWF32 || format == kWBF16 || format == kWI8, "ygg_prepare_weights: format %d", format);
+  YGG_CHECK_ARG(E >= 1 && d_out >= 1 && d_in >= 1, "ygg_prepare_weights: bad sizes E=%d d_out=%d d_in=%d", E, d_out,
+                d_in);
+  YGG_CHECK_ARG(W && out, "ygg_prepare_weights: null pointer");
+  YGG_CHECK_ARG(format != kWI8 || scales, "ygg_prepare_weights: int8 format needs a scales buffer [E, d_out]");
+  if (format == kWI8) {
+    quant_scale_kernel<<<E * d_out, 256, 0, stream>>>(W, d_in, scales);
+    if (check_launch("quant_scale")) return -1;
+  }
+  const size_t JB = (size_t)(d_out + 31) / 32, IP = (size_t)(d_in + 1) / 2;
+  const size_t total = (format == kWF32) ? (size_t)E * d_out * d_in : (size_t)E * JB * IP * 64;
+  prep_weights_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(W, E, d_out, d_in, format, scales, out);
+  return check_launch("prep_weights");
+}
+
+YGG_API int ygg_prepare_bias(const float* b, int E, int d_out, float* out, hipStream_t stream) {
+  YGG_CHECK_ARG(b && out && E >= 1 && d_out >= 1, "ygg_prepare_bias: bad arguments");
+  const size_t n = (size_t)E * d_out;
+  prep_bias_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(b, n, out);
+  return check_launch("prep_bias");
+}
+
+template <int ACT>
+static void launch_mfma(dim3 grid, hipStream_t st, bool out_blade, bool wi8, int out_dt, const uint16_t* A,
+                        const void* Wp, const float* sc, const float* bias, const int32_t* off, int E, int d_in,
+                        int d_out, void* Y) {
+#define YGG_L(OB, WI, OD) grouped_cl_mfma<ACT, OB, WI, OD><<<grid, 256, 0, st>>>(A, Wp, sc, bias, off, E, d_in, d_out, Y)
+  if (out_dt == kBF16) {
+    if (out_blade) { if (wi8) YGG_L(true, true, kBF16); else YGG_L(true, false, kBF16); }
+    else { if (wi8) YGG_L(false, true, kBF16); else YGG_L(false, false, kBF16); }
+  } else {
+    if (out_blade) { if (wi8) YGG_L(true, true, kF32); else YGG_L(true, false, kF32); }
+    else { if (wi8) YGG_L(false, true, kF32); else YGG_L(false, false, kF32); }
+  }
+#undef YGG_L
+}
+
+template <int ACT>
+static void launch_f32(dim3 grid, hipStream_t st, bool out_blade, const float* A, const float* W, const float* bias,
+                       const int32_t* off, int E, int d_in, int d_out, float* Y) {
+  if (out_blade) grouped_cl_f32<ACT, true><<<grid, 256, 0, st>>>(A, W, bias, off, E, d_in, d_out, Y);
+  else grouped_cl_f32<ACT, false><<<grid, 256, 0, st>>>(A, W, bias, off, E, d_in, d_out, Y);
+}
+
+// x: [P, d_in, 8] in mask order (dtype f32 for format F32, bf16 otherwise).
+// y: [P, d_out, 8] (f32 for format F32; y_dtype for the others), mask order
+//    or blade order.  P_max bounds the rows (offsets[E] <= P_max).
+YGG_API int ygg_grouped_clifford_linear(const void* x, int P_max, const void* Wp, int format, const float* scales,
+                                        const float* bias, const int32_t* offsets, int E, int d_in, int d_out,
+                                        int act, void* y, int y_dtype, int y_blade_order, hipStream_t stream) {
+  YGG_CHECK_ARG(format == kWF32 || format == kWBF16 || format == kWI8, "grouped_clifford_linear: format %d", format);
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "grouped_clifford_linear: activation %d", act);
+  YGG_CHECK_ARG(E >= 1 && d_in >= 1 && d_out >= 1 && P_max >= 0, "grouped_clifford_linear: bad sizes");
+  YGG_CHECK_ARG(format != kWI8 || scales, "grouped_clifford_linear: int8 weights need scales");
+  YGG_CHECK_ARG(format == kWF32 ? y_dtype == kF32 : (y_dtype == kF32 || y_dtype == kBF16),
+                "grouped_clifford_linear: output dtype %d invalid for format %d", y_dtype, format);
+  if (P_max == 0) return 0;
+  YGG_CHECK_ARG(x && Wp && offsets && y, "grouped_clifford_linear: null pointer");
+  const bool ob = y_blade_order != 0;
+  if (format == kWF32) {
+    dim3 grid((P_max + kF32BM - 1) / kF32BM + E, (d_out + kF32BN - 1) / kF32BN);
+    const float* A = static_cast<const float*>(x);
+    const float* W = static_cast<const float*>(Wp);
+    float* Y = static_cast<float*>(y);
+    switch (act) {
+      case kActNone: launch_f32<kActNone>(grid, stream, ob, A, W, bias, offsets, E, d_in, d_out, Y); break;
+      case kActGelu: launch_f32<kActGelu>(grid, stream, ob, A, W, bias, offsets, E, d_in, d_out, Y); break;
+      case kActRelu: launch_f32<kActRelu>(grid, stream, ob, A, W, bias, offsets, E, d_in, d_out, Y); break;
+      default: launch_f32<kActSigmoid>(grid, stream, ob, A, W, bias, offsets, E, d_in, d_out, Y); break;
+    }
+    return check_launch("grouped_cl_f32");
+  }
+  dim3 grid((P_max + kMfmaBM - 1) / kMfmaBM + E, (d_out + kMfmaBN - 1) / kMfmaBN);
+  const uint16_t* A = static_cast<const uint16_t*>(x);
+  const bool wi8 = format == kWI8;
+  switch (act) {
+    case kActNone: launch_mfma<kActNone>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
+    case kActGelu: launch_mfma<kActGelu>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
+    case kActRelu: launch_mfma<kActRelu>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
+    default: launch_mfma<kActSigmoid>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
+  }
+  return check_launch("grouped_cl_mfma");
+}
+
+// Operator boundary of the path: out[m, n] = sum_k gp(a[m, k], b[k, n]).
+YGG_API int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K, int N, hipStream_t stream) {
+  YGG_CHECK_ARG(M >= 0 && K >= 0 && N >= 0, "ygg_geom_matmul_f32: bad sizes");
+  if (M == 0 || N == 0) return 0;
+  YGG_CHECK_ARG(a && b && out, "ygg_geom_matmul_f32: null pointer");
+  dim3 grid((N + 63) / 64, (M + 3) / 4);
+  geom_matmul_kernel<<<grid, 256, 0, stream>>>(a, b, out, M, K, N);
+  return check_launch("geom_matmul");
+}

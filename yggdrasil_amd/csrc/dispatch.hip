@@ -1,0 +1,232 @@
+// dispatch.hip -- token dispatch (gather into expert-grouped rows) and the
+// weighted combine, gfx950.
+//
+// Replaces hlm_block.py:178 (expert_input = flat_x[token_ids]) and
+// hlm_block.py:180-181 (weighted = w * y; np.add.at(output, token_ids, ...)).
+//
+// Dispatch is token-driven: one wave reads a token's row once (coalesced
+// 16-byte loads) and writes it to its k sorted positions, so x is read once
+// (N*R bytes) and the sorted buffer written once (N*k*R bytes).  Optionally
+// the two components e3/e12 are exchanged on the way, producing the "mask
+// order" the expert products consume.
+//
+// Combine is gather-based and atomic-free: one wave per token reads its k
+// rows and adds  w_s * y_s  in ascending expert order, each product rounded
+// before its add (no fused multiply-add) -- the order and rounding of
+// np.add.at called once per expert in ascending order.  Optionally a
+// residual is added last (hlm_block.py:151, x + ffn_out).
+
+#include "ygg_common.h"
+
+namespace ygg {
+
+// --- one multivector in registers ---------------------------------------
+struct MV {
+  float v[8];
+};
+
+template <int DT>
+__device__ inline MV load_mv(const void* base, size_t mv_index) {
+  MV m;
+  if constexpr (DT == kF32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + mv_index * 8);
+    const float4 a = p[0], b = p[1];
+    m.v[0] = a.x; m.v[1] = a.y; m.v[2] = a.z; m.v[3] = a.w;
+    m.v[4] = b.x; m.v[5] = b.y; m.v[6] = b.z; m.v[7] = b.w;
+  } else {
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + mv_index * 8);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      m.v[2 * c] = bf16_bits_to_f32((uint16_t)(w[c] & 0xffff));
+      m.v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(w[c] >> 16));
+    }
+  }
+  return m;
+}
+
+template <int DT>
+__device__ inline void store_mv(void* base, size_t mv_index, const MV& m) {
+  if constexpr (DT == kF32) {
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(base) + mv_index * 8);
+    p[0] = make_float4(m.v[0], m.v[1], m.v[2], m.v[3]);
+    p[1] = make_float4(m.v[4], m.v[5], m.v[6], m.v[7]);
+  } else {
+    uint4 q;
+    q.x = pack_bf16x2(m.v[0], m.v[1]);
+    q.y = pack_bf16x2(m.v[2], m.v[3]);
+    q.z = pack_bf16x2(m.v[4], m.v[5]);
+    q.w = pack_bf16x2(m.v[6], m.v[7]);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + mv_index * 8) = q;
+  }
+}
+
+// Raw 16/32-byte multivector copy (no conversion), optional e3<->e12 swap.
+template <int DT>
+struct RawMV {
+  uint4 a, b;  // b unused for bf16
+};
+
+template <int DT, bool SWAP34>
+__device__ inline RawMV<DT> load_raw(const void* base, size_t mv_index) {
+  RawMV<DT> r;
+  if constexpr (DT == kF32) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const float*>(base) + mv_index * 8);
+    r.a = p[0];
+    r.b = p[1];
+    if constexpr (SWAP34) {  // components 3 (a.w) and 4 (b.x)
+      const uint32_t t = r.a.w;
+      r.a.w = r.b.x;
+      r.b.x = t;
+    }
+  } else {
+    r.a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + mv_index * 8);
+    if constexpr (SWAP34) {  // component 3 = hi half of dword 1, component 4 = lo half of dword 2
+      const uint32_t d1 = r.a.y, d2 = r.a.z;
+      r.a.y = (d1 & 0xffffu) | (d2 << 16);
+      r.a.z = (d1 >> 16) | (d2 & 0xffff0000u);
+    }
+  }
+  return r;
+}
+
+template <int DT>
+__device__ inline void store_raw(void* base, size_t mv_index, const RawMV<DT>& r) {
+  if constexpr (DT == kF32) {
+    uint4* p = reinterpret_cast<uint4*>(static_cast<float*>(base) + mv_index * 8);
+    p[0] = r.a;
+    p[1] = r.b;
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + mv_index * 8) = r.a;
+  }
+}
+
+constexpr int kTokPerBlock = 4;  // one wave per token
+
+template <int DT, bool TO_MASK>
+__global__ __launch_bounds__(256) void dispatch_kernel(const void* __restrict__ x, int N, int k, int d,
+                                                       const int32_t* __restrict__ slot_pos,
+                                                       void* __restrict__ xs) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kTokPerBlock + (threadIdx.x >> 6);
+  if (t >= N) return;
+  int dst[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) dst[s] = (s < k) ? slot_pos[(size_t)t * k + s] : 0;
+  for (int i = lane; i < d; i += 64) {
+    const RawMV<DT> r = load_raw<DT, TO_MASK>(x, (size_t)t * d + i);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      if (s < k) store_raw<DT>(xs, (size_t)dst[s] * d + i, r);
+  }
+}
+
+template <int YT, bool Y_MASK, int OT, bool RESID>
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ ys, int N, int k, int d,
+                                                      const int32_t* __restrict__ topk_idx,
+                                                      const float* __restrict__ topk_w,
+                                                      const int32_t* __restrict__ slot_pos,
+                                                      const void* __restrict__ resid, void* __restrict__ out) {
+  // every product is rounded before its add, as in the reference: no contraction to fma
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kTokPerBlock + (threadIdx.x >> 6);
+  if (t >= N) return;
+  int ex[8], row[8];
+  float w[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const bool on = s < k;
+    ex[s] = on ? topk_idx[(size_t)t * k + s] : 0x7fffffff;
+    row[s] = on ? slot_pos[(size_t)t * k + s] : 0;
+    w[s] = on ? topk_w[(size_t)t * k + s] : 0.f;
+  }
+  // ascending expert order (insertion sort over <= 8 slots; distinct experts)
+#pragma unroll
+  for (int a = 1; a < 8; ++a)
+#pragma unroll
+    for (int b = a; b > 0; --b)
+      if (ex[b] < ex[b - 1]) {
+        int te = ex[b]; ex[b] = ex[b - 1]; ex[b - 1] = te;
+        int tr = row[b]; row[b] = row[b - 1]; row[b - 1] = tr;
+        float tw = w[b]; w[b] = w[b - 1]; w[b - 1] = tw;
+      }
+  for (int i = lane; i < d; i += 64) {
+    MV acc;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s < k) {
+        const MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc.v[c] = acc.v[c] + w[s] * y.v[c];
+      }
+    }
+    if constexpr (Y_MASK) {  // back to blade order
+      const float t3 = acc.v[3];
+      acc.v[3] = acc.v[4];
+      acc.v[4] = t3;
+    }
+    if constexpr (RESID) {
+      const MV r = load_mv<OT>(resid, (size_t)t * d + i);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc.v[c] = r.v[c] + acc.v[c];
+    }
+    store_mv<OT>(out, (size_t)t * d + i, acc);
+  }
+}
+
+}  // namespace ygg
+
+using namespace ygg;
+
+YGG_API int ygg_dispatch(const void* x, int dtype, int N, int k, int d, const int32_t* slot_pos, void* x_sorted,
+                         int to_mask_order, hipStream_t stream) {
+  YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_dispatch: dtype %d unsupported", dtype);
+  YGG_CHECK_ARG(N >= 0 && k >= 1 && k <= 8 && d >= 1, "ygg_dispatch: bad sizes N=%d k=%d d=%d", N, k, d);
+  if (N == 0) return 0;
+  YGG_CHECK_ARG(x && slot_pos && x_sorted, "ygg_dispatch: null pointer");
+  const int grid = (N + kTokPerBlock - 1) / kTokPerBlock;
+  if (dtype == kF32) {
+    if (to_mask_order) dispatch_kernel<kF32, true><<<grid, 256, 0, stream>>>(x, N, k, d, slot_pos, x_sorted);
+    else dispatch_kernel<kF32, false><<<grid, 256, 0, stream>>>(x, N, k, d, slot_pos, x_sorted);
+  } else {
+    if (to_mask_order) dispatch_kernel<kBF16, true><<<grid, 256, 0, stream>>>(x, N, k, d, slot_pos, x_sorted);
+    else dispatch_kernel<kBF16, false><<<grid, 256, 0, stream>>>(x, N, k, d, slot_pos, x_sorted);
+  }
+  return check_launch("dispatch");
+}
+
+template <int YT, int OT>
+static void launch_combine(int grid, hipStream_t st, const void* ys, int N, int k, int d, const int32_t* idx,
+                           const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask) {
+  if (y_mask) {
+    if (resid) combine_kernel<YT, true, OT, true><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+    else combine_kernel<YT, true, OT, false><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+  } else {
+    if (resid) combine_kernel<YT, false, OT, true><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+    else combine_kernel<YT, false, OT, false><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+  }
+}
+
+YGG_API int ygg_combine(const void* y_sorted, int y_dtype, int y_mask_order, int N, int k, int d,
+                        const int32_t* topk_idx, const float* topk_w, const int32_t* slot_pos, const void* residual,
+                        void* out, int out_dtype, hipStream_t stream) {
+  YGG_CHECK_ARG((y_dtype == kF32 || y_dtype == kBF16) && (out_dtype == kF32 || out_dtype == kBF16),
+                "ygg_combine: dtypes %d/%d unsupported", y_dtype, out_dtype);
+  YGG_CHECK_ARG(N >= 0 && k >= 1 && k <= 8 && d >= 1, "ygg_combine: bad sizes N=%d k=%d d=%d", N, k, d);
+  if (N == 0) return 0;
+  YGG_CHECK_ARG(y_sorted && topk_idx && topk_w && slot_pos && out, "ygg_combine: null pointer");
+  const int grid = (N + kTokPerBlock - 1) / kTokPerBlock;
+  const bool ym = y_mask_order != 0;
+  if (y_dtype == kF32 && out_dtype == kF32)
+    launch_combine<kF32, kF32>(grid, stream, y_sorted, N, k, d, topk_idx, topk_w, slot_pos, residual, out, ym);
+  else if (y_dtype == kBF16 && out_dtype == kBF16)
+    launch_combine<kBF16, kBF16>(grid, stream, y_sorted, N, k, d, topk_idx, topk_w, slot_pos, residual, out, ym);
+  else if (y_dtype == kBF16 && out_dtype == kF32)
+    launch_combine<kBF16, kF32>(grid, stream, y_sorted, N, k, d, topk_idx, topk_w, slot_pos, residual, out, ym);
+  else
+    launch_combine<kF32, kBF16>(grid, stream, y_sorted, N, k, d, topk_idx, topk_w, slot_pos, residual, out, ym);
+  return check_launch("combine");
+}

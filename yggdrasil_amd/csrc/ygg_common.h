@@ -1,0 +1,110 @@
+// ygg_common.h -- shared definitions for the MI355X (gfx950) MoE-HLM kernels.
+//
+// Multivector layouts used on the device
+// --------------------------------------
+// * "blade order" -- the reference's flat layout 1,e1,e2,e3,e12,e13,e23,e123
+//   (rune/types/multivector.py:7).  Every tensor that crosses the C ABI
+//   (layer input x, layer output, user-visible weights) is in blade order.
+// * "mask order" -- component c is the blade whose generator bitmask is c
+//   (bit0 = e1, bit1 = e2, bit2 = e3): 1,e1,e2,e12,e3,e13,e23,e123.  In this
+//   order the geometric product of basis blades is  e_p e_q = s(p,q) e_{p^q},
+//   so the 8x8 block L(w) of a weight multivector is a signed XOR-permutation.
+//   Internal activations between the two expert products are kept in mask
+//   order, and the prepared weights are stored in mask order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifndef YGG_API
+#define YGG_API extern "C" __attribute__((visibility("default")))
+#endif
+
+namespace ygg {
+
+// blade index (blade order) -> generator bitmask; the map is an involution
+// except for the e3 / e12 swap: mask order position of blade b is kBladeMask[b].
+__host__ __device__ constexpr int blade_to_mask(int b) {
+  return b == 0 ? 0 : b == 1 ? 1 : b == 2 ? 2 : b == 3 ? 4 : b == 4 ? 3 : b == 5 ? 5 : b == 6 ? 6 : 7;
+}
+__host__ __device__ constexpr int mask_to_blade(int m) {
+  return m == 0 ? 0 : m == 1 ? 1 : m == 2 ? 2 : m == 3 ? 4 : m == 4 ? 3 : m == 5 ? 5 : m == 6 ? 6 : 7;
+}
+
+// Sign of e_A e_B for generator bitmasks A, B in Cl(3,0): (-1)^(number of
+// pairs x in A, y in B with x > y) -- each such pair is one transposition
+// needed to bring the concatenated word into sorted order; e_i e_i = +1.
+__host__ __device__ constexpr int mask_product_sign(int a, int b) {
+  int swaps = 0;
+  for (int x = 0; x < 3; ++x)
+    if (a & (1 << x))
+      for (int y = 0; y < x; ++y)
+        if (b & (1 << y)) ++swaps;
+  return (swaps & 1) ? -1 : 1;
+}
+
+// --- weight sign folding ---------------------------------------------------
+// Prepared weights store  W'_p = kWFold[p] * W_p  (mask order) and every
+// output blade r of a product is produced as  kOutFold[r] * y_r.  With this
+// choice the remaining sign of every entry of the expanded block,
+//   kOutFold[r] * kWFold[p] * s(p, p^r)   (A operand at mask position p),
+// is -1 on exactly one aligned pair {2t, 2t+1} of p for each r and +1
+// elsewhere, so one 32-bit XOR per output blade applies all signs to a
+// packed bf16 operand.  (Found by exhaustive search over the 2^16 sign
+// foldings of weights and inputs; checked by static_assert below.)
+__host__ __device__ constexpr int kWFold(int p) { return (p == 2 || p == 4) ? -1 : 1; }
+__host__ __device__ constexpr int kOutFold(int r) { return (r == 0 || r == 4) ? -1 : 1; }
+
+// Residual sign of entry (r, p) after folding.
+__host__ __device__ constexpr int folded_sign(int r, int p) {
+  return kOutFold(r) * kWFold(p) * mask_product_sign(p, p ^ r);
+}
+// The aligned pair index t (p in {2t, 2t+1}) that carries the -1 for row r.
+__host__ __device__ constexpr int neg_pair(int r) {
+  return folded_sign(r, 0) < 0 ? 0 : folded_sign(r, 2) < 0 ? 1 : folded_sign(r, 4) < 0 ? 2 : 3;
+}
+
+constexpr bool check_folding() {
+  for (int r = 0; r < 8; ++r) {
+    int t = neg_pair(r);
+    for (int p = 0; p < 8; ++p) {
+      int want = (p / 2 == t) ? -1 : 1;
+      if (folded_sign(r, p) != want) return false;
+    }
+  }
+  return true;
+}
+static_assert(check_folding(), "sign folding must leave one negative aligned pair per output blade");
+
+// --- bf16 helpers (bit-level; round to nearest even) --------------------------
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffffu) ? 0x40u : 0u));  // inf / nan
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
+  return __builtin_bit_cast(float, (uint32_t)h << 16);
+}
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+// --- error reporting ------------------------------------------------------
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+enum DType : int { kF32 = 0, kBF16 = 1, kI8 = 2 };
+enum Act : int { kActNone = 0, kActGelu = 1, kActRelu = 2, kActSigmoid = 3 };
+
+inline int dtype_size(int dt) { return dt == kF32 ? 4 : dt == kBF16 ? 2 : dt == kI8 ? 1 : 0; }
+
+}  // namespace ygg
+
+#define YGG_CHECK_ARG(cond, ...)        \
+  do {                                  \
+    if (!(cond)) {                      \
+      ::ygg::set_error(__VA_ARGS__);    \
+      return -1;                        \
+    }                                   \
+  } while (0)

@@ -1,0 +1,233 @@
+"""Drop-in torch modules for the MoE-HLM expert layer (host side, PyTorch-ROCm).
+
+``CliffordMoELayer`` keeps the geoformer MoE module interface
+``forward(x: (B, T, D)) -> (out: (B, T, D), aux_loss: 0-d tensor)``
+(``geoformer/moe_hlm/router.py:97-142``, ``geoformer/triton_kernels/expert_gemm.py:192-254``)
+with ``D = 8 d`` multivector-minor, and also accepts the holograph layout
+``(B, T, d, 8)`` of ``HLMBlock._moe_forward`` (``holograph/models/hlm_block.py:154-183``),
+whose arithmetic it computes: CliffordRouter gating (``holograph/layers/clifford_router.py:24-123``),
+experts ``CliffordFFN`` = CliffordLinear -> grade-wise activation -> CliffordLinear
+(``hlm_block.py:41-61``), and the weighted combine in ascending expert order.
+
+All compute runs in the HIP library (``include/ygg_moe.h``); this module only
+owns parameters, prepares the device weight layouts and allocates outputs.
+There is no CPU path.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+from . import ops
+
+ACTIVATIONS = ("gelu", "relu", "sigmoid")  # hlm_block.py:28-32
+ROUTERS = ("energy", "logits", "clifford_head")
+
+
+@dataclass
+class MoEHLMConfig:
+    """Layer configuration (mirrors HLMConfig's MoE fields, hlm_config.py:9-78).
+
+    d_model     multivector channels d (flat width 8 d)
+    d_ff        expert hidden width F (multivectors)
+    n_experts   E (<= 64)
+    top_k       k (<= 8)
+    activation  'gelu' | 'relu' | 'sigmoid' (grade-wise)
+    dtype       activation dtype: torch.float32 or torch.bfloat16
+    weight_format  'f32' (fp32 layers), 'bf16' or 'int8' (bf16 layers)
+    router      'energy' -- CliffordRouter's grade-energy logits (default, the reference);
+                'clifford_head' -- CliffordLinear(d -> E) then the scalar part;
+                'logits' -- the caller passes logits to forward()
+    """
+
+    d_model: int
+    d_ff: int
+    n_experts: int = 4
+    top_k: int = 2
+    activation: str = "gelu"
+    dtype: torch.dtype = torch.float32
+    weight_format: str | None = None
+    router: str = "energy"
+
+    def __post_init__(self):
+        if self.activation not in ACTIVATIONS:
+            raise ValueError(f"activation must be one of {ACTIVATIONS}")
+        if self.router not in ROUTERS:
+            raise ValueError(f"router must be one of {ROUTERS}")
+        if self.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("dtype must be float32 or bfloat16")
+        if self.weight_format is None:
+            self.weight_format = "f32" if self.dtype == torch.float32 else "bf16"
+        if (self.dtype == torch.float32) != (self.weight_format == "f32"):
+            raise ValueError("fp32 layers use 'f32' weights; bf16 layers use 'bf16' or 'int8'")
+        if not 1 <= self.n_experts <= 64 or not 1 <= self.top_k <= min(8, self.n_experts):
+            raise ValueError("need 1 <= n_experts <= 64 and 1 <= top_k <= min(8, n_experts)")
+
+
+def xavier_clifford_init(d_out: int, d_in: int, generator=None) -> torch.Tensor:
+    """Grade-wise Xavier init of a CliffordLinear weight (clifford_linear.py:58-81)."""
+    w = torch.zeros(d_out, d_in, 8)
+    fan = d_in + d_out
+    for lo, hi in ((0, 1), (1, 4), (4, 7), (7, 8)):
+        n = hi - lo
+        w[..., lo:hi] = torch.randn(d_out, d_in, n, generator=generator) * math.sqrt(2.0 / (fan * n))
+    return w
+
+
+class CliffordMoELayer(nn.Module):
+    """Routed mixture of CliffordFFN experts on Cl(3,0) multivectors."""
+
+    def __init__(self, cfg: MoEHLMConfig, device=None, generator: torch.Generator | None = None):
+        super().__init__()
+        self.cfg = cfg
+        E, d, F = cfg.n_experts, cfg.d_model, cfg.d_ff
+        self.router_weight = nn.Parameter(torch.randn(E, 4, generator=generator) * 0.1)  # clifford_router.py:48
+        self.router_bias = nn.Parameter(torch.zeros(E))  # clifford_router.py:49
+        self.w_up = nn.Parameter(torch.stack([xavier_clifford_init(F, d, generator) for _ in range(E)]))
+        self.b_up = nn.Parameter(torch.zeros(E, F, 8))
+        self.w_down = nn.Parameter(torch.stack([xavier_clifford_init(d, F, generator) for _ in range(E)]))
+        self.b_down = nn.Parameter(torch.zeros(E, d, 8))
+        if cfg.router == "clifford_head":
+            self.head_weight = nn.Parameter(xavier_clifford_init(E, d, generator))
+        else:
+            self.head_weight = None
+        self._prepared = None
+        self._workspace = None
+        self.last_routing = None
+        if device is not None:
+            self.to(device)
+
+    # -- parameters ----------------------------------------------------------
+    @torch.no_grad()
+    def load_reference_weights(self, router_weight=None, router_bias=None, w_up=None, b_up=None, w_down=None,
+                               b_down=None, head_weight=None):
+        """Copy weights given in the reference's layouts (blade order, fp32)."""
+        for name, val in (("router_weight", router_weight), ("router_bias", router_bias), ("w_up", w_up),
+                          ("b_up", b_up), ("w_down", w_down), ("b_down", b_down), ("head_weight", head_weight)):
+            if val is not None:
+                p = getattr(self, name)
+                p.copy_(torch.as_tensor(val, dtype=p.dtype, device=p.device).reshape(p.shape))
+        self._prepared = None
+
+    def _param_versions(self):
+        return tuple(p._version for p in self.parameters()) + (self.w_up.device,)
+
+    @torch.no_grad()
+    def prepare(self):
+        """Build the device weight layouts (done lazily; redone when parameters change)."""
+        fmt = self.cfg.weight_format
+        head = None
+        if self.head_weight is not None:
+            head = ops.prepare_weights(self.head_weight.detach().unsqueeze(0), "f32" if fmt == "f32" else "bf16")
+        self._prepared = dict(
+            key=self._param_versions(),
+            w_up=ops.prepare_weights(self.w_up.detach(), fmt),
+            w_down=ops.prepare_weights(self.w_down.detach(), fmt),
+            b_up=ops.prepare_bias(self.b_up.detach()),
+            b_down=ops.prepare_bias(self.b_down.detach()),
+            head=head,
+        )
+        return self._prepared
+
+    def _get_prepared(self):
+        if self._prepared is None or self._prepared["key"] != self._param_versions():
+            self.prepare()
+        return self._prepared
+
+    # -- forward ---------------------------------------------------------------
+    def _head_logits(self, flat_x: torch.Tensor, prep) -> torch.Tensor:
+        """CliffordLinear(d -> E) then grade 0 (hlm.py:109,141-145 pattern)."""
+        Nt = flat_x.shape[0]
+        xs = ops.to_mask_order(flat_x)
+        offsets = torch.tensor([0, Nt], device=flat_x.device, dtype=torch.int32)
+        y = ops.grouped_clifford_linear(xs, prep["head"], offsets, None, "none", out_dtype=torch.float32)
+        return y[..., 0].contiguous()
+
+    def moe_forward(self, x: torch.Tensor, logits: torch.Tensor | None = None,
+                    residual: torch.Tensor | None = None) -> torch.Tensor:
+        """``HLMBlock._moe_forward``: x (B, T, d, 8) -> (B, T, d, 8) (+ residual)."""
+        cfg = self.cfg
+        if x.dim() != 4 or x.shape[-1] != 8 or x.shape[-2] != cfg.d_model:
+            raise ValueError(f"expected (B, T, {cfg.d_model}, 8), got {tuple(x.shape)}")
+        if x.dtype != cfg.dtype:
+            raise ValueError(f"layer dtype is {cfg.dtype}, input is {x.dtype}")
+        B, T = x.shape[:2]
+        flat = x.reshape(B * T, cfg.d_model, 8).contiguous()
+        prep = self._get_prepared()
+        if cfg.router == "logits":
+            if logits is None:
+                raise ValueError("router='logits' needs logits")
+        elif cfg.router == "clifford_head" and logits is None:
+            logits = self._head_logits(flat, prep)
+        if logits is not None:
+            logits = logits.reshape(B * T, cfg.n_experts).float().contiguous()
+        res = residual.reshape(B * T, cfg.d_model, 8).contiguous() if residual is not None else None
+        ws_bytes = ops.moe_workspace_bytes(B * T, cfg.d_model, cfg.d_ff, cfg.n_experts, cfg.top_k, cfg.dtype)
+        if self._workspace is None or self._workspace.numel() < ws_bytes or self._workspace.device != x.device:
+            self._workspace = torch.empty((max(ws_bytes, 1),), device=x.device, dtype=torch.uint8)
+        out, routing = ops.moe_forward(flat, cfg.top_k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"],
+                                       cfg.activation, logits=logits,
+                                       router_weight=self.router_weight.detach() if logits is None else None,
+                                       router_bias=self.router_bias.detach() if logits is None else None,
+                                       residual=res, workspace=self._workspace)
+        self.last_routing = routing
+        return out.reshape(B, T, cfg.d_model, 8)
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None):
+        """geoformer interface: (B, T, 8 d) or (B, T, d, 8) -> (same shape, aux_loss)."""
+        flat_in = x.dim() == 3
+        if flat_in:
+            B, T, D = x.shape
+            if D != 8 * self.cfg.d_model:
+                raise ValueError(f"expected D = 8 * {self.cfg.d_model}, got {D}")
+            x4 = x.reshape(B, T, self.cfg.d_model, 8)
+        else:
+            x4 = x
+        out = self.moe_forward(x4, logits=logits)
+        return (out.reshape(x.shape) if flat_in else out), self.aux_loss()
+
+    def aux_loss(self) -> torch.Tensor:
+        """CliffordRouter.load_balance_loss (clifford_router.py:108-117) on this call's counts.
+
+        The reference's formula sum_e (f_e - 1/E)^2 with f = counts / sum(counts); the
+        reference never updates its counts and so always returns 0, this layer uses the
+        counts of the last forward.
+        """
+        if self.last_routing is None:
+            return torch.zeros((), device=self.w_up.device)
+        c = self.last_routing["counts"].float()
+        f = c / (c.sum() + 1e-12)
+        return ((f - 1.0 / self.cfg.n_experts) ** 2).sum()
+
+
+class CliffordLinear(nn.Module):
+    """CliffordLinear (clifford_linear.py:84-123) on the GPU: y = W * x + b per output channel."""
+
+    def __init__(self, d_in: int, d_out: int, bias: bool = True, dtype: torch.dtype = torch.float32, device=None):
+        super().__init__()
+        self.d_in, self.d_out, self.dtype = d_in, d_out, dtype
+        self.weight = nn.Parameter(xavier_clifford_init(d_out, d_in))
+        self.bias = nn.Parameter(torch.zeros(d_out, 8)) if bias else None
+        self._prep = None
+        if device is not None:
+            self.to(device)
+
+    def _prepared(self):
+        key = (self.weight._version, None if self.bias is None else self.bias._version, self.weight.device)
+        if self._prep is None or self._prep[0] != key:
+            fmt = "f32" if self.dtype == torch.float32 else "bf16"
+            self._prep = (key, ops.prepare_weights(self.weight.detach().unsqueeze(0), fmt),
+                          ops.prepare_bias(self.bias.detach().unsqueeze(0)) if self.bias is not None else None)
+        return self._prep
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        batch = x.shape[:-2]
+        flat = ops.to_mask_order(x.reshape(-1, self.d_in, 8).to(self.dtype))
+        _, pw, pb = self._prepared()
+        offsets = torch.tensor([0, flat.shape[0]], device=x.device, dtype=torch.int32)
+        y = ops.grouped_clifford_linear(flat, pw, offsets, pb, "none", out_dtype=self.dtype)
+        return y.reshape(*batch, self.d_out, 8)

@@ -1,0 +1,257 @@
+"""Torch-tensor wrappers over the C ABI (``include/ygg_moe.h``).
+
+Every function takes CUDA (HIP) tensors, allocates its outputs with torch on
+the same device, and enqueues the HIP kernels on the current torch stream.
+There is no CPU path: CPU tensors are rejected.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+from ._native import check, lib, ptr, stream_handle
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
+ACT_CODE = {"none": 0, "gelu": 1, "relu": 2, "sigmoid": 3}
+WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2}
+
+
+def _dev(*tensors):
+    for t in tensors:
+        if t is not None:
+            if not t.is_cuda:
+                raise ValueError("yggdrasil_amd ops run on the GPU only (got a CPU tensor)")
+            if not t.is_contiguous():
+                raise ValueError("tensors must be contiguous")
+    return tensors[0].device
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; use float32 or bfloat16") from None
+
+
+# ---------------------------------------------------------------------------
+# operator boundary
+# ---------------------------------------------------------------------------
+
+
+def geom_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``out[m, n] = sum_k gp(a[m, k], b[k, n])`` (fp32, blade order).
+
+    Drop-in for ``rune.ops.batched.geom_matmul`` (``rune/ops/batched.py:320-344``).
+    """
+    dev = _dev(a, b)
+    if a.dtype != torch.float32 or b.dtype != torch.float32:
+        raise ValueError("geom_matmul is fp32")
+    if a.dim() != 3 or b.dim() != 3 or a.shape[2] != 8 or b.shape[2] != 8 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"shapes {tuple(a.shape)} x {tuple(b.shape)} do not form (M,K,8) x (K,N,8)")
+    M, K, _ = a.shape
+    Nn = b.shape[1]
+    out = torch.empty((M, Nn, 8), device=dev, dtype=torch.float32)
+    check(lib().ygg_geom_matmul_f32(ptr(a), ptr(b), ptr(out), M, K, Nn, stream_handle(dev)), "geom_matmul")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Routing:
+    """Result of :func:`route` (all on the device)."""
+
+    topk_idx: torch.Tensor  # (N, k) int32, slot 0 = most probable
+    topk_w: torch.Tensor  # (N, k) fp32, renormalised
+    counts: torch.Tensor  # (E,) int32
+    offsets: torch.Tensor  # (E+1,) int32
+    perm: torch.Tensor  # (N*k,) int32, token of each expert-grouped row
+    slot_pos: torch.Tensor  # (N, k) int32, row of each slot
+
+    @property
+    def k(self) -> int:
+        return self.topk_idx.shape[1]
+
+
+def router_energy_logits(x: torch.Tensor, router_weight: torch.Tensor, router_bias: torch.Tensor,
+                         return_energy: bool = False):
+    """CliffordRouter logits from grade energies (``clifford_router.py:54-90``). x: (N, d, 8)."""
+    dev = _dev(x, router_weight, router_bias)
+    Nt, d = x.shape[0], x.shape[1]
+    E = router_weight.shape[0]
+    logits = torch.empty((Nt, E), device=dev, dtype=torch.float32)
+    energy = torch.empty((Nt, 4), device=dev, dtype=torch.float32) if return_energy else None
+    check(lib().ygg_router_energy_logits(ptr(x), _dtype_code(x), Nt, d, ptr(router_weight.float().contiguous()),
+                                         ptr(router_bias.float().contiguous()), E, ptr(logits), ptr(energy),
+                                         stream_handle(dev)), "router_energy_logits")
+    return (logits, energy) if return_energy else logits
+
+
+def route(logits: torch.Tensor, k: int) -> Routing:
+    """Softmax, top-k (lowest index wins ties) and the expert counting sort."""
+    dev = _dev(logits)
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise ValueError("logits must be (N, E) float32")
+    Nt, E = logits.shape
+    L = lib()
+    ws_bytes = L.ygg_route_workspace_bytes(Nt, E, k)
+    i32 = dict(device=dev, dtype=torch.int32)
+    r = Routing(
+        topk_idx=torch.empty((Nt, k), **i32),
+        topk_w=torch.empty((Nt, k), device=dev, dtype=torch.float32),
+        counts=torch.empty((E,), **i32),
+        offsets=torch.empty((E + 1,), **i32),
+        perm=torch.empty((Nt * k,), **i32),
+        slot_pos=torch.empty((Nt, k), **i32),
+    )
+    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    check(L.ygg_route(ptr(logits), Nt, E, k, ptr(r.topk_idx), ptr(r.topk_w), ptr(r.counts), ptr(r.offsets),
+                      ptr(r.perm), ptr(r.slot_pos), ptr(ws), ws_bytes, stream_handle(dev)), "route")
+    return r
+
+
+def dispatch(x: torch.Tensor, routing: Routing, mask_order: bool = False) -> torch.Tensor:
+    """Expert-grouped copy of the token rows: ``out[slot_pos[t, s]] = x[t]``. x: (N, d, 8)."""
+    dev = _dev(x)
+    Nt, d = x.shape[0], x.shape[1]
+    k = routing.k
+    out = torch.empty((Nt * k, d, 8), device=dev, dtype=x.dtype)
+    check(lib().ygg_dispatch(ptr(x), _dtype_code(x), Nt, k, d, ptr(routing.slot_pos), ptr(out), int(mask_order),
+                             stream_handle(dev)), "dispatch")
+    return out
+
+
+def combine(y_sorted: torch.Tensor, routing: Routing, residual: torch.Tensor | None = None,
+            y_mask_order: bool = False, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Weighted combine in ascending expert order (+ residual). y_sorted: (N*k, d, 8)."""
+    dev = _dev(y_sorted, residual)
+    Nt, k = routing.topk_idx.shape
+    d = y_sorted.shape[1]
+    out_dtype = out_dtype or y_sorted.dtype
+    if residual is not None and residual.dtype != out_dtype:
+        raise ValueError("residual dtype must equal the output dtype")
+    out = torch.empty((Nt, d, 8), device=dev, dtype=out_dtype)
+    check(lib().ygg_combine(ptr(y_sorted), _dtype_code(y_sorted), int(y_mask_order), Nt, k, d,
+                            ptr(routing.topk_idx), ptr(routing.topk_w), ptr(routing.slot_pos), ptr(residual),
+                            ptr(out), DTYPE_CODE[out_dtype], stream_handle(dev)), "combine")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# expert products
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class PreparedWeights:
+    """Expert weights in the device layout of one weight format."""
+
+    data: torch.Tensor
+    scales: torch.Tensor | None
+    fmt: str
+    E: int
+    d_out: int
+    d_in: int
+
+
+def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
+    """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8')."""
+    dev = _dev(w)
+    if w.dim() == 3:
+        w = w.unsqueeze(0)
+    w = w.float().contiguous()
+    E, d_out, d_in, _ = w.shape
+    code = WFORMAT_CODE[fmt]
+    L = lib()
+    nbytes = L.ygg_prepared_weight_bytes(E, d_out, d_in, code)
+    data = torch.empty((nbytes,), device=dev, dtype=torch.uint8)
+    scales = torch.empty((E, d_out), device=dev, dtype=torch.float32) if fmt == "int8" else None
+    check(L.ygg_prepare_weights(ptr(w), E, d_out, d_in, code, ptr(data), ptr(scales), stream_handle(dev)),
+          "prepare_weights")
+    return PreparedWeights(data, scales, fmt, E, d_out, d_in)
+
+
+def prepare_bias(b: torch.Tensor | None) -> torch.Tensor | None:
+    """(E, d_out, 8) blade order -> mask order fp32."""
+    if b is None:
+        return None
+    dev = _dev(b)
+    b = b.float().contiguous()
+    if b.dim() == 2:
+        b = b.unsqueeze(0)
+    E, d_out, _ = b.shape
+    out = torch.empty_like(b)
+    check(lib().ygg_prepare_bias(ptr(b), E, d_out, ptr(out), stream_handle(dev)), "prepare_bias")
+    return out
+
+
+def grouped_clifford_linear(x_sorted: torch.Tensor, pw: PreparedWeights, offsets: torch.Tensor,
+                            bias_prepared: torch.Tensor | None = None, act: str = "none",
+                            out_dtype: torch.dtype | None = None, out_blade_order: bool = True) -> torch.Tensor:
+    """Per-expert CliffordLinear on expert-grouped rows. x_sorted: (P, d_in, 8) in mask order."""
+    dev = _dev(x_sorted, offsets, bias_prepared)
+    P = x_sorted.shape[0]
+    if x_sorted.shape[1] != pw.d_in:
+        raise ValueError(f"x has d_in={x_sorted.shape[1]}, weights expect {pw.d_in}")
+    want_x = torch.float32 if pw.fmt == "f32" else torch.bfloat16
+    if x_sorted.dtype != want_x:
+        raise ValueError(f"weight format {pw.fmt} takes {want_x} activations")
+    out_dtype = out_dtype or x_sorted.dtype
+    y = torch.empty((P, pw.d_out, 8), device=dev, dtype=out_dtype)
+    check(lib().ygg_grouped_clifford_linear(ptr(x_sorted), P, ptr(pw.data), WFORMAT_CODE[pw.fmt], ptr(pw.scales),
+                                            ptr(bias_prepared), ptr(offsets), pw.E, pw.d_in, pw.d_out,
+                                            ACT_CODE[act], ptr(y), DTYPE_CODE[out_dtype], int(out_blade_order),
+                                            stream_handle(dev)), "grouped_clifford_linear")
+    return y
+
+
+def moe_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype) -> int:
+    return lib().ygg_moe_workspace_bytes(Nt, d, F, E, k, DTYPE_CODE[dtype])
+
+
+def moe_forward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: PreparedWeights,
+                b_up: torch.Tensor | None = None, b_down: torch.Tensor | None = None, act: str = "gelu",
+                logits: torch.Tensor | None = None, router_weight: torch.Tensor | None = None,
+                router_bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """The whole layer in one call (``ygg_moe_forward``). x: (N, d, 8). Returns (out, Routing-lite)."""
+    dev = _dev(x, logits, residual)
+    Nt, d = x.shape[0], x.shape[1]
+    E, F = w_up.E, w_up.d_out
+    if w_down.d_in != F or w_down.d_out != d or w_up.d_in != d or w_down.E != E:
+        raise ValueError("expert weight shapes do not chain d -> F -> d")
+    if w_up.fmt != w_down.fmt:
+        raise ValueError("up and down weights must share a format")
+    ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype)
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    if out is None:
+        out = torch.empty_like(x)
+    i32 = dict(device=dev, dtype=torch.int32)
+    topk_idx = torch.empty((Nt, k), **i32)
+    topk_w = torch.empty((Nt, k), device=dev, dtype=torch.float32)
+    counts = torch.empty((E,), **i32)
+    offsets = torch.empty((E + 1,), **i32)
+    rw = router_weight.float().contiguous() if router_weight is not None else None
+    rb = router_bias.float().contiguous() if router_bias is not None else None
+    check(lib().ygg_moe_forward(ptr(x), _dtype_code(x), Nt, d, F, E, k, ACT_CODE[act], ptr(logits), ptr(rw),
+                                ptr(rb), ptr(w_up.data), ptr(w_up.scales), ptr(b_up), ptr(w_down.data),
+                                ptr(w_down.scales), ptr(b_down), WFORMAT_CODE[w_up.fmt], ptr(residual), ptr(out),
+                                ptr(topk_idx), ptr(topk_w), ptr(counts), ptr(offsets), ptr(workspace), ws_bytes,
+                                stream_handle(dev)), "moe_forward")
+    return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets)
+
+
+def to_mask_order(x: torch.Tensor) -> torch.Tensor:
+    """Blade order -> mask order (exchange components 3 and 4)."""
+    return x[..., [0, 1, 2, 4, 3, 5, 6, 7]].contiguous()
+
+
+def symbols() -> list[str]:
+    return list(N.SIGNATURES)
