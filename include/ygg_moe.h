@@ -18,7 +18,8 @@
  *    where an argument says "mask order" (1, e1, e2, e12, e3, e13, e23, e123,
  *    i.e. e3 and e12 exchanged), the layout the expert products consume.
  *  - dtype codes: 0 = fp32, 1 = bf16 (activations); weight formats:
- *    0 = fp32, 1 = bf16 (dual, sign-folded), 2 = int8 per-output-channel.
+ *    0 = fp32, 1 = bf16 (dual, sign-folded), 2 = int8 per-output-channel,
+ *    3 = bf16 Pauli (the weights as 2x2 complex matrices; even d_in).
  *    activation codes: 0 none, 1 gelu, 2 relu, 3 sigmoid
  *    (holograph/models/hlm_block.py:28-32).
  */
@@ -119,6 +120,29 @@ int ygg_grouped_clifford_linear(const void* x, int P_max, const void* w_prepared
                                 const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out,
                                 int act, void* y, int y_dtype, int y_blade_order, ygg_stream_t stream);
 
+/* The same products with weights in format 3, computed as complex GEMMs:
+ * Cl(3,0) is the algebra of 2x2 complex matrices, so CliffordLinear is a
+ * complex contraction with 32 real multiply-adds per multivector pair.
+ * x_layout 0: x holds blade-order bf16 rows (N, d_in, 8) and row r of the
+ *   product reads x[gather[r]] (gather NULL: x[r]) -- the dispatch copy of
+ *   hlm_block.py:178 fused into the product;
+ * x_layout 1: x holds "Pauli half-rows" (rows, 2, d_in, 4) bf16, the layout
+ *   this call writes for y_layout 0 (see ygg_pauli_rows_from_blade); row r of
+ *   the product reads x[gather[r]] (gather NULL: x[r]).
+ * y_layout 0: Pauli half-rows (P, 2, d_out, 4) bf16 (d_out even);
+ * y_layout 1: blade-order rows (P, d_out, 8) of y_dtype (0 fp32, 1 bf16).
+ * bias: prepared with ygg_prepare_bias (mask order) or NULL.  act as above.
+ * x and one expert's prepared weights must each be smaller than 2 GiB.
+ * Replaces CliffordLinear.forward (clifford_linear.py:101-123) of every
+ * expert, with the activation (activations.py:15-128) fused. */
+int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather, int P_max, const void* w_prepared,
+                             const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out, int act,
+                             void* y, int y_layout, int y_dtype, ygg_stream_t stream);
+
+/* Blade-order bf16 rows (rows, d, 8) -> Pauli half-rows (rows, 2, d, 4) bf16;
+ * d even.  Conversion helper for callers of ygg_pauli_grouped_linear. */
+int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out, ygg_stream_t stream);
+
 /* ---- the whole layer ---------------------------------------------------------
  * Workspace bytes of ygg_moe_forward. */
 size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype);
@@ -126,7 +150,8 @@ size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype);
 /* HLMBlock._moe_forward (hlm_block.py:154-183): x (N, d, 8) of dtype ->
  * out (N, d, 8) of dtype (+ residual if not NULL).  logits (N, E) or NULL
  * (then router_w/router_b give the grade-energy logits).  Expert weights
- * prepared with ygg_prepare_weights (format 0 for fp32, 1 or 2 for bf16),
+ * prepared with ygg_prepare_weights (format 0 for fp32, 1, 2 or 3 for bf16;
+ * format 3 gathers the token rows inside the up projection),
  * biases prepared with ygg_prepare_bias or NULL.  topk_idx/topk_w/counts/
  * offsets as in ygg_route. */
 int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act, const float* logits,

@@ -74,6 +74,15 @@ def test_argument_errors_are_reported_not_aborted():
     assert L.ygg_prepare_weights(None, 1, 1, 1, 5, None, None, None) == -1
     assert L.ygg_grouped_clifford_linear(None, 1, None, 2, None, None, None, 1, 1, 1, 1, None, 1, 0, None) == -1
     assert b"scales" in L.ygg_last_error()
+    # Pauli products: odd d_in, unknown layouts, Pauli rows in fp32 are rejected before any launch
+    assert L.ygg_pauli_grouped_linear(None, 0, None, 4, None, None, None, 1, 3, 4, 0, None, 1, 1, None) == -1
+    assert b"even" in L.ygg_last_error()
+    assert L.ygg_pauli_grouped_linear(None, 5, None, 4, None, None, None, 1, 2, 4, 0, None, 1, 1, None) == -1
+    assert b"x layout" in L.ygg_last_error()
+    assert L.ygg_pauli_grouped_linear(None, 1, None, 4, None, None, None, 1, 2, 4, 0, None, 0, 0, None) == -1
+    assert b"dtype" in L.ygg_last_error()
+    assert L.ygg_prepared_weight_bytes(2, 4, 3, 3) == 0  # odd d_in has no Pauli layout
+    assert L.ygg_prepared_weight_bytes(2, 4, 6, 3) == 2 * 4 * 6 * 16
 
 
 def test_config_validation():
@@ -81,7 +90,10 @@ def test_config_validation():
 
     c = MoEHLMConfig(d_model=8, d_ff=16)
     assert c.weight_format == "f32"
-    assert MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.bfloat16).weight_format == "bf16"
+    assert MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.bfloat16).weight_format == "pauli"
+    assert MoEHLMConfig(d_model=7, d_ff=16, dtype=torch.bfloat16).weight_format == "bf16"
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=7, d_ff=16, dtype=torch.bfloat16, weight_format="pauli")
     with pytest.raises(ValueError):
         MoEHLMConfig(d_model=8, d_ff=16, activation="swish")
     with pytest.raises(ValueError):

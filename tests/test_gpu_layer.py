@@ -73,12 +73,12 @@ def test_grouped_clifford_linear(fmt, act, d_in, d_out, E, P):
         assert normwise_err(y[rows], ref) < tol, e
 
 
-def _run_layer_case(name):
+def _run_layer_case(name, fmt_override=None):
     yggdrasil_amd, ops = _mods()
     p, inp, ref = load_case(name)
     bf16 = bool(p.get("bf16"))
     dt = torch.bfloat16 if bf16 else torch.float32
-    fmt = "int8" if p.get("int8") else ("bf16" if bf16 else "f32")
+    fmt = fmt_override or ("int8" if p.get("int8") else ("bf16" if bf16 else "f32"))
     router = {None: "energy", "clifford_head": "clifford_head"}.get(p.get("logits"), "logits")
     cfg = yggdrasil_amd.MoEHLMConfig(d_model=p["d"], d_ff=p["F"], n_experts=p["E"], top_k=p["k"],
                                      activation=p["act"], dtype=dt, weight_format=fmt, router=router)
@@ -108,6 +108,12 @@ def _run_layer_case(name):
 @pytest.mark.parametrize("name", LAYER_CASES)
 def test_layer_against_reference_golden(name):
     _run_layer_case(name)
+
+
+@pytest.mark.parametrize("name", ["c3_small", "c5_small"])
+def test_layer_pauli_weights_against_reference_golden(name):
+    """The bf16 goldens again, with the expert products on Pauli (complex 2x2) weights."""
+    _run_layer_case(name, fmt_override="pauli")
 
 
 def test_geoformer_interface_flat_input():
@@ -169,10 +175,11 @@ def _sampled_layer_check(N, d, F, E, k, fmt, logits, seed, n_sample=12):
     return max(errs)
 
 
-def test_full_c3_prefill_bf16_sampled():
+@pytest.mark.parametrize("fmt", ["bf16", "pauli"])
+def test_full_c3_prefill_bf16_sampled(fmt):
     g = np.random.default_rng(303)
     logits = _inputs.zipf_logits(g, 8192, 32, 4)
-    _sampled_layer_check(8192, 128, 512, 32, 4, "bf16", logits, 33)
+    _sampled_layer_check(8192, 128, 512, 32, 4, fmt, logits, 33)
 
 
 def test_full_c4_decode_int8_sampled():

@@ -1,0 +1,189 @@
+"""GPU parity: the Pauli (complex 2x2) grouped CliffordLinear against the oracle.
+
+The kernel rounds its operands to bf16 in Pauli coordinates.  Each product is
+pinned three ways:
+
+* the linear part (``act='none'``, fp32 output) against the oracle run on the
+  operands rounded exactly as the kernel rounds them (``pauli_round``), to 1e-4
+  normwise -- this leaves only the fp32 summation order;
+* the fused activation against the oracle's activation applied to the
+  kernel's own pre-activation output, to 2e-5 normwise;
+* the whole product against the oracle on the exact fp32 weights, to the
+  bf16 bound (the sigmoid's magnitude gate is excluded there: for vectors of
+  small norm it amplifies any rounding of the direction).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import _inputs
+from _gpu_helpers import TOL_BF16, normwise_err, say
+from oracle import moe
+
+pytestmark = pytest.mark.gpu
+
+TOL_LINEAR_SAME_OPERANDS = 1e-4
+TOL_EPILOGUE = 2e-5
+TOL_BF16_LINEAR = 1e-2
+
+
+def _ops():
+    from yggdrasil_amd import ops
+
+    return ops
+
+
+def _bf16(a):
+    return _inputs.bf16_round(np.asarray(a, np.float32))
+
+
+def pauli_round(x, scale=1.0):
+    """Blade fp32 -> Pauli coordinates (fp32 sums) -> bf16 -> back to blade (exact).
+
+    ``scale`` = 0.5 reproduces the prepared weights, which hold W/2 (a power of
+    two: it does not change the rounding).
+    """
+    x = np.asarray(x, np.float32) * np.float32(scale)
+    s, v1, v2, v3, b12, b13, b23, t = [x[..., i] for i in range(8)]
+    P = [s + v3, t + b12, v1 + b13, b23 + v2, v1 - b13, b23 - v2, s - v3, t - b12]
+    m00r, m00i, m10r, m10i, m01r, m01i, m11r, m11i = [_bf16(p).astype(np.float64) for p in P]
+    out = np.stack([(m00r + m11r) / 2, (m10r + m01r) / 2, (m10i - m01i) / 2, (m00r - m11r) / 2,
+                    (m00i - m11i) / 2, (m10r - m01r) / 2, (m10i + m01i) / 2, (m00i + m11i) / 2], -1)
+    return (out / scale).astype(np.float32)
+
+
+def _offsets(g, E, P, empty_first=True):
+    counts = np.bincount(g.integers(0, E, P), minlength=E)
+    if empty_first and E > 2:
+        counts[-1] += counts[0]
+        counts[0] = 0
+    counts[-1] += P - counts.sum()
+    return np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+
+
+def _per_expert(offsets, fn):
+    errs = []
+    for e in range(len(offsets) - 1):
+        rows = slice(offsets[e], offsets[e + 1])
+        if offsets[e] < offsets[e + 1]:
+            errs.append(fn(e, rows))
+    return max(errs)
+
+
+@pytest.mark.parametrize("act,d_in,d_out,E,P,N,x_layout", [
+    ("none", 16, 64, 4, 200, 90, "blade"), ("gelu", 128, 512, 3, 300, 120, "pauli"),
+    ("sigmoid", 10, 40, 5, 77, 77, "blade"), ("relu", 2, 6, 2, 33, 20, "pauli"),
+    ("gelu", 64, 130, 2, 129, 64, "blade"), ("none", 512, 128, 4, 260, 100, "pauli"),
+    ("gelu", 128, 512, 32, 3000, 1000, "pauli")])
+def test_pauli_product(act, d_in, d_out, E, P, N, x_layout):
+    ops = _ops()
+    g = np.random.default_rng(d_in * 13 + d_out + E)
+    W = (g.standard_normal((E, d_out, d_in, 8), dtype=np.float32) / np.sqrt(8 * d_in)).astype(np.float32)
+    b = (0.3 * g.standard_normal((E, d_out, 8))).astype(np.float32)
+    x = _bf16(g.standard_normal((N, d_in, 8), dtype=np.float32))
+    gather = g.integers(0, N, P).astype(np.int32)
+    offsets = _offsets(g, E, P)
+    say(f"pauli product act={act} d_in={d_in} d_out={d_out} E={E} P={P} N={N} x={x_layout}")
+    pw = ops.prepare_weights(torch.from_numpy(W).cuda(), "pauli")
+    pb = ops.prepare_bias(torch.from_numpy(b).cuda())
+    xt = torch.from_numpy(x).cuda().bfloat16()
+    if x_layout == "pauli":
+        xt = ops.pauli_rows_from_blade(xt)
+    off = torch.from_numpy(offsets).cuda()
+    gt = torch.from_numpy(gather).cuda()
+
+    def run(a, y_layout="blade"):
+        return ops.pauli_grouped_linear(xt, pw, off, pb, a, x_layout=x_layout, gather=gt, y_layout=y_layout,
+                                        out_dtype=torch.float32)
+
+    pre = run("none").cpu().numpy()
+    xr, Wr = pauli_round(x), pauli_round(W, 0.5)
+    err = _per_expert(offsets, lambda e, rows: normwise_err(pre[rows], moe.clifford_linear(xr[gather[rows]], Wr[e], b[e])))
+    assert err < TOL_LINEAR_SAME_OPERANDS, err
+    y = run(act).cpu().numpy() if act != "none" else pre
+    assert normwise_err(y, moe.ACTIVATIONS[act](pre)) < TOL_EPILOGUE
+    if act != "sigmoid":
+        err = _per_expert(offsets, lambda e, rows: normwise_err(
+            y[rows], moe.ACTIVATIONS[act](moe.clifford_linear(x[gather[rows]], W[e], b[e]))))
+        assert err < TOL_BF16_LINEAR, err
+    if d_out % 2 == 0:
+        # the Pauli half-row output holds the same values, rounded to bf16
+        yp = run(act, "pauli")
+        back = ops.pauli_grouped_linear(yp, ops.prepare_weights(_identity_weights(d_out), "pauli"),
+                                        torch.tensor([0, P], device="cuda", dtype=torch.int32), None, "none",
+                                        x_layout="pauli", y_layout="blade", out_dtype=torch.float32)
+        assert normwise_err(back.cpu().numpy(), y) < 8e-3
+
+
+def _identity_weights(d):
+    w = torch.zeros(1, d, d, 8)
+    w[0, torch.arange(d), torch.arange(d), 0] = 1.0
+    return w.cuda()
+
+
+def test_pauli_rows_roundtrip_exact_for_representable_values():
+    """Blade -> Pauli is exact when every pairwise sum is a bf16 value (small integers)."""
+    ops = _ops()
+    g = np.random.default_rng(3)
+    x = g.integers(-8, 9, size=(37, 6, 8)).astype(np.float32)
+    say("pauli rows roundtrip")
+    xp = ops.pauli_rows_from_blade(torch.from_numpy(x).cuda().bfloat16()).float().cpu().numpy()
+    s, v1, v2, v3, b12, b13, b23, t = [x[..., i] for i in range(8)]
+    col0 = np.stack([s + v3, t + b12, v1 + b13, b23 + v2], -1)
+    col1 = np.stack([v1 - b13, b23 - v2, s - v3, t - b12], -1)
+    assert np.array_equal(xp[:, 0], col0) and np.array_equal(xp[:, 1], col1)
+
+
+def test_pauli_small_integer_product_is_exact():
+    """Integer operands whose Pauli coordinates and sums stay exact in bf16/fp32 give exact results."""
+    ops = _ops()
+    g = np.random.default_rng(4)
+    E, d_in, d_out, P = 2, 8, 6, 40
+    W = g.integers(-2, 3, size=(E, d_out, d_in, 8)).astype(np.float32)
+    x = g.integers(-2, 3, size=(P, d_in, 8)).astype(np.float32)
+    offsets = np.array([0, 17, P], np.int32)
+    say("pauli integer product")
+    y = ops.pauli_grouped_linear(torch.from_numpy(x).cuda().bfloat16(), ops.prepare_weights(torch.from_numpy(W).cuda(),
+                                 "pauli"), torch.from_numpy(offsets).cuda(), None, "none", x_layout="blade",
+                                 y_layout="blade", out_dtype=torch.float32).cpu().numpy()
+    for e in range(E):
+        rows = slice(offsets[e], offsets[e + 1])
+        assert np.array_equal(y[rows], moe.clifford_linear(x[rows], W[e], None))
+
+
+def test_pauli_rejects_bad_arguments():
+    ops = _ops()
+    with pytest.raises(ValueError):
+        ops.prepare_weights(torch.zeros(1, 4, 3, 8, device="cuda"), "pauli")
+    L = ops.lib()
+    assert L.ygg_pauli_grouped_linear(None, 0, None, 4, None, None, None, 65, 4, 4, 0, None, 1, 1, None) == -1
+    assert b"E <= 64" in L.ygg_last_error()
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "pauli"])
+def test_layer_formats_against_oracle(fmt):
+    """Whole layer with 'pauli' and with 'bf16' (8x8 L(w) blocks) weights against the oracle on exact weights."""
+    import yggdrasil_amd
+
+    g = np.random.default_rng(12)
+    N, d, F, E, k = 500, 32, 96, 6, 2
+    x = _bf16(g.standard_normal((1, N, d, 8), dtype=np.float32))
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F, bias_std=0.2)
+    logits_np = g.standard_normal((N, E), dtype=np.float32)
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, dtype=torch.bfloat16,
+                                     weight_format=fmt, router="logits")
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    say(f"layer fmt={fmt} N={N} d={d} F={F} E={E} k={k}")
+    out = layer.moe_forward(torch.from_numpy(x).cuda().bfloat16(), logits=torch.from_numpy(logits_np).cuda())
+    out = out.float().cpu().numpy().reshape(N, d, 8)
+    idx = layer.last_routing["topk_idx"].cpu().numpy()
+    idx_o, w = moe.route_topk(moe.softmax(logits_np), k)
+    assert np.array_equal(idx, idx_o)
+    ref = np.zeros((N, d, 8), np.float32)
+    for t in range(N):
+        for s in np.argsort(idx[t]):
+            e = idx[t, s]
+            ref[t] += w[t, s] * moe.clifford_ffn(x[0, t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+    assert normwise_err(out, ref) < TOL_BF16

@@ -53,6 +53,9 @@ extern "C" int ygg_combine(const void*, int, int, int, int, int, const int32_t*,
                            const void*, void*, int, hipStream_t);
 extern "C" int ygg_grouped_clifford_linear(const void*, int, const void*, int, const float*, const float*,
                                            const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
+extern "C" int ygg_pauli_grouped_linear(const void*, int, const int32_t*, int, const void*, const float*,
+                                        const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
+extern "C" int ygg_pauli_rows_from_blade(const void*, int, int, void*, hipStream_t);
 
 YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype) {
   const size_t P = (size_t)N * k;
@@ -74,8 +77,10 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
                             float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
                             size_t workspace_bytes, hipStream_t stream) {
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
-  YGG_CHECK_ARG(dtype == kF32 ? w_format == 0 : (w_format == 1 || w_format == 2),
+  YGG_CHECK_ARG(dtype == kF32 ? w_format == kWF32 : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
                 "ygg_moe_forward: weight format %d does not match dtype %d", w_format, dtype);
+  YGG_CHECK_ARG(w_format != kWPauli || (d % 2 == 0 && F % 2 == 0),
+                "ygg_moe_forward: the Pauli weight format needs even d and F (d=%d F=%d)", d, F);
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype),
                 "ygg_moe_forward: workspace of %zu bytes, need %zu", workspace_bytes,
                 ygg_moe_workspace_bytes(N, d, F, E, k, dtype));
@@ -104,6 +109,19 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
     logits = lg;
   }
   if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
+  if (w_format == kWPauli) {
+    // x -> Pauli half-rows once (in the x_sorted region: N <= P rows); up: gather those
+    // rows through perm inside the product -> h in Pauli half-rows; down: h -> y_sorted
+    // in blade order.  No expert-grouped copy of x is made.
+    if (ygg_pauli_rows_from_blade(x, N, d, xs, stream)) return -1;
+    if (ygg_pauli_grouped_linear(xs, /*Pauli rows*/ 1, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h,
+                                 /*Pauli rows*/ 0, kBF16, stream))
+      return -1;
+    if (ygg_pauli_grouped_linear(h, /*Pauli rows*/ 1, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, ys,
+                                 /*blade*/ 1, kBF16, stream))
+      return -1;
+    return ygg_combine(ys, kBF16, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
+  }
   if (ygg_dispatch(x, dtype, N, k, d, slot_pos, xs, /*to_mask_order=*/1, stream)) return -1;
   if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
                                   /*blade=*/0, stream))

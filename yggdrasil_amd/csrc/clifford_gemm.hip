@@ -36,8 +36,6 @@ namespace ygg {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2 };
-
 // ---------------------------------------------------------------------------
 // activations (mask order: grade = popcount of the component index)
 // ---------------------------------------------------------------------------
@@ -430,16 +428,18 @@ YGG_API size_t ygg_prepared_weight_bytes(int E, int d_out, int d_in, int format)
     case kWF32: return (size_t)E * d_out * d_in * 8 * 4;
     case kWBF16: return (size_t)E * JB * IP * 64 * 16 * 2;
     case kWI8: return (size_t)E * JB * IP * 64 * 8;
+    case kWPauli: return (d_in % 2) ? 0 : (size_t)E * d_out * d_in * 8 * 2;
     default: return 0;
   }
 }
 
 YGG_API int ygg_prepare_weights(const float* W, int E, int d_out, int d_in, int format, void* out, float* scales,
                                 hipStream_t stream) {
-  YGG_CHECK_ARG(format == kWF32 || format == kWBF16 || format == kWI8, "ygg_prepare_weights: format %d", format);
+  YGG_CHECK_ARG(format >= kWF32 && format <= kWPauli, "ygg_prepare_weights: format %d", format);
   YGG_CHECK_ARG(E >= 1 && d_out >= 1 && d_in >= 1, "ygg_prepare_weights: bad sizes E=%d d_out=%d d_in=%d", E, d_out,
                 d_in);
   YGG_CHECK_ARG(W && out, "ygg_prepare_weights: null pointer");
+  if (format == kWPauli) return pauli_prepare_weights(W, E, d_out, d_in, out, stream);
   YGG_CHECK_ARG(format != kWI8 || scales, "ygg_prepare_weights: int8 format needs a scales buffer [E, d_out]");
   if (format == kWI8) {
     quant_scale_kernel<<<E * d_out, 256, 0, stream>>>(W, d_in, scales);

@@ -1,0 +1,631 @@
+// pauli_gemm.hip -- grouped CliffordLinear expert products as complex GEMMs
+// on the bf16 MFMA units of gfx950.
+//
+// Replaces, for every expert e of the MoE-HLM layer, CliffordLinear.forward
+// (holograph/layers/clifford_linear.py:101-123), i.e. geom_matmul
+// (rune/ops/batched.py:320-344) on that expert's rows, and the grade-wise
+// activation (holograph/layers/activations.py:15-128) after the up projection.
+//
+// Algebra
+// -------
+// Cl(3,0) is isomorphic to the 2x2 complex matrices (Pauli representation):
+//   e1 -> sx, e2 -> sy, e3 -> sz, e12 -> i sz, e13 -> -i sy, e23 -> i sx, e123 -> i I.
+// A multivector  s + v1 e1 + v2 e2 + v3 e3 + b12 e12 + b13 e13 + b23 e23 + t e123
+// maps to
+//   M00 = (s + v3) + i (t + b12)     M01 = (v1 - b13) + i (b23 - v2)
+//   M10 = (v1 + b13) + i (b23 + v2)  M11 = (s - v3) + i (t - b12)
+// and the geometric product maps to the matrix product.  A CliffordLinear
+//   y[m, j] = sum_i W[j, i] x[m, i]
+// is therefore the complex contraction  Y_mj[a, b] = sum_{i, c} W_ji[a, c] X_mi[c, b]:
+// rows (m, b), contraction (i, c), columns (j, a) -- 32 real multiply-adds per
+// (input, output) multivector pair instead of the 64 of the 8x8 block L(w).
+//
+// Layouts
+// -------
+// * Pauli half-rows ("PH"): a row of d multivectors is stored as two halves,
+//   b = 0 then b = 1; half b holds, for every multivector i, column b of its
+//   matrix as 4 reals (c0 re, c0 im, c1 re, c1 im).  Row (m, b) of the GEMM is
+//   then one contiguous run of 4 d values.
+// * Prepared weights ("PW", bf16): per (expert, j, input pair p = i/2), 32
+//   bytes: [a = 0 | a = 1] x [i = 2p | 2p + 1] x [c0 | c1] x (u, -v), where
+//   u + iv = W_ji[a, c] / 2.  The 1/2 makes the inverse map a plain sum.
+//   (u, -v) is the B operand of the real part; the imaginary part uses the
+//   A operand rotated within each complex pair, (re, im) -> (im, -re).
+//
+// Work decomposition
+// ------------------
+// v_mfma_f32_32x32x16_bf16: one K step is 4 input multivectors.  A wave owns
+// WR x 16 tokens (WR row blocks of 32 GEMM rows) and WC x 32 output
+// multivectors, with four accumulators per block pair (a = 0, 1) x (re, im),
+// so all 8 reals of an output multivector land in one lane: the inverse map,
+// bias, grade-wise activation and the output layout are fused into the
+// epilogue with no shuffles.
+//
+// The launch is persistent: one workgroup per CU walks a flat stream of
+// (tile, K chunk) steps.  Tiles are (row tile of one expert) x (column tile);
+// row tiles never straddle experts (device-side offsets, no host sync).  The
+// tile list is cut into one contiguous range per XCD (workgroup b runs on XCD
+// b mod 8), so the workgroups sharing an L2 work on neighbouring row tiles of
+// the same expert.  Each step stages KC input multivectors of the activation
+// and weight tiles in LDS (double buffered, one barrier per step); the raw
+// buffer loads of step f + 1 are issued before step f computes, so the next
+// tile's first loads are in flight during the current tile's epilogue.
+// Activation rows are gathered through the expert-grouped row index, which
+// fuses the dispatch copy into the up projection.
+
+#include "ygg_common.h"
+
+namespace ygg {
+
+typedef __bf16 pbf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 pbf16x2_t __attribute__((ext_vector_type(2)));
+typedef float pf32x2_t __attribute__((ext_vector_type(2)));
+typedef float pf32x16_t __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// activations in blade coordinates (hardware exp2 / rcp / sqrt)
+// ---------------------------------------------------------------------------
+// sigma(z) = 1 / (1 + e^-z).  tanh-GELU:  0.5 v (1 + tanh(u)) = v sigma(2u),
+// u = sqrt(2/pi) (v + 0.044715 v^3); the magnitude gate (c / |c|) gelu(|c|)
+// is  c sigma(2 u(|c|)); tanh(t) = 2 sigma(2t) - 1.
+__device__ inline float fsigmoid(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));
+}
+__device__ inline float gelu_gate(float v) {  // gelu(v) / v
+  const float k2 = 2.0f * 0.7978845608028654f;
+  return fsigmoid(k2 * (v + 0.044715f * v * v * v));
+}
+__device__ inline float ftanh(float t) { return 2.0f * fsigmoid(2.0f * t) - 1.0f; }
+
+// y: blade order 1,e1,e2,e3,e12,e13,e23,e123
+template <int ACT>
+__device__ inline void activate_blade(float* y) {
+  if constexpr (ACT == kActNone) {
+    return;
+  } else {
+    const float m1 = __builtin_amdgcn_sqrtf(y[1] * y[1] + y[2] * y[2] + y[3] * y[3] + 1e-12f);
+    const float m2 = __builtin_amdgcn_sqrtf(y[4] * y[4] + y[5] * y[5] + y[6] * y[6] + 1e-12f);
+    float f0, f1, f2;
+    if constexpr (ACT == kActGelu) {
+      f0 = gelu_gate(y[0]);
+      f1 = gelu_gate(m1);
+      f2 = gelu_gate(m2);
+      y[7] = ftanh(y[7]);
+    } else if constexpr (ACT == kActSigmoid) {
+      y[0] = fsigmoid(y[0]);
+      f0 = 1.0f;
+      f1 = fsigmoid(m1) * __builtin_amdgcn_rcpf(m1);
+      f2 = fsigmoid(m2) * __builtin_amdgcn_rcpf(m2);
+      y[7] = ftanh(y[7]);
+    } else {  // relu with zero thresholds: grade 0 clamps, the rest pass through
+      f0 = y[0] > 0.f ? 1.0f : 0.0f;
+      f1 = 1.0f;
+      f2 = 1.0f;
+    }
+    y[0] *= f0;
+    y[1] *= f1;
+    y[2] *= f1;
+    y[3] *= f1;
+    y[4] *= f2;
+    y[5] *= f2;
+    y[6] *= f2;
+  }
+}
+
+// blade -> Pauli columns: col0 = (M00, M10), col1 = (M01, M11), (re, im) each
+__device__ inline void blade_to_pauli(const float* x, float* c0, float* c1) {
+  c0[0] = x[0] + x[3];  // M00 re = s + v3
+  c0[1] = x[7] + x[4];  // M00 im = t + b12
+  c0[2] = x[1] + x[5];  // M10 re = v1 + b13
+  c0[3] = x[6] + x[2];  // M10 im = b23 + v2
+  c1[0] = x[1] - x[5];  // M01 re = v1 - b13
+  c1[1] = x[6] - x[2];  // M01 im = b23 - v2
+  c1[2] = x[0] - x[3];  // M11 re = s - v3
+  c1[3] = x[7] - x[4];  // M11 im = t - b12
+}
+
+// Pauli (already halved by the weights) -> blade.  y00 = (re, im) of Y[0][0], ...
+__device__ inline void pauli_to_blade(float y00r, float y00i, float y01r, float y01i, float y10r, float y10i,
+                                      float y11r, float y11i, float* x) {
+  x[0] = y00r + y11r;  // s
+  x[3] = y00r - y11r;  // v3
+  x[7] = y00i + y11i;  // t
+  x[4] = y00i - y11i;  // b12
+  x[1] = y10r + y01r;  // v1
+  x[5] = y10r - y01r;  // b13
+  x[6] = y10i + y01i;  // b23
+  x[2] = y10i - y01i;  // v2
+}
+
+// two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even)
+__device__ inline uint32_t pack2_bf16(float lo, float hi) {
+  const pf32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, pbf16x2_t));
+}
+__device__ inline float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ inline float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+// (re, im) -> (im, -re) on each bf16 pair of a dword
+__device__ inline uint32_t rot_conj(uint32_t w) { return __builtin_amdgcn_alignbit(w, w, 16) ^ 0x80000000u; }
+
+enum PauliIn : int { kInBladeGather = 0, kInPauliRows = 1 };
+enum PauliOut : int { kOutPauliRows = 0, kOutBlade = 1 };
+
+constexpr int kPauliMaxExperts = 64;
+// buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format)
+constexpr int kBufferFlags = 0x00020000;
+
+template <int WR_, int WC_, int BWT_, int BWJ_, int KC_>
+struct PauliTile {
+  static constexpr int WR = WR_, WC = WC_, BWT = BWT_, BWJ = BWJ_, KC = KC_;
+  static constexpr int NT = 64 * BWT * BWJ;       // threads
+  static constexpr int T = BWT * WR * 16;         // tokens per tile
+  static constexpr int BN = BWJ * WC * 32;        // output multivectors per tile
+  static constexpr int A_STRIDE = KC * 8 + 16;    // bytes per LDS row (m, b): KC mv x 4 bf16, +16 pad
+  static constexpr int W_STRIDE = KC * 16 + 16;   // bytes per LDS column j: KC/2 pairs x 32 B, +16 pad
+  static constexpr int A_BYTES = 2 * T * A_STRIDE;
+  static constexpr int W_BYTES = BN * W_STRIDE;
+  static constexpr int STAGE = A_BYTES + W_BYTES;
+  // 16-byte global pieces per stage
+  static constexpr int A_ITEMS_GATHER = T * KC;   // one blade multivector each
+  static constexpr int A_ITEMS_ROWS = T * KC;     // 2T rows x KC/2 pairs
+  static constexpr int W_ITEMS = BN * KC;         // BN columns x KC/2 pairs x (a = 0, 1)
+  static constexpr int A_PER = A_ITEMS_ROWS / NT, W_PER = W_ITEMS / NT;
+  static_assert(KC % 4 == 0, "KC must be a multiple of the MFMA K step (4 multivectors)");
+  static_assert(A_ITEMS_ROWS % NT == 0 && W_ITEMS % NT == 0, "staging split");
+};
+
+struct PauliTileInfo {
+  int e, row0, row_end, col0;
+};
+
+template <int ACT, int IN, int OUT, int OUT_DT, class TL>
+__global__ __launch_bounds__(TL::NT) void pauli_gemm_kernel(
+    const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
+    const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
+    void* __restrict__ Y, int n_xcd) {
+  constexpr int NT = TL::NT, T = TL::T, BN = TL::BN, KC = TL::KC, WR = TL::WR, WC = TL::WC, BWT = TL::BWT;
+  constexpr int A_PER = TL::A_PER, W_PER = TL::W_PER;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TL::STAGE];
+  __shared__ int s_off[kPauliMaxExperts + 1];   // expert row offsets
+  __shared__ int s_tbeg[kPauliMaxExperts + 1];  // first row tile of each expert
+
+  const int tid = threadIdx.x;
+  for (int i = tid; i <= E; i += NT) s_off[i] = offsets[i];
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int x = 0; x < E; ++x) {
+      s_tbeg[x] = acc;
+      acc += (s_off[x + 1] - s_off[x] + T - 1) / T;
+    }
+    s_tbeg[E] = acc;
+  }
+  __syncthreads();
+
+  const int CT = (d_out + BN - 1) / BN;
+  const int n_tiles = s_tbeg[E] * CT;
+  const int nk = (d_in + KC - 1) / KC;
+  // this workgroup's tiles: XCD x gets the contiguous range [lo, hi), its
+  // workgroups take every per_xcd-th tile of it
+  const int per_xcd = gridDim.x / n_xcd;
+  const int xcd = blockIdx.x % n_xcd, slot = blockIdx.x / n_xcd;
+  const int lo = (int)((long long)n_tiles * xcd / n_xcd), hi = (int)((long long)n_tiles * (xcd + 1) / n_xcd);
+  const int n_mine = (hi - lo > slot) ? (hi - lo - slot + per_xcd - 1) / per_xcd : 0;
+  const int total = n_mine * nk;
+
+  auto decode = [&](int n) {  // n-th tile of this workgroup
+    const int L = lo + slot + n * per_xcd;
+    const int rt = L / CT, ct = L - rt * CT;
+    int a = 0, b = E - 1;  // last expert with s_tbeg <= rt (experts with no tiles are skipped)
+    while (a < b) {
+      const int m = (a + b + 1) >> 1;
+      if (s_tbeg[m] <= rt) a = m;
+      else b = m - 1;
+    }
+    PauliTileInfo t;
+    t.e = a;
+    t.row0 = s_off[a] + (rt - s_tbeg[a]) * T;
+    t.row_end = s_off[a + 1];
+    t.col0 = ct * BN;
+    return t;
+  };
+
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wt = wave % BWT, wj = wave / BWT;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int IP = d_in >> 1;  // input pairs (d_in even)
+
+  // ---- staging: global -> registers -> LDS --------------------------------
+  // Staging loads are raw buffer loads: an offset past the end of the
+  // descriptor's range reads zero, so the K tail and out-of-range columns
+  // need no branches.  Row offsets are 32-bit (operands below 2 GiB).
+  const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0,
+                                                                          0x7fffffff, kBufferFlags);
+  constexpr uint32_t kOff = 0x80000000u;  // reads zero
+  PauliTileInfo ld = {0, 0, 1, 0};  // tile of the chunk being loaded
+  __amdgpu_buffer_rsrc_t w_rsrc = x_rsrc;
+  uint32_t a_row[A_PER];  // byte offset of each staged A item's row, fixed for a tile
+  auto load_chunk = [&](int f, uint4 (&ra)[A_PER], uint4 (&rw)[W_PER]) {
+    const int kc = f % nk;
+    if (kc == 0) {
+      ld = decode(f / nk);
+      w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Wp) + (size_t)ld.e * d_out * IP * 16, (short)0,
+                                                 (uint32_t)d_out * IP * 32, kBufferFlags);
+#pragma unroll
+      for (int u = 0; u < A_PER; ++u) {
+        const int item = tid + u * NT;
+        const int tl = (IN == kInBladeGather) ? item / KC : (item / (KC / 2)) >> 1;
+        int r = ld.row0 + tl;
+        r = r < ld.row_end ? r : ld.row_end - 1;
+        const int src = gather ? gather[r] : r;
+        if constexpr (IN == kInBladeGather)
+          a_row[u] = (uint32_t)src * d_in * 16;
+        else
+          a_row[u] = (uint32_t)(2 * src + ((item / (KC / 2)) & 1)) * d_in * 8;
+      }
+    }
+    const int i0 = kc * KC;
+#pragma unroll
+    for (int u = 0; u < W_PER; ++u) {
+      const int item = tid + u * NT;
+      const int jl = item / KC, q = item % KC;  // q: pair (q / 2), a (q % 2)
+      const int j = ld.col0 + jl;               // j >= d_out lies past the expert's range: zero
+      const int p = (i0 >> 1) + (q >> 1);
+      const uint32_t off = (p < IP) ? ((uint32_t)(j * IP + p) * 2 + (q & 1)) * 16 : kOff;
+      rw[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off, 0, 0));
+    }
+#pragma unroll
+    for (int u = 0; u < A_PER; ++u) {
+      const int item = tid + u * NT;
+      uint32_t off;
+      if constexpr (IN == kInBladeGather) {
+        const int i = i0 + item % KC;
+        off = (i < d_in) ? a_row[u] + (uint32_t)i * 16 : kOff;
+      } else {
+        const int p = (i0 >> 1) + item % (KC / 2);  // 16-byte piece = one input pair
+        off = (p < IP) ? a_row[u] + (uint32_t)p * 16 : kOff;
+      }
+      ra[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, off, 0, 0));
+    }
+  };
+  auto store_chunk = [&](int buf, const uint4 (&ra)[A_PER], const uint4 (&rw)[W_PER]) {
+    unsigned char* As = smem + buf * TL::STAGE;
+    unsigned char* Ws = As + TL::A_BYTES;
+#pragma unroll
+    for (int u = 0; u < A_PER; ++u) {
+      const int item = tid + u * NT;
+      if constexpr (IN == kInBladeGather) {
+        const int tl = item / KC, il = item % KC;
+        const uint4 q = ra[u];
+        const float x[8] = {bf_lo(q.x), bf_hi(q.x), bf_lo(q.y), bf_hi(q.y),
+                            bf_lo(q.z), bf_hi(q.z), bf_lo(q.w), bf_hi(q.w)};
+        float c0[4], c1[4];
+        blade_to_pauli(x, c0, c1);
+        *reinterpret_cast<uint2*>(As + (2 * tl) * TL::A_STRIDE + il * 8) =
+            make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+        *reinterpret_cast<uint2*>(As + (2 * tl + 1) * TL::A_STRIDE + il * 8) =
+            make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+      } else {
+        const int rl = item / (KC / 2), q = item % (KC / 2);
+        *reinterpret_cast<uint4*>(As + rl * TL::A_STRIDE + q * 16) = ra[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < W_PER; ++u) {
+      const int item = tid + u * NT;
+      const int jl = item / KC, q = item % KC;
+      *reinterpret_cast<uint4*>(Ws + jl * TL::W_STRIDE + q * 16) = rw[u];
+    }
+  };
+
+  pf32x16_t acc[WR][WC][2][2];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int a = 0; a < WR; ++a)
+#pragma unroll
+      for (int b = 0; b < WC; ++b)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][c][d][v] = 0.f;
+  };
+
+  auto compute_chunk = [&](int buf) {
+    const unsigned char* As = smem + buf * TL::STAGE;
+    const unsigned char* Ws = As + TL::A_BYTES;
+#pragma unroll
+    for (int s = 0; s < KC / 4; ++s) {
+      uint4 av[WR], wv[WC][2];
+#pragma unroll
+      for (int rb = 0; rb < WR; ++rb) {
+        const int row = (wt * WR + rb) * 32 + l32;
+        av[rb] = *reinterpret_cast<const uint4*>(As + row * TL::A_STRIDE + (4 * s + 2 * g) * 8);
+      }
+#pragma unroll
+      for (int cb = 0; cb < WC; ++cb) {
+        const int col = (wj * WC + cb) * 32 + l32;
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+          wv[cb][a] = *reinterpret_cast<const uint4*>(Ws + col * TL::W_STRIDE + (2 * s + g) * 32 + a * 16);
+      }
+#pragma unroll
+      for (int rb = 0; rb < WR; ++rb) {
+        const uint4 ap = make_uint4(rot_conj(av[rb].x), rot_conj(av[rb].y), rot_conj(av[rb].z), rot_conj(av[rb].w));
+        const pbf16x8_t A0 = __builtin_bit_cast(pbf16x8_t, av[rb]);
+        const pbf16x8_t A1 = __builtin_bit_cast(pbf16x8_t, ap);
+#pragma unroll
+        for (int cb = 0; cb < WC; ++cb)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            const pbf16x8_t B = __builtin_bit_cast(pbf16x8_t, wv[cb][a]);
+            acc[rb][cb][a][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A0, B, acc[rb][cb][a][0], 0, 0, 0);
+            acc[rb][cb][a][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, B, acc[rb][cb][a][1], 0, 0, 0);
+          }
+      }
+    }
+  };
+
+  // Bias of the tile being computed, loaded when its first chunk is computed
+  // (raw buffer loads: a null bias is an empty range and reads zero).
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(bias), (short)0, bias ? (uint32_t)E * d_out * 32 : 0u, kBufferFlags);
+  float bvs[WC][8];
+  auto load_bias = [&](const PauliTileInfo& ti) {
+#pragma unroll
+    for (int cb = 0; cb < WC; ++cb) {
+      const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
+      const uint32_t off = (j < d_out) ? (uint32_t)(ti.e * d_out + j) * 32 : kOff;
+      const uint4 lo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, off, 0, 0));
+      const uint4 hi = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, off + 16, 0, 0));
+      const uint32_t m[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};  // mask order
+#pragma unroll
+      for (int c = 0; c < 8; ++c) bvs[cb][c] = __builtin_bit_cast(float, m[blade_to_mask(c)]);
+    }
+  };
+
+  auto epilogue = [&](const PauliTileInfo& ti) {
+#pragma unroll
+    for (int cb = 0; cb < WC; ++cb) {
+      const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
+      if (j >= d_out) continue;
+      const float* bv = bvs[cb];
+#pragma unroll
+      for (int rb = 0; rb < WR; ++rb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int t = (wt * WR + rb) * 16 + 4 * q + 2 * g + h;
+            const int row = ti.row0 + t;
+            if (row >= ti.row_end) continue;
+            const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
+            float y[8];
+            pauli_to_blade(acc[rb][cb][0][0][v0], acc[rb][cb][0][1][v0], acc[rb][cb][0][0][v0 + 1],
+                           acc[rb][cb][0][1][v0 + 1], acc[rb][cb][1][0][v0], acc[rb][cb][1][1][v0],
+                           acc[rb][cb][1][0][v0 + 1], acc[rb][cb][1][1][v0 + 1], y);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) y[c] += bv[c];
+            activate_blade<ACT>(y);
+            if constexpr (OUT == kOutPauliRows) {
+              float c0[4], c1[4];
+              blade_to_pauli(y, c0, c1);
+              uint16_t* Yh = static_cast<uint16_t*>(Y);
+              *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row) * d_out + j) * 4) =
+                  make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+              *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row + 1) * d_out + j) * 4) =
+                  make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+            } else if constexpr (OUT_DT == kBF16) {
+              uint4 o;
+              o.x = pack2_bf16(y[0], y[1]);
+              o.y = pack2_bf16(y[2], y[3]);
+              o.z = pack2_bf16(y[4], y[5]);
+              o.w = pack2_bf16(y[6], y[7]);
+              *reinterpret_cast<uint4*>(static_cast<uint16_t*>(Y) + ((size_t)row * d_out + j) * 8) = o;
+            } else {
+              float4* p = reinterpret_cast<float4*>(static_cast<float*>(Y) + ((size_t)row * d_out + j) * 8);
+              p[0] = make_float4(y[0], y[1], y[2], y[3]);
+              p[1] = make_float4(y[4], y[5], y[6], y[7]);
+            }
+          }
+      }
+    }
+  };
+
+  // ---- the stream of (tile, chunk) steps ------------------------------------
+  // chunk f lives in register set f % 2 and LDS buffer f % 2; step f loads
+  // chunk f + 2, computes chunk f, stores chunk f + 1, then one barrier.
+  uint4 ra[A_PER], rw[W_PER];
+  zero_acc();
+  if (total > 0) {
+    load_chunk(0, ra, rw);
+    store_chunk(0, ra, rw);
+  }
+  __syncthreads();
+  PauliTileInfo cur = {0, 0, 1, 0};  // tile being computed
+  for (int f = 0; f < total; ++f) {
+    const int buf = f & 1;
+    if (f % nk == 0) {
+      cur = decode(f / nk);
+      load_bias(cur);
+    }
+    if (f + 1 < total) load_chunk(f + 1, ra, rw);
+    compute_chunk(buf);
+    if (f % nk == nk - 1) {
+      epilogue(cur);
+      zero_acc();
+    }
+    if (f + 1 < total) store_chunk(buf ^ 1, ra, rw);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight preparation: (E, d_out, d_in, 8) fp32 blade -> PW bf16
+// ---------------------------------------------------------------------------
+// One thread per (e, j, i): writes the 2 x 8-byte halves (a = 0, 1) of its
+// multivector in the 32-byte record of its input pair.
+__global__ __launch_bounds__(256) void pauli_prep_weights_kernel(const float* __restrict__ W, int E, int d_out,
+                                                                 int d_in, uint16_t* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)E * d_out * d_in;
+  if (n >= total) return;
+  const int i = (int)(n % d_in);
+  const size_t ej = n / d_in;  // e * d_out + j
+  const float* w = W + n * 8;
+  float x[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) x[c] = 0.5f * w[c];
+  // Pauli entries W[a][c] = u + iv
+  float c0[4], c1[4];
+  blade_to_pauli(x, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
+  // a = 0: c = 0 -> M00, c = 1 -> M01;  a = 1: c = 0 -> M10, c = 1 -> M11; store (u, -v)
+  const uint2 a0 = make_uint2(pack2_bf16(c0[0], -c0[1]), pack2_bf16(c1[0], -c1[1]));
+  const uint2 a1 = make_uint2(pack2_bf16(c0[2], -c0[3]), pack2_bf16(c1[2], -c1[3]));
+  const int IP = d_in >> 1;
+  uint16_t* rec = out + ((ej * IP + (i >> 1)) * 2) * 8;  // 32-byte record of pair i/2
+  *reinterpret_cast<uint2*>(rec + (i & 1) * 4) = a0;       // a = 0 half, slot of i within the pair
+  *reinterpret_cast<uint2*>(rec + 8 + (i & 1) * 4) = a1;   // a = 1 half
+}
+
+// blade rows (bf16) -> Pauli half-rows (bf16); one thread per multivector
+__global__ __launch_bounds__(256) void blade_to_pauli_rows_kernel(const uint16_t* __restrict__ x, int rows, int d,
+                                                                  uint16_t* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)rows * d) return;
+  const size_t m = n / d;
+  const int i = (int)(n % d);
+  const uint4 q = *reinterpret_cast<const uint4*>(x + n * 8);
+  const float v[8] = {bf_lo(q.x), bf_hi(q.x), bf_lo(q.y), bf_hi(q.y), bf_lo(q.z), bf_hi(q.z), bf_lo(q.w), bf_hi(q.w)};
+  float c0[4], c1[4];
+  blade_to_pauli(v, c0, c1);
+  *reinterpret_cast<uint2*>(out + ((2 * m) * d + i) * 4) = make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+  *reinterpret_cast<uint2*>(out + ((2 * m + 1) * d + i) * 4) =
+      make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+}
+
+}  // namespace ygg
+
+using namespace ygg;
+
+namespace {
+// tile configuration of the launches below
+using Tile = PauliTile</*WR*/ 2, /*WC*/ 1, /*BWT*/ 2, /*BWJ*/ 4, /*KC*/ 16>;
+
+// persistent grid: one workgroup per CU (the LDS tile allows no more)
+struct DeviceShape {
+  int cus = 0, xcds = 1;
+};
+DeviceShape device_shape() {
+  static thread_local int cached_dev = -1;
+  static thread_local DeviceShape cached;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 64;
+    cached.cus = cus;
+    // MI355X (gfx950): 256 CUs in 8 XCDs; workgroups are dealt to the XCDs round robin
+    cached.xcds = (cus % 8 == 0) ? 8 : 1;
+    cached_dev = dev;
+  }
+  return cached;
+}
+
+template <int ACT, int IN, int OUT, int ODT>
+int launch_pauli(hipStream_t st, const uint16_t* X, const int32_t* gather, const uint16_t* Wp, const float* bias,
+                 const int32_t* offsets, int E, int P_max, int d_in, int d_out, void* Y) {
+  const DeviceShape ds = device_shape();
+  // never more workgroups than tiles can exist
+  const long long max_tiles =
+      ((long long)(P_max + Tile::T - 1) / Tile::T + E) * ((d_out + Tile::BN - 1) / Tile::BN);
+  int grid = ds.cus;
+  int xcds = ds.xcds;
+  if (max_tiles < grid) {
+    grid = (int)max_tiles;
+    xcds = 1;
+  }
+  pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
+      <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds);
+  return check_launch("pauli_gemm");
+}
+
+template <int ACT>
+int launch_pauli_act(hipStream_t st, int in_layout, int out_layout, int y_dtype, const uint16_t* X,
+                     const int32_t* gather, const uint16_t* Wp, const float* bias, const int32_t* offsets, int E,
+                     int P_max, int d_in, int d_out, void* Y) {
+#define YGG_PL(IN, OUT, ODT) launch_pauli<ACT, IN, OUT, ODT>(st, X, gather, Wp, bias, offsets, E, P_max, d_in, d_out, Y)
+  if (in_layout == kInBladeGather) {
+    if (out_layout == kOutPauliRows) return YGG_PL(kInBladeGather, kOutPauliRows, kBF16);
+    if (y_dtype == kBF16) return YGG_PL(kInBladeGather, kOutBlade, kBF16);
+    return YGG_PL(kInBladeGather, kOutBlade, kF32);
+  }
+  if (out_layout == kOutPauliRows) return YGG_PL(kInPauliRows, kOutPauliRows, kBF16);
+  if (y_dtype == kBF16) return YGG_PL(kInPauliRows, kOutBlade, kBF16);
+  return YGG_PL(kInPauliRows, kOutBlade, kF32);
+#undef YGG_PL
+}
+}  // namespace
+
+// Pauli weight preparation, called by ygg_prepare_weights (format 3).
+int ygg::pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream) {
+  YGG_CHECK_ARG(d_in >= 2 && (d_in % 2) == 0, "ygg_prepare_weights: the bf16 Pauli format needs an even d_in (got %d)",
+                d_in);
+  const size_t total = (size_t)E * d_out * d_in;
+  pauli_prep_weights_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(W, E, d_out, d_in,
+                                                                                  static_cast<uint16_t*>(out));
+  return check_launch("pauli_prep_weights");
+}
+
+YGG_API int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out, hipStream_t stream) {
+  YGG_CHECK_ARG(rows >= 0 && d >= 2 && (d % 2) == 0, "ygg_pauli_rows_from_blade: rows=%d d=%d (d must be even)",
+                rows, d);
+  if (rows == 0) return 0;
+  YGG_CHECK_ARG(x && out, "ygg_pauli_rows_from_blade: null pointer");
+  const size_t n = (size_t)rows * d;
+  blade_to_pauli_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(static_cast<const uint16_t*>(x), rows,
+                                                                               d, static_cast<uint16_t*>(out));
+  return check_launch("blade_to_pauli_rows");
+}
+
+YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather, int P_max, const void* w,
+                                     const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act,
+                                     void* y, int y_layout, int y_dtype, hipStream_t stream) {
+  YGG_CHECK_ARG(x_layout == kInBladeGather || x_layout == kInPauliRows, "ygg_pauli_grouped_linear: x layout %d",
+                x_layout);
+  YGG_CHECK_ARG(y_layout == kOutPauliRows || y_layout == kOutBlade, "ygg_pauli_grouped_linear: y layout %d", y_layout);
+  YGG_CHECK_ARG(y_layout == kOutPauliRows ? y_dtype == kBF16 : (y_dtype == kBF16 || y_dtype == kF32),
+                "ygg_pauli_grouped_linear: y dtype %d invalid for layout %d", y_dtype, y_layout);
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_pauli_grouped_linear: activation %d", act);
+  YGG_CHECK_ARG(E >= 1 && E <= kPauliMaxExperts && P_max >= 0 && d_in >= 2 && (d_in % 2) == 0 && d_out >= 1 &&
+                    (y_layout != kOutPauliRows || (d_out % 2) == 0),
+                "ygg_pauli_grouped_linear: bad sizes E=%d P=%d d_in=%d d_out=%d (E <= %d; d_in, and d_out of Pauli "
+                "rows, must be even)",
+                E, P_max, d_in, d_out, kPauliMaxExperts);
+  if (P_max == 0) return 0;
+  YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear: null pointer");
+  // staging uses 32-bit buffer offsets: every operand stays below 2 GiB
+  const size_t lim = (size_t)1 << 31;
+  YGG_CHECK_ARG((size_t)d_out * d_in * 16 < lim && (size_t)E * d_out * 32 < lim &&
+                    (gather != nullptr || (size_t)P_max * d_in * 16 < lim),
+                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (P=%d d_in=%d d_out=%d)",
+                P_max, d_in, d_out);
+  const uint16_t* X = static_cast<const uint16_t*>(x);
+  const uint16_t* Wp = static_cast<const uint16_t*>(w);
+  switch (act) {
+    case kActNone:
+      return launch_pauli_act<kActNone>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+                                        d_in, d_out, y);
+    case kActGelu:
+      return launch_pauli_act<kActGelu>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+                                        d_in, d_out, y);
+    case kActRelu:
+      return launch_pauli_act<kActRelu>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+                                        d_in, d_out, y);
+    default:
+      return launch_pauli_act<kActSigmoid>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E,
+                                           P_max, d_in, d_out, y);
+  }
+}

@@ -96,6 +96,11 @@ int check_launch(const char* what);
 
 enum DType : int { kF32 = 0, kBF16 = 1, kI8 = 2 };
 enum Act : int { kActNone = 0, kActGelu = 1, kActRelu = 2, kActSigmoid = 3 };
+// prepared weight formats (ygg_prepare_weights)
+enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3 };
+
+// bf16 Pauli weight layout (pauli_gemm.hip)
+int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
 
 inline int dtype_size(int dt) { return dt == kF32 ? 4 : dt == kBF16 ? 2 : dt == kI8 ? 1 : 0; }
 

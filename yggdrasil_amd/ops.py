@@ -16,7 +16,10 @@ from ._native import check, lib, ptr, stream_handle
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
 ACT_CODE = {"none": 0, "gelu": 1, "relu": 2, "sigmoid": 3}
-WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2}
+WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2, "pauli": 3}
+# activation row layouts of pauli_grouped_linear
+X_LAYOUT = {"blade": 0, "pauli": 1}
+Y_LAYOUT = {"pauli": 0, "blade": 1}
 
 
 def _dev(*tensors):
@@ -161,7 +164,7 @@ class PreparedWeights:
 
 
 def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
-    """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8')."""
+    """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8' | 'pauli')."""
     dev = _dev(w)
     if w.dim() == 3:
         w = w.unsqueeze(0)
@@ -170,6 +173,8 @@ def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
     code = WFORMAT_CODE[fmt]
     L = lib()
     nbytes = L.ygg_prepared_weight_bytes(E, d_out, d_in, code)
+    if nbytes == 0:
+        raise ValueError(f"weight format {fmt!r} cannot hold shape (E={E}, d_out={d_out}, d_in={d_in})")
     data = torch.empty((nbytes,), device=dev, dtype=torch.uint8)
     scales = torch.empty((E, d_out), device=dev, dtype=torch.float32) if fmt == "int8" else None
     check(L.ygg_prepare_weights(ptr(w), E, d_out, d_in, code, ptr(data), ptr(scales), stream_handle(dev)),
@@ -195,6 +200,8 @@ def grouped_clifford_linear(x_sorted: torch.Tensor, pw: PreparedWeights, offsets
                             bias_prepared: torch.Tensor | None = None, act: str = "none",
                             out_dtype: torch.dtype | None = None, out_blade_order: bool = True) -> torch.Tensor:
     """Per-expert CliffordLinear on expert-grouped rows. x_sorted: (P, d_in, 8) in mask order."""
+    if pw.fmt == "pauli":
+        raise ValueError("Pauli weights run through pauli_grouped_linear")
     dev = _dev(x_sorted, offsets, bias_prepared)
     P = x_sorted.shape[0]
     if x_sorted.shape[1] != pw.d_in:
@@ -209,6 +216,49 @@ def grouped_clifford_linear(x_sorted: torch.Tensor, pw: PreparedWeights, offsets
                                             ACT_CODE[act], ptr(y), DTYPE_CODE[out_dtype], int(out_blade_order),
                                             stream_handle(dev)), "grouped_clifford_linear")
     return y
+
+
+def pauli_grouped_linear(x: torch.Tensor, pw: PreparedWeights, offsets: torch.Tensor,
+                         bias_prepared: torch.Tensor | None = None, act: str = "none", x_layout: str = "blade",
+                         gather: torch.Tensor | None = None, rows: int | None = None, y_layout: str = "blade",
+                         out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Per-expert CliffordLinear with Pauli (complex 2x2) weights.
+
+    x_layout 'blade': x is (N, d_in, 8) bf16 in blade order; output row r reads
+    x[gather[r]] (or x[r]).  x_layout 'pauli': x is (P, 2, d_in, 4) Pauli half-rows.
+    y_layout 'pauli' returns (P, 2, d_out, 4) bf16; 'blade' returns (P, d_out, 8).
+    ``rows`` is the number of product rows P (default: len(gather) or x's rows).
+    """
+    if pw.fmt != "pauli":
+        raise ValueError("pauli_grouped_linear needs weights prepared with fmt='pauli'")
+    dev = _dev(x, offsets, bias_prepared, gather)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("Pauli products take bf16 activations")
+    d_in_x = x.shape[1] if x_layout == "blade" else x.shape[2]
+    if d_in_x != pw.d_in:
+        raise ValueError(f"x has d_in={d_in_x}, weights expect {pw.d_in}")
+    if rows is None:
+        rows = gather.shape[0] if gather is not None else x.shape[0]
+    if y_layout == "pauli":
+        y = torch.empty((rows, 2, pw.d_out, 4), device=dev, dtype=torch.bfloat16)
+    else:
+        y = torch.empty((rows, pw.d_out, 8), device=dev, dtype=out_dtype)
+    check(lib().ygg_pauli_grouped_linear(ptr(x), X_LAYOUT[x_layout], ptr(gather), rows, ptr(pw.data),
+                                         ptr(bias_prepared), ptr(offsets), pw.E, pw.d_in, pw.d_out, ACT_CODE[act],
+                                         ptr(y), Y_LAYOUT[y_layout], DTYPE_CODE[y.dtype], stream_handle(dev)),
+          "pauli_grouped_linear")
+    return y
+
+
+def pauli_rows_from_blade(x: torch.Tensor) -> torch.Tensor:
+    """(rows, d, 8) bf16 blade order -> (rows, 2, d, 4) Pauli half-rows."""
+    dev = _dev(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("bf16 rows only")
+    rows, d = x.shape[0], x.shape[1]
+    out = torch.empty((rows, 2, d, 4), device=dev, dtype=torch.bfloat16)
+    check(lib().ygg_pauli_rows_from_blade(ptr(x), rows, d, ptr(out), stream_handle(dev)), "pauli_rows_from_blade")
+    return out
 
 
 def moe_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype) -> int:
