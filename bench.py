@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--configs", default="c3,c1,c2,c4,c5")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=256)
+    # a plain device copy of this many MiB, run (3 times) before the configs: the reference
+    # point that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc profile
+    ap.add_argument("--calib-copy-mb", type=int, default=0)
     return ap.parse_args()
 
 
@@ -317,6 +320,14 @@ def main():
         print(json.dumps({"error": "no GPU"}))
         sys.exit(1)
     names = [s.strip() for s in args.configs.split(",") if s.strip()]
+    if args.calib_copy_mb:
+        n = args.calib_copy_mb << 18  # fp32 elements
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     results = {}
     for name in names:
         c = CONFIGS[name]
