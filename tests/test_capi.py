@@ -49,9 +49,10 @@ def test_host_side_sizes():
         pytest.skip("library not built")
     L = _native.lib()
     assert L.ygg_version() == 1
-    # route workspace: slot ranks + two per-block histograms, 256-byte aligned
-    nb = (16384 + 255) // 256
-    assert L.ygg_route_workspace_bytes(16384, 16, 2) == ((16384 * 2 * 4 + 2 * nb * 16 * 4) + 255) // 256 * 256
+    # route workspace: one histogram row per 32-token block (scanned in place), 256-byte aligned
+    nb = (16384 + 31) // 32
+    assert L.ygg_route_workspace_bytes(16384, 16, 2) == (nb * 16 * 4 + 255) // 256 * 256
+    assert L.ygg_route_workspace_bytes(33, 5, 3) == 256
     # prepared weights: bf16 dual layout pads d_out to 32 and d_in to 2
     assert L.ygg_prepared_weight_bytes(32, 512, 128, 1) == 32 * 16 * 64 * 64 * 32
     assert L.ygg_prepared_weight_bytes(2, 5, 7, 1) == 2 * 1 * 4 * 64 * 32

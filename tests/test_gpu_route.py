@@ -80,6 +80,34 @@ def test_route_ties_lowest_index_wins(E, k):
     _check_route(logits, k, E, f"ties E={E} k={k}")
 
 
+@pytest.mark.parametrize("E,k", [(1, 1), (3, 2), (5, 5), (7, 3), (9, 4), (12, 2), (20, 6), (33, 8), (63, 2)])
+def test_route_expert_counts_off_the_lane_grid(E, k):
+    """E below 8 and E not a multiple of 8 take the other branches of the pairwise row sum."""
+    r = np.random.default_rng(100 + E * 8 + k)
+    _check_route(r.standard_normal((613, E), dtype=np.float32) * 3, k, E, f"E={E} k={k}")
+
+
+def test_route_nan_rows_stay_in_range():
+    """NaN logits leave the weights unspecified but every slot still names a distinct valid expert."""
+    ops = _ops()
+    r = np.random.default_rng(77)
+    N, E, k = 300, 24, 4
+    logits = r.standard_normal((N, E), dtype=np.float32)
+    logits[::7, 3] = np.nan
+    logits[::11] = np.nan
+    say("route NaN rows")
+    rt = ops.route(torch.from_numpy(logits).cuda(), k)
+    idx = rt.topk_idx.cpu().numpy()
+    assert idx.min() >= 0 and idx.max() < E
+    assert all(len(set(row)) == k for row in idx)
+    assert rt.counts.cpu().numpy().sum() == N * k
+    perm = rt.perm.cpu().numpy()
+    assert np.array_equal(np.sort(perm), np.repeat(np.arange(N), k))
+    clean = ~np.isnan(logits).any(axis=1)
+    idx_o, _ = moe.route_topk(moe.softmax(logits[clean]), k)
+    assert np.array_equal(idx[clean], idx_o)
+
+
 def test_route_zipf_skew_and_empty_experts():
     r = np.random.default_rng(9)
     N, E, k = 3000, 32, 4

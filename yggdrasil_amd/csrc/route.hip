@@ -7,198 +7,232 @@
 //   * hlm_block.py:165-177        flat slots grouped by expert (counts, perm)
 //                                 (ygg_route)
 //
-// Design.  Routing is a few MB of traffic, so the kernels aim at few launches
-// and no atomics (the permutation must be bit-exact and deterministic):
-//   K1 route_topk_rank   one thread per token: max, exp, pairwise sum (the
-//                        summation tree NumPy uses for a row of E floats),
-//                        k selections with lowest-index ties, renormalise;
-//                        then, per 256-token block, every slot's rank among
-//                        the block's slots of the same expert from 64-lane
-//                        ballots, and the block histogram.
-//   K2 route_scan        one block: per expert, exclusive scan of the block
-//                        histograms over blocks; counts and offsets.
-//   K3 route_place       one thread per token: sorted position of every slot
-//                        = offsets[e] + block_base[b][e] + rank; writes perm
-//                        and slot_pos.
-// The expert-grouped order within an expert is ascending token order, which
-// is the reference's dispatch order (hlm_block.py:172-178).
+// Design.  Routing moves a few MB, so it is latency bound: the aim is short
+// dependency chains and enough waves, with no atomics (the permutation must
+// be deterministic and bit-exact):
+//   K1 route_select  eight lanes per token, 32 tokens per 256-thread block.
+//                    Lane j holds the logits j, j+8, j+16, ...: a shuffle tree
+//                    gives the row max, and lane j's running sum of its own
+//                    elements followed by the xor-shuffle tree (1, 2, 4) is
+//                    exactly NumPy's pairwise summation of a row (eight
+//                    accumulators, ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then
+//                    the remainder in order).  Top-k is k rounds of a shuffle
+//                    argmax (higher probability, then lower index).  Lane j of
+//                    a token then holds slot j, so a 64-lane ballot per expert
+//                    ranks every slot among the block's slots of that expert
+//                    in token order; the rank goes to slot_pos and the block
+//                    histogram to the workspace.
+//   K2 route_scan    one workgroup: for every expert, the exclusive scan of the
+//                    block histograms over blocks (in place), counts, offsets.
+//   K3 route_place   one thread per slot: slot_pos += offsets[e] + block base;
+//                    perm[slot_pos] = token.
+// Within an expert the rows are in ascending token order, the reference's
+// dispatch order (hlm_block.py:172-178).
 
 #include "ygg_common.h"
 
 namespace ygg {
 
-constexpr int kRouteBlock = 256;
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
+constexpr int kSelLanes = 8;                          // lanes per token
+constexpr int kSelBlock = 256;                        // threads per K1 block
+constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
+constexpr int kScanMaxThreads = 1024;
 
-// Pairwise summation of n floats as NumPy does for one reduced row
-// (blocks of 8 accumulators, combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)),
-// remainder added sequentially; fewer than 8 values: sequential from 0).
-__device__ inline float numpy_row_sum(const float* v, int n) {
-  if (n < 8) {
-    float s = 0.f;
-    for (int i = 0; i < n; ++i) s = __fadd_rn(s, v[i]);
-    return s;
-  }
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = v[j];
-  int i = 8;
-  for (; i + 8 <= n; i += 8) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], v[i + j]);
-  }
-  float s = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
-                      __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
-  for (; i < n; ++i) s = __fadd_rn(s, v[i]);
-  return s;
-}
-
-template <int MAXE>
-__global__ __launch_bounds__(kRouteBlock) void route_topk_rank(const float* __restrict__ logits, int N, int E, int k,
-                                                               int32_t* __restrict__ topk_idx,
-                                                               float* __restrict__ topk_w,
-                                                               int32_t* __restrict__ slot_rank,
-                                                               int32_t* __restrict__ block_hist) {
-  __shared__ int32_t wave_cnt[kRouteBlock / 64][MAXE];
+template <int Q>  // Q = ceil(E / 8) logits per lane
+__global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
+                                                          int32_t* __restrict__ topk_idx,
+                                                          float* __restrict__ topk_w,
+                                                          int32_t* __restrict__ slot_rank,
+                                                          int32_t* __restrict__ block_hist) {
+  __shared__ int32_t wave_cnt[kSelBlock / 64][kMaxExperts];
   const int tid = threadIdx.x;
-  const int t = blockIdx.x * kRouteBlock + tid;
+  const int j = tid & (kSelLanes - 1);
+  const int t = blockIdx.x * kSelTokens + tid / kSelLanes;
   const bool active = t < N;
   const int lane = tid & 63, wave = tid >> 6;
 
+  // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
+  float p[Q];
+  float m = -INFINITY;
+  const float* row = logits + (size_t)(active ? t : 0) * E;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    p[q] = (active && e < E) ? row[e] : -INFINITY;
+    m = fmaxf(m, p[q]);
+  }
+#pragma unroll
+  for (int o = 1; o < kSelLanes; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    p[q] = (e < E) ? expf(__fsub_rn(p[q], m)) : 0.f;
+  }
+  // NumPy pairwise sum of the row: rows of fewer than 8 values are summed in
+  // order; otherwise accumulator j sums the elements j, j+8, ... below
+  // E8 = E - E % 8, the eight accumulators are combined as a tree and the
+  // remaining E % 8 values are added in order.
+  const int E8 = E - (E & 7);
+  float sum;
+  if (E < 8) {
+    sum = 0.f;
+    for (int e = 0; e < E; ++e) sum = __fadd_rn(sum, __shfl(p[0], (lane & ~7) + e));
+  } else {
+    float r = p[0];
+#pragma unroll
+    for (int q = 1; q < Q; ++q)
+      if (j + kSelLanes * q < E8) r = __fadd_rn(r, p[q]);
+    r = __fadd_rn(r, __shfl_xor(r, 1));
+    r = __fadd_rn(r, __shfl_xor(r, 2));
+    r = __fadd_rn(r, __shfl_xor(r, 4));
+    sum = r;
+    for (int e = E8; e < E; ++e) sum = __fadd_rn(sum, __shfl(p[Q - 1], (lane & ~7) + (e & 7)));
+  }
+  const float denom = __fadd_rn(sum, 1e-12f);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) p[q] = __fdiv_rn(p[q], denom);
+
+  // ---- top-k: k rounds of (max probability, then min index) over the 8 lanes.
+  // The selection key orders NaN probabilities below every real one, so the
+  // order is total, all 8 lanes agree on each winner and every slot gets a
+  // valid expert (with NaN logits the weights are unspecified).
+  float key[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) key[q] = (p[q] == p[q]) ? p[q] : -1.0f;
   int sel[kMaxTopK];
+  float wsel[kMaxTopK];
+  uint32_t taken = 0;  // bit q: this lane's element q is selected
 #pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) sel[s] = -1;
-
-  if (active) {
-    float p[MAXE];
-    const float* row = logits + (size_t)t * E;
-    float m = -INFINITY;
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel[s] = 0;
+    wsel[s] = 0.f;
+    if (s < k) {
+      float bv = -2.0f;
+      int bi = 0x7fffffff;
 #pragma unroll
-    for (int e = 0; e < MAXE; ++e)
-      if (e < E) {
-        p[e] = row[e];
-        m = fmaxf(m, p[e]);
-      }
-#pragma unroll
-    for (int e = 0; e < MAXE; ++e)
-      if (e < E) p[e] = expf(__fsub_rn(p[e], m));
-    const float denom = __fadd_rn(numpy_row_sum(p, E), 1e-12f);
-#pragma unroll
-    for (int e = 0; e < MAXE; ++e)
-      if (e < E) p[e] = __fdiv_rn(p[e], denom);
-
-    // k selections: highest probability, lowest index among equals
-    uint64_t taken = 0;
-    float wsel[kMaxTopK];
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) {
-      if (s < k) {
-        int best = -1;
-        float bv = 0.f;
-#pragma unroll
-        for (int e = 0; e < MAXE; ++e) {
-          if (e < E && !((taken >> e) & 1ull) && (best < 0 || p[e] > bv)) {
-            best = e;
-            bv = p[e];
-          }
+      for (int q = 0; q < Q; ++q) {
+        const int e = j + kSelLanes * q;
+        if (e < E && !((taken >> q) & 1u) && (key[q] > bv || (key[q] == bv && e < bi))) {
+          bv = key[q];
+          bi = e;
         }
-        taken |= 1ull << best;
-        sel[s] = best;
-        wsel[s] = bv;
       }
+#pragma unroll
+      for (int o = 1; o < kSelLanes; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      // k <= E: at least one candidate remains, so bi is a valid expert
+      sel[s] = bi;
+      wsel[s] = bv;
+      if ((bi & (kSelLanes - 1)) == j) taken |= 1u << ((bi / kSelLanes) & 31);
     }
-    // renormalise; the sum runs from the least to the most probable slot
-    float ssum = 0.f;
+  }
+  // renormalise; the sum runs from the least to the most probable slot
+  float ssum = 0.f;
 #pragma unroll
-    for (int s = kMaxTopK - 1; s >= 0; --s)
-      if (s < k) ssum = __fadd_rn(ssum, wsel[s]);
-    ssum = __fadd_rn(ssum, 1e-12f);
+  for (int s = kMaxTopK - 1; s >= 0; --s)
+    if (s < k) ssum = __fadd_rn(ssum, wsel[s]);
+  ssum = __fadd_rn(ssum, 1e-12f);
+  int my_e = -1;  // lane j holds slot j
+  float my_w = 0.f;
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) {
-        topk_idx[(size_t)t * k + s] = sel[s];
-        topk_w[(size_t)t * k + s] = __fdiv_rn(wsel[s], ssum);
-      }
+  for (int s = 0; s < kMaxTopK; ++s)
+    if (s == j && s < k) {
+      my_e = sel[s];
+      my_w = __fdiv_rn(wsel[s], ssum);
+    }
+  if (!active) my_e = -1;
+  if (my_e >= 0) {
+    topk_idx[(size_t)t * k + j] = my_e;
+    topk_w[(size_t)t * k + j] = my_w;
   }
 
-  // per-expert rank of every slot among this block's slots (token order)
+  // ---- rank of every slot among the block's slots of its expert (token order)
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int rank[kMaxTopK];
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) rank[s] = 0;
+  int rank = 0;
   for (int e = 0; e < E; ++e) {
-    bool has = false;
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) has |= (sel[s] == e);
-    const uint64_t bal = __ballot(has);
-    const int r = __popcll(bal & lt_mask);
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s)
-      if (sel[s] == e) rank[s] = r;
+    const uint64_t bal = __ballot(my_e == e);
+    if (my_e == e) rank = __popcll(bal & lt_mask);
     if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
   }
   __syncthreads();
-  if (active) {
-#pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) {
-      if (s < k) {
-        const int e = sel[s];
-        int base = 0;
-        for (int w = 0; w < wave; ++w) base += wave_cnt[w][e];
-        slot_rank[(size_t)t * k + s] = base + rank[s];
-      }
-    }
+  if (my_e >= 0) {
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wave_cnt[w][my_e];
+    slot_rank[(size_t)t * k + j] = base + rank;
   }
   if (tid < E) {
     int c = 0;
 #pragma unroll
-    for (int w = 0; w < kRouteBlock / 64; ++w) c += wave_cnt[w][tid];
+    for (int w = 0; w < kSelBlock / 64; ++w) c += wave_cnt[w][tid];
     block_hist[(size_t)blockIdx.x * E + tid] = c;
   }
 }
 
-// One block.  Thread e walks the blocks in order (coalesced across e).
-__global__ __launch_bounds__(64) void route_scan(const int32_t* __restrict__ block_hist, int nblocks, int E,
-                                                 int32_t* __restrict__ block_base, int32_t* __restrict__ counts,
-                                                 int32_t* __restrict__ offsets) {
+// One workgroup of EP x G threads (EP = E rounded up to a power of two, G <= 64
+// threads per expert).  Thread (g, e) owns a contiguous range of blocks.
+__global__ __launch_bounds__(kScanMaxThreads) void route_scan(int32_t* __restrict__ block_hist, int nblocks, int E,
+                                                              int EP, int32_t* __restrict__ counts,
+                                                              int32_t* __restrict__ offsets) {
+  __shared__ int32_t part[kScanMaxThreads];
   __shared__ int32_t tot[kMaxExperts];
-  const int e = threadIdx.x;
-  int run = 0;
-  if (e < E) {
-    for (int b = 0; b < nblocks; ++b) {
-      block_base[(size_t)b * E + e] = run;
-      run += block_hist[(size_t)b * E + e];
-    }
-    counts[e] = run;
-  }
-  tot[e] = (e < E) ? run : 0;
+  const int tid = threadIdx.x;
+  const int e = tid % EP, g = tid / EP;
+  const int G = blockDim.x / EP;
+  const int per = (nblocks + G - 1) / G;
+  const int b0 = g * per, b1 = min(nblocks, b0 + per);
+  int s = 0;
+  if (e < E)
+    for (int b = b0; b < b1; ++b) s += block_hist[(size_t)b * E + e];
+  part[tid] = s;
   __syncthreads();
-  if (e == 0) {
+  if (g == 0) {  // exclusive scan over the G ranges of expert e
+    int run = 0;
+    for (int h = 0; h < G; ++h) {
+      const int v = part[h * EP + e];
+      part[h * EP + e] = run;
+      run += v;
+    }
+    if (e < E) tot[e] = run;
+  }
+  __syncthreads();
+  if (e < E) {
+    int run = part[tid];
+    for (int b = b0; b < b1; ++b) {
+      const int v = block_hist[(size_t)b * E + e];
+      block_hist[(size_t)b * E + e] = run;
+      run += v;
+    }
+  }
+  if (tid == 0) {
     int acc = 0;
-    for (int i = 0; i < E; ++i) {
-      offsets[i] = acc;
-      acc += tot[i];
+    for (int x = 0; x < E; ++x) {
+      counts[x] = tot[x];
+      offsets[x] = acc;
+      acc += tot[x];
     }
     offsets[E] = acc;
   }
 }
 
-__global__ __launch_bounds__(kRouteBlock) void route_place(const int32_t* __restrict__ topk_idx,
-                                                           const int32_t* __restrict__ slot_rank,
-                                                           const int32_t* __restrict__ block_base,
-                                                           const int32_t* __restrict__ offsets, int N, int E, int k,
-                                                           int32_t* __restrict__ perm,
-                                                           int32_t* __restrict__ slot_pos) {
-  const int t = blockIdx.x * kRouteBlock + threadIdx.x;
-  if (t >= N) return;
-  for (int s = 0; s < k; ++s) {
-    const size_t f = (size_t)t * k + s;
-    const int e = topk_idx[f];
-    const int pos = offsets[e] + block_base[(size_t)blockIdx.x * E + e] + slot_rank[f];
-    perm[pos] = t;
-    slot_pos[f] = pos;
-  }
+__global__ __launch_bounds__(256) void route_place(const int32_t* __restrict__ topk_idx,
+                                                   const int32_t* __restrict__ block_base,
+                                                   const int32_t* __restrict__ offsets, int N, int E, int k,
+                                                   int32_t* __restrict__ perm, int32_t* __restrict__ slot_pos) {
+  const size_t f = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (f >= (size_t)N * k) return;
+  const int t = (int)(f / k);
+  const int e = topk_idx[f];
+  const int pos = offsets[e] + block_base[(size_t)(t / kSelTokens) * E + e] + slot_pos[f];
+  slot_pos[f] = pos;
+  perm[pos] = t;
 }
 
 // Grade energy of one token -> normalised -> logits.  One wave per token;
@@ -251,9 +285,9 @@ __global__ __launch_bounds__(256) void router_energy_logits_kernel(const void* _
 using namespace ygg;
 
 YGG_API size_t ygg_route_workspace_bytes(int N, int E, int k) {
-  const size_t nb = (size_t)(N + kRouteBlock - 1) / kRouteBlock;
-  const size_t bytes = (size_t)N * k * 4 + 2 * nb * E * 4;
-  return (bytes + 255) & ~(size_t)255;
+  (void)k;
+  const size_t nb = (size_t)(N + kSelTokens - 1) / kSelTokens;
+  return (nb * E * 4 + 255) & ~(size_t)255;
 }
 
 YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
@@ -267,23 +301,29 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   YGG_CHECK_ARG(N == 0 || (logits && topk_idx && topk_w && perm && slot_pos && workspace),
                 "ygg_route: null pointer argument");
   YGG_CHECK_ARG(counts && offsets, "ygg_route: null counts/offsets");
-  const int nb = (N + kRouteBlock - 1) / kRouteBlock;
-  int32_t* slot_rank = static_cast<int32_t*>(workspace);
-  int32_t* block_hist = slot_rank + (size_t)N * k;
-  int32_t* block_base = block_hist + (size_t)nb * E;
+  const int nb = (N + kSelTokens - 1) / kSelTokens;
+  int32_t* block_hist = static_cast<int32_t*>(workspace);
   if (nb > 0) {
-    if (E <= 16)
-      route_topk_rank<16><<<nb, kRouteBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_rank, block_hist);
-    else if (E <= 32)
-      route_topk_rank<32><<<nb, kRouteBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_rank, block_hist);
-    else
-      route_topk_rank<64><<<nb, kRouteBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_rank, block_hist);
-    if (check_launch("route_topk_rank")) return -1;
+    // slot ranks go to slot_pos; route_place turns them into rows
+    switch ((E + 7) / 8) {
+#define YGG_SEL(Q)                                                                                            \
+  case Q:                                                                                                     \
+    route_select<Q><<<nb, kSelBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_pos, block_hist); \
+    break;
+      YGG_SEL(1) YGG_SEL(2) YGG_SEL(3) YGG_SEL(4) YGG_SEL(5) YGG_SEL(6) YGG_SEL(7) YGG_SEL(8)
+#undef YGG_SEL
+    }
+    if (check_launch("route_select")) return -1;
   }
-  route_scan<<<1, 64, 0, stream>>>(block_hist, nb, E, block_base, counts, offsets);
+  int EP = 1;
+  while (EP < E) EP <<= 1;
+  const int G = min(64, kScanMaxThreads / EP);
+  route_scan<<<1, EP * G, 0, stream>>>(block_hist, nb, E, EP, counts, offsets);
   if (check_launch("route_scan")) return -1;
   if (nb > 0) {
-    route_place<<<nb, kRouteBlock, 0, stream>>>(topk_idx, slot_rank, block_base, offsets, N, E, k, perm, slot_pos);
+    const size_t slots = (size_t)N * k;
+    route_place<<<(unsigned)((slots + 255) / 256), 256, 0, stream>>>(topk_idx, block_hist, offsets, N, E, k, perm,
+                                                                     slot_pos);
     if (check_launch("route_place")) return -1;
   }
   return 0;
