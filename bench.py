@@ -130,7 +130,7 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
             logits=L.get("logits"), router_w=L.get("router_w"), router_b=L.get("router_b")))
         del L["w_up"], L["w_down"]
     torch.cuda.synchronize()
-    ws = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype), device="cuda", dtype=torch.uint8)
+    ws = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype, c["fmt"]), device="cuda", dtype=torch.uint8)
     bufs = [torch.empty_like(x), torch.empty_like(x)]
     resid = c["layers"] > 1
     info = {}

@@ -144,8 +144,8 @@ int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather,
 int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out, ygg_stream_t stream);
 
 /* ---- the whole layer ---------------------------------------------------------
- * Workspace bytes of ygg_moe_forward. */
-size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype);
+ * Workspace bytes of ygg_moe_forward for activation dtype and weight format. */
+size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format);
 
 /* HLMBlock._moe_forward (hlm_block.py:154-183): x (N, d, 8) of dtype ->
  * out (N, d, 8) of dtype (+ residual if not NULL).  logits (N, E) or NULL

@@ -36,7 +36,9 @@ def test_geom_matmul_operator(name):
 @pytest.mark.parametrize("fmt,act,d_in,d_out,E,P", [
     ("f32", "none", 8, 16, 3, 50), ("f32", "gelu", 64, 256, 8, 512), ("f32", "relu", 7, 5, 2, 33),
     ("bf16", "none", 16, 64, 4, 200), ("bf16", "gelu", 128, 512, 3, 300), ("bf16", "sigmoid", 9, 40, 5, 77),
-    ("int8", "gelu", 32, 64, 4, 100), ("int8", "none", 128, 96, 2, 70)])
+    ("int8", "gelu", 32, 64, 4, 100), ("int8", "none", 128, 96, 2, 70),
+    # at most 16 rows per expert on average: the decode-shape (weight-streaming) kernel
+    ("int8", "gelu", 128, 512, 8, 60), ("int8", "sigmoid", 10, 40, 5, 30), ("int8", "none", 64, 130, 4, 50)])
 def test_grouped_clifford_linear(fmt, act, d_in, d_out, E, P):
     _, ops = _mods()
     g = np.random.default_rng(d_in * 7 + d_out + E)
@@ -186,6 +188,37 @@ def test_full_c4_decode_int8_sampled():
     g = np.random.default_rng(404)
     logits = g.standard_normal((64, 32), dtype=np.float32)
     _sampled_layer_check(64, 128, 512, 32, 2, "int8", logits, 44, n_sample=16)
+
+
+def test_decode_int8_skewed_layer():
+    """Decode-shape int8 layer: one expert gets more than 16 rows (row-block loop), F = 302
+    gives three K splits of the down product with a tail, bias on both products."""
+    yggdrasil_amd, _ = _mods()
+    g = np.random.default_rng(606)
+    N, d, F, E, k = 64, 96, 302, 8, 2
+    x = _inputs.bf16_round(g.standard_normal((N, d, 8), dtype=np.float32))
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F, bias_std=0.3)
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    logits[:40, 0] += 6.0  # expert 0 takes 40 tokens
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, dtype=torch.bfloat16,
+                                     weight_format="int8", router="logits")
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    say(f"decode int8 skewed N={N} d={d} F={F} E={E} k={k}")
+    y = layer.moe_forward(torch.from_numpy(x).cuda().bfloat16().reshape(1, N, d, 8),
+                          logits=torch.from_numpy(logits).cuda()).float().cpu().numpy().reshape(N, d, 8)
+    idx = layer.last_routing["topk_idx"].cpu().numpy()
+    assert layer.last_routing["counts"].cpu().numpy()[0] >= 40
+    idx_o, w_o = moe.route_topk(moe.softmax(logits), k)
+    assert np.array_equal(idx, idx_o)
+    wu_q = moe.dequantize_int8(*moe.quantize_int8(wu))
+    wd_q = moe.dequantize_int8(*moe.quantize_int8(wd))
+    ref = np.zeros((N, d, 8), np.float32)
+    for t in range(N):
+        for s in np.argsort(idx[t]):
+            e = idx[t, s]
+            ref[t] += w_o[t, s] * moe.clifford_ffn(x[t][None], wu_q[e], bu[e], wd_q[e], bd[e], "gelu")[0]
+    assert normwise_err(y, ref) < TOL_BF16
 
 
 def test_module_rejects_cpu_tensors():

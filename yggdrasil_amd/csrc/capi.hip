@@ -57,16 +57,24 @@ extern "C" int ygg_pauli_grouped_linear(const void*, int, const int32_t*, int, c
                                         const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
 extern "C" int ygg_pauli_rows_from_blade(const void*, int, int, void*, hipStream_t);
 
-YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype) {
+// y_sorted region: bf16/fp32 rows, or for the decode-shape int8 path the fp32
+// partial planes of the K-split down product
+static size_t ys_bytes(size_t P, int E, int d, int F, int dtype, int w_format) {
+  const size_t es = (dtype == kF32) ? 4 : 2;
+  if (decode_shape((int)P, E, w_format)) return (size_t)decode_splits(F) * P * d * 8 * 4;
+  return P * d * 8 * es;
+}
+
+YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format) {
   const size_t P = (size_t)N * k;
   const size_t es = (dtype == kF32) ? 4 : 2;
   size_t b = 0;
   b += align256((size_t)N * E * 4);       // logits
   b += align256(P * 4) * 2;               // perm, slot_pos
   b += align256(ygg_route_workspace_bytes(N, E, k));
-  b += align256(P * d * 8 * es);          // x_sorted
+  b += align256(P * d * 8 * es);          // x_sorted (Pauli half-rows of x for format 3)
   b += align256(P * F * 8 * es);          // h
-  b += align256(P * d * 8 * es);          // y_sorted
+  b += align256(ys_bytes(P, E, d, F, dtype, w_format));  // y_sorted
   return b;
 }
 
@@ -81,9 +89,9 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
                 "ygg_moe_forward: weight format %d does not match dtype %d", w_format, dtype);
   YGG_CHECK_ARG(w_format != kWPauli || (d % 2 == 0 && F % 2 == 0),
                 "ygg_moe_forward: the Pauli weight format needs even d and F (d=%d F=%d)", d, F);
-  YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype),
+  YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format),
                 "ygg_moe_forward: workspace of %zu bytes, need %zu", workspace_bytes,
-                ygg_moe_workspace_bytes(N, d, F, E, k, dtype));
+                ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format));
   YGG_CHECK_ARG(logits || (router_w && router_b), "ygg_moe_forward: need logits or router parameters");
   if (N == 0) return 0;
   const size_t P = (size_t)N * k;
@@ -123,6 +131,18 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
     return ygg_combine(ys, kBF16, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
   }
   if (ygg_dispatch(x, dtype, N, k, d, slot_pos, xs, /*to_mask_order=*/1, stream)) return -1;
+  if (decode_shape((int)P, E, w_format)) {
+    // decode: weight-streaming products; the down product in K splits whose fp32
+    // partial planes the combine adds in split order
+    if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
+                                    /*blade=*/0, stream))
+      return -1;
+    if (decode_linear_partial(static_cast<const uint16_t*>(h), (int)P, static_cast<const int8_t*>(w_down), s_down,
+                              b_down, offsets, E, F, d, static_cast<float*>(ys), stream))
+      return -1;
+    return combine_planes(static_cast<const float*>(ys), decode_splits(F), (int)P, N, k, d, topk_idx, topk_w,
+                          slot_pos, residual, out, dtype, stream);
+  }
   if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
                                   /*blade=*/0, stream))
     return -1;

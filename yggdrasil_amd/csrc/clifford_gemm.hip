@@ -306,6 +306,120 @@ __global__ __launch_bounds__(256, 2) void grouped_cl_mfma(const uint16_t* __rest
 }
 
 // ---------------------------------------------------------------------------
+// decode-shape kernel: int8 weights, a few rows per expert
+// ---------------------------------------------------------------------------
+// Weight bytes, not FLOPs, bound this shape, so the work is cut for memory
+// parallelism: one 512-thread workgroup per (expert, 16 output multivectors,
+// K split); the eight waves split the split's contraction, and every lane
+// issues all its weight loads at once (one memory latency, no serial K loop).
+// int8 is widened to bf16 in registers (exact), the 8x8 L(w) rows are built
+// as in the prefill kernel, and v_mfma_f32_16x16x32_bf16 runs over 16-row
+// blocks of the expert's rows.  The waves' partial sums are added in LDS in
+// fixed wave order.  With more than one K split each split writes an fp32
+// partial plane (scale applied, bias in split 0) and the consumer adds the
+// planes in split order -- deterministic either way.
+constexpr int kDecWaves = 8;
+constexpr int kDecJ = 16;     // output multivectors per workgroup
+constexpr int kDecRows = 16;  // rows per MFMA block
+constexpr int kDecKPW = 4;    // K steps (4 input multivectors each) per wave
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int ACT, bool OUT_BLADE, int OUT_DT, bool PARTIAL>
+__global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(const uint16_t* __restrict__ A,
+                                                                      const int8_t* __restrict__ Wq,
+                                                                      const float* __restrict__ wscale,
+                                                                      const float* __restrict__ bias,
+                                                                      const int32_t* __restrict__ offsets, int d_in,
+                                                                      int d_out, int P_max, void* __restrict__ Y) {
+  __shared__ float part[kDecWaves][kDecRows][kDecJ][9];  // +1 float of padding per multivector
+  const int e = blockIdx.x, split = blockIdx.z;
+  const int row_beg = offsets[e], row_end = offsets[e + 1];
+  if (row_beg >= row_end) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int jl = lane & 15, g = lane >> 4;  // output column (B) / row (A) within the block; k group
+  const int j = blockIdx.y * kDecJ + jl;
+  const int JB = (d_out + 31) >> 5, IP = (d_in + 1) >> 1;
+  const int KS = (d_in + 3) >> 2;  // K steps of 4 input multivectors
+  const int ks_split = kDecWaves * kDecKPW;
+  const int ks0 = split * ks_split + wave * kDecKPW;
+
+  // all weight loads of this lane: multivector (j, i = 4 ks + g) of expert e
+  uint2 wq[kDecKPW];
+#pragma unroll
+  for (int u = 0; u < kDecKPW; ++u) {
+    const int i = 4 * (ks0 + u) + g;
+    wq[u] = make_uint2(0, 0);
+    if (ks0 + u < KS && i < d_in && j < d_out) {
+      const size_t slot = (((size_t)e * JB + (j >> 5)) * IP + (i >> 1)) * 64 + (j & 31) * 2 + (i & 1);
+      wq[u] = *reinterpret_cast<const uint2*>(Wq + slot * 8);
+    }
+  }
+
+  for (int r0 = row_beg; r0 < row_end; r0 += kDecRows) {
+    const int arow = min(r0 + jl, row_end - 1);  // rows past the expert's range are not stored
+    f32x4_t acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kDecKPW; ++u) {
+      const int i = 4 * (ks0 + u) + g;
+      uint4 a = make_uint4(0, 0, 0, 0);
+      if (ks0 + u < KS && i < d_in) a = *reinterpret_cast<const uint4*>(A + ((size_t)arow * d_in + i) * 8);
+      int c[8];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        c[p] = (int)(int8_t)((wq[u].x >> (8 * p)) & 0xff);
+        c[4 + p] = (int)(int8_t)((wq[u].y >> (8 * p)) & 0xff);
+      }
+      uint32_t raw[4], sw[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        raw[t] = i8pair_to_bf16x2(c[2 * t], c[2 * t + 1]);
+        sw[t] = (raw[t] >> 16) | (raw[t] << 16);
+      }
+      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<0>(raw, sw), acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<1>(raw, sw), acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<2>(raw, sw), acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<3>(raw, sw), acc[3], 0, 0, 0);
+      acc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<4>(raw, sw), acc[4], 0, 0, 0);
+      acc[5] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<5>(raw, sw), acc[5], 0, 0, 0);
+      acc[6] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<6>(raw, sw), acc[6], 0, 0, 0);
+      acc[7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<7>(raw, sw), acc[7], 0, 0, 0);
+    }
+    // lane holds column jl, rows 4 g + v, all 8 output blades
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) part[wave][4 * g + v][jl][r] = acc[r][v];
+    __syncthreads();
+    if (tid < kDecRows * kDecJ) {
+      const int rl = tid / kDecJ, jj = tid % kDecJ;
+      const int row = r0 + rl, jo = blockIdx.y * kDecJ + jj;
+      if (row < row_end && jo < d_out) {
+        const float sc = wscale[(size_t)e * d_out + jo];
+        const bool with_bias = bias != nullptr && (!PARTIAL || split == 0);
+        float y[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          float s = 0.f;
+#pragma unroll
+          for (int w = 0; w < kDecWaves; ++w) s += part[w][rl][jj][r];
+          y[r] = (float)kOutFold(r) * s * sc + (with_bias ? bias[((size_t)e * d_out + jo) * 8 + r] : 0.f);
+        }
+        if constexpr (PARTIAL) {
+          store_out8<kF32>(Y, ((size_t)split * P_max + row) * d_out + jo, y, /*blade_order=*/true);
+        } else {
+          activate_mask_order<ACT>(y);
+          store_out8<OUT_DT>(Y, (size_t)row * d_out + jo, y, OUT_BLADE);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 kernel (VALU fused multiply-adds; LDS-staged tiles)
 // ---------------------------------------------------------------------------
 constexpr int kF32BM = 32, kF32BN = 32, kF32KI = 8;
@@ -474,6 +588,17 @@ static void launch_mfma(dim3 grid, hipStream_t st, bool out_blade, bool wi8, int
 }
 
 template <int ACT>
+static void launch_decode(dim3 grid, hipStream_t st, bool out_blade, int out_dt, const uint16_t* A, const int8_t* W,
+                          const float* sc, const float* bias, const int32_t* off, int d_in, int d_out, int P_max,
+                          void* Y) {
+#define YGG_D(OB, OD) \
+  grouped_cl_decode_i8<ACT, OB, OD, false><<<grid, 64 * kDecWaves, 0, st>>>(A, W, sc, bias, off, d_in, d_out, P_max, Y)
+  if (out_dt == kBF16) { if (out_blade) YGG_D(true, kBF16); else YGG_D(false, kBF16); }
+  else { if (out_blade) YGG_D(true, kF32); else YGG_D(false, kF32); }
+#undef YGG_D
+}
+
+template <int ACT>
 static void launch_f32(dim3 grid, hipStream_t st, bool out_blade, const float* A, const float* W, const float* bias,
                        const int32_t* off, int E, int d_in, int d_out, float* Y) {
   if (out_blade) grouped_cl_f32<ACT, true><<<grid, 256, 0, st>>>(A, W, bias, off, E, d_in, d_out, Y);
@@ -508,9 +633,21 @@ YGG_API int ygg_grouped_clifford_linear(const void* x, int P_max, const void* Wp
     }
     return check_launch("grouped_cl_f32");
   }
-  dim3 grid((P_max + kMfmaBM - 1) / kMfmaBM + E, (d_out + kMfmaBN - 1) / kMfmaBN);
   const uint16_t* A = static_cast<const uint16_t*>(x);
   const bool wi8 = format == kWI8;
+  // decode shape (at most 16 rows per expert on average, one K split): weight-streaming kernel
+  if (wi8 && P_max <= kDecRows * E && (d_in + 3) / 4 <= kDecWaves * kDecKPW) {
+    dim3 dgrid(E, (d_out + kDecJ - 1) / kDecJ, 1);
+    const int8_t* Wq = static_cast<const int8_t*>(Wp);
+    switch (act) {
+      case kActNone: launch_decode<kActNone>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
+      case kActGelu: launch_decode<kActGelu>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
+      case kActRelu: launch_decode<kActRelu>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
+      default: launch_decode<kActSigmoid>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
+    }
+    return check_launch("grouped_cl_decode_i8");
+  }
+  dim3 grid((P_max + kMfmaBM - 1) / kMfmaBM + E, (d_out + kMfmaBN - 1) / kMfmaBN);
   switch (act) {
     case kActNone: launch_mfma<kActNone>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
     case kActGelu: launch_mfma<kActGelu>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
@@ -518,6 +655,22 @@ YGG_API int ygg_grouped_clifford_linear(const void* x, int P_max, const void* Wp
     default: launch_mfma<kActSigmoid>(grid, stream, ob, wi8, y_dtype, A, Wp, scales, bias, offsets, E, d_in, d_out, y); break;
   }
   return check_launch("grouped_cl_mfma");
+}
+
+// Decode-shape int8 product with the contraction cut into ygg::decode_splits()
+// splits: y_planes (splits, P_max, d_out, 8) fp32 blade order, to be summed in
+// split order (no activation).  Used by ygg_moe_forward for the down product.
+int ygg::decode_splits(int d_in) { return ((d_in + 3) / 4 + kDecWaves * kDecKPW - 1) / (kDecWaves * kDecKPW); }
+bool ygg::decode_shape(int P_max, int E, int format) { return format == kWI8 && P_max <= kDecRows * E; }
+
+int ygg::decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
+                               const int32_t* offsets, int E, int d_in, int d_out, float* y_planes,
+                               hipStream_t stream) {
+  if (P_max == 0) return 0;
+  dim3 grid(E, (d_out + kDecJ - 1) / kDecJ, decode_splits(d_in));
+  grouped_cl_decode_i8<kActNone, true, kF32, true>
+      <<<grid, 64 * kDecWaves, 0, stream>>>(x, Wq, scales, bias, offsets, d_in, d_out, P_max, y_planes);
+  return check_launch("grouped_cl_decode_i8 (K split)");
 }
 
 // Operator boundary of the path: out[m, n] = sum_k gp(a[m, k], b[k, n]).

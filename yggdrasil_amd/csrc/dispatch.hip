@@ -126,7 +126,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_w,
                                                       const int32_t* __restrict__ slot_pos,
-                                                      const void* __restrict__ resid, void* __restrict__ out) {
+                                                      const void* __restrict__ resid, void* __restrict__ out,
+                                                      int planes, size_t plane_stride) {
   // every product is rounded before its add, as in the reference: no contraction to fma
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -158,7 +159,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s < k) {
-        const MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
+        MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
+        for (int p = 1; p < planes; ++p) {  // K-split partial planes, added in plane order
+          const MV yp = load_mv<YT>(ys, p * plane_stride + (size_t)row[s] * d + i);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) y.v[c] = y.v[c] + yp.v[c];
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc.v[c] = acc.v[c] + w[s] * y.v[c];
       }
@@ -200,14 +206,33 @@ YGG_API int ygg_dispatch(const void* x, int dtype, int N, int k, int d, const in
 
 template <int YT, int OT>
 static void launch_combine(int grid, hipStream_t st, const void* ys, int N, int k, int d, const int32_t* idx,
-                           const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask) {
+                           const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask,
+                           int planes = 1, size_t plane_stride = 0) {
+#define YGG_C(YM, RS) \
+  combine_kernel<YT, YM, OT, RS><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out, planes, plane_stride)
   if (y_mask) {
-    if (resid) combine_kernel<YT, true, OT, true><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
-    else combine_kernel<YT, true, OT, false><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+    if (resid) YGG_C(true, true);
+    else YGG_C(true, false);
   } else {
-    if (resid) combine_kernel<YT, false, OT, true><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
-    else combine_kernel<YT, false, OT, false><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out);
+    if (resid) YGG_C(false, true);
+    else YGG_C(false, false);
   }
+#undef YGG_C
+}
+
+int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
+                        const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
+                        hipStream_t stream) {
+  if (N == 0) return 0;
+  const int grid = (N + kTokPerBlock - 1) / kTokPerBlock;
+  const size_t stride = (size_t)P_max * d;
+  if (out_dtype == kF32)
+    launch_combine<kF32, kF32>(grid, stream, y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, out, false,
+                               planes, stride);
+  else
+    launch_combine<kF32, kBF16>(grid, stream, y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, out, false,
+                                planes, stride);
+  return check_launch("combine (partial planes)");
 }
 
 YGG_API int ygg_combine(const void* y_sorted, int y_dtype, int y_mask_order, int N, int k, int d,

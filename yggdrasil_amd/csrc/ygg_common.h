@@ -102,6 +102,21 @@ enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3 };
 // bf16 Pauli weight layout (pauli_gemm.hip)
 int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
 
+// decode-shape int8 products (clifford_gemm.hip): whether (P_max rows, E
+// experts, format) takes the weight-streaming kernel, its number of K splits
+// for a given d_in, and the K-split product writing fp32 partial planes
+// (splits, P_max, d_out, 8) in blade order, bias in split 0, no activation.
+bool decode_shape(int P_max, int E, int format);
+int decode_splits(int d_in);
+int decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
+                          const int32_t* offsets, int E, int d_in, int d_out, float* y_planes, hipStream_t stream);
+
+// combine of fp32 blade-order partial planes (dispatch.hip): the planes of a
+// row are added in plane order, then weighted and combined as ygg_combine does.
+int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
+                   const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
+                   hipStream_t stream);
+
 inline int dtype_size(int dt) { return dt == kF32 ? 4 : dt == kBF16 ? 2 : dt == kI8 ? 1 : 0; }
 
 }  // namespace ygg

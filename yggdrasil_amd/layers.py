@@ -173,7 +173,8 @@ class CliffordMoELayer(nn.Module):
         if logits is not None:
             logits = logits.reshape(B * T, cfg.n_experts).float().contiguous()
         res = residual.reshape(B * T, cfg.d_model, 8).contiguous() if residual is not None else None
-        ws_bytes = ops.moe_workspace_bytes(B * T, cfg.d_model, cfg.d_ff, cfg.n_experts, cfg.top_k, cfg.dtype)
+        ws_bytes = ops.moe_workspace_bytes(B * T, cfg.d_model, cfg.d_ff, cfg.n_experts, cfg.top_k, cfg.dtype,
+                                           cfg.weight_format)
         if self._workspace is None or self._workspace.numel() < ws_bytes or self._workspace.device != x.device:
             self._workspace = torch.empty((max(ws_bytes, 1),), device=x.device, dtype=torch.uint8)
         out, routing = ops.moe_forward(flat, cfg.top_k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"],

@@ -261,8 +261,8 @@ def pauli_rows_from_blade(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def moe_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype) -> int:
-    return lib().ygg_moe_workspace_bytes(Nt, d, F, E, k, DTYPE_CODE[dtype])
+def moe_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype, fmt: str) -> int:
+    return lib().ygg_moe_workspace_bytes(Nt, d, F, E, k, DTYPE_CODE[dtype], WFORMAT_CODE[fmt])
 
 
 def moe_forward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: PreparedWeights,
@@ -278,7 +278,7 @@ def moe_forward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: Prepared
         raise ValueError("expert weight shapes do not chain d -> F -> d")
     if w_up.fmt != w_down.fmt:
         raise ValueError("up and down weights must share a format")
-    ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype)
+    ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     if out is None:
