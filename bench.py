@@ -32,11 +32,13 @@ sys.path.insert(0, ROOT)
 PEAK_BF16 = 2.5e15  # dense bf16 MFMA, FLOP/s
 PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
-SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c3l": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1l": 1, "c2": 2, "c3": 3, "c3l": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
-    "c1": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="f32", logits="energy", layers=1),
+    "c1": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1),
+    # config 1 again with the fp32 8x8 L(w)-block products on the vector units (comparison)
+    "c1l": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="f32", logits="energy", layers=1),
     "c2": dict(N=16384, d=128, E=16, k=2, F=0, dtype="f32", fmt=None, logits="normal", layers=1),
     "c3": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1),
     # config 3 again with the 8x8 L(w)-block expert products (comparison; not in the default set)
@@ -170,6 +172,20 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         def down():
             ops.check(L.ygg_pauli_grouped_linear(h.data_ptr(), 1, None, N * k, P0["w_down"].data.data_ptr(), None,
                                                  r.offsets.data_ptr(), E, F, d, 0, ys.data_ptr(), 1, dt_code, st))
+    elif c["fmt"] == "pauli_f32":
+        # as above in fp32 split rows; the layer's down product splits its contraction
+        # into partial planes, the exported entry timed here writes blade rows directly
+        xp = ops.pauli_rows_from_blade_f32(x)
+        h = torch.empty((N * k, 2, 2, F, 2), device="cuda", dtype=x.dtype)
+
+        def up():
+            ops.check(L.ygg_pauli_grouped_linear_f32(xp.data_ptr(), r.perm.data_ptr(), N * k,
+                                                     P0["w_up"].data.data_ptr(), None, r.offsets.data_ptr(), E, d,
+                                                     F, 1, h.data_ptr(), 0, st))
+
+        def down():
+            ops.check(L.ygg_pauli_grouped_linear_f32(h.data_ptr(), None, N * k, P0["w_down"].data.data_ptr(), None,
+                                                     r.offsets.data_ptr(), E, F, d, 0, ys.data_ptr(), 1, st))
     else:
         xs = ops.dispatch(x, r, mask_order=True)
         h = torch.empty((N * k, F, 8), device="cuda", dtype=x.dtype)
@@ -189,6 +205,8 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     ms_route = time_fn(torch, lambda: ops.route(logits, k), steps, warmup)
     if c["fmt"] == "pauli":  # the only pass over x before the products: the Pauli conversion
         ms_disp = time_fn(torch, lambda: ops.pauli_rows_from_blade(x), steps, warmup)
+    elif c["fmt"] == "pauli_f32":
+        ms_disp = time_fn(torch, lambda: ops.pauli_rows_from_blade_f32(x), steps, warmup)
     else:
         ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, mask_order=True), steps, warmup)
     ms_comb = time_fn(torch, lambda: ops.combine(ys, r), steps, warmup)
@@ -200,7 +218,7 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     rdc_bytes = (4 * N * E + 8 * N * k + 4 * N * k) + (N * R + P * R + 4 * P) + (P * R + 8 * P + N * R)
     n_touched = int((counts > 0).sum())
     wbytes_expert = {"bf16": 2 * 2 * 8 * d * F, "pauli": 2 * 2 * 8 * d * F, "int8": 2 * 8 * d * F + 4 * (d + F),
-                     "f32": 2 * 4 * 8 * d * F}[c["fmt"]]
+                     "f32": 2 * 4 * 8 * d * F, "pauli_f32": 2 * 4 * 8 * d * F}[c["fmt"]]
     layer_flops = 2 * flops_proj
     res = dict(
         workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"], layers=c["layers"],

@@ -19,7 +19,8 @@
  *    i.e. e3 and e12 exchanged), the layout the expert products consume.
  *  - dtype codes: 0 = fp32, 1 = bf16 (activations); weight formats:
  *    0 = fp32, 1 = bf16 (dual, sign-folded), 2 = int8 per-output-channel,
- *    3 = bf16 Pauli (the weights as 2x2 complex matrices; even d_in).
+ *    3 = bf16 Pauli (the weights as 2x2 complex matrices; even d_in),
+ *    4 = fp32 Pauli (fp32 layers on the fp32 MFMA units).
  *    activation codes: 0 none, 1 gelu, 2 relu, 3 sigmoid
  *    (holograph/models/hlm_block.py:28-32).
  */
@@ -143,6 +144,21 @@ int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather,
  * d even.  Conversion helper for callers of ygg_pauli_grouped_linear. */
 int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out, ygg_stream_t stream);
 
+/* fp32 products with weights in format 4 (v_mfma_f32_32x32x2_f32):
+ * x holds fp32 "Pauli split rows" (rows, 2, 2, d_in, 2) -- see
+ * ygg_pauli_rows_from_blade_f32 -- and row r of the product reads
+ * x[gather[r]] (gather NULL: x[r]).  y_layout 0: Pauli split rows
+ * (P, 2, 2, d_out, 2) fp32; 1: blade-order fp32 rows (P, d_out, 8).
+ * bias prepared (mask order) or NULL; act as above.  Replaces
+ * CliffordLinear.forward (clifford_linear.py:101-123) of every expert, with
+ * the activation (activations.py:15-128) fused, for fp32 layers. */
+int ygg_pauli_grouped_linear_f32(const float* x, const int32_t* gather, int P_max, const float* w_prepared,
+                                 const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out,
+                                 int act, float* y, int y_layout, ygg_stream_t stream);
+
+/* Blade-order fp32 rows (rows, d, 8) -> fp32 Pauli split rows (rows, 2, 2, d, 2). */
+int ygg_pauli_rows_from_blade_f32(const float* x, int rows, int d, float* out, ygg_stream_t stream);
+
 /* ---- the whole layer ---------------------------------------------------------
  * Workspace bytes of ygg_moe_forward for activation dtype and weight format. */
 size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format);
@@ -150,7 +166,7 @@ size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int
 /* HLMBlock._moe_forward (hlm_block.py:154-183): x (N, d, 8) of dtype ->
  * out (N, d, 8) of dtype (+ residual if not NULL).  logits (N, E) or NULL
  * (then router_w/router_b give the grade-energy logits).  Expert weights
- * prepared with ygg_prepare_weights (format 0 for fp32, 1, 2 or 3 for bf16;
+ * prepared with ygg_prepare_weights (format 0 or 4 for fp32, 1, 2 or 3 for bf16;
  * format 3 gathers the token rows inside the up projection),
  * biases prepared with ygg_prepare_bias or NULL.  topk_idx/topk_w/counts/
  * offsets as in ygg_route. */

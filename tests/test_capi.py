@@ -84,13 +84,20 @@ def test_argument_errors_are_reported_not_aborted():
     assert b"dtype" in L.ygg_last_error()
     assert L.ygg_prepared_weight_bytes(2, 4, 3, 3) == 0  # odd d_in has no Pauli layout
     assert L.ygg_prepared_weight_bytes(2, 4, 6, 3) == 2 * 4 * 6 * 16
+    assert L.ygg_prepared_weight_bytes(2, 4, 3, 4) == 2 * 4 * 3 * 64  # fp32 Pauli takes odd d_in
 
 
 def test_config_validation():
     from yggdrasil_amd import MoEHLMConfig
 
     c = MoEHLMConfig(d_model=8, d_ff=16)
-    assert c.weight_format == "f32"
+    assert c.weight_format == "pauli_f32"
+    assert MoEHLMConfig(d_model=7, d_ff=5).weight_format == "pauli_f32"
+    assert MoEHLMConfig(d_model=8, d_ff=16, weight_format="f32").weight_format == "f32"
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, weight_format="pauli")
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.bfloat16, weight_format="pauli_f32")
     assert MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.bfloat16).weight_format == "pauli"
     assert MoEHLMConfig(d_model=7, d_ff=16, dtype=torch.bfloat16).weight_format == "bf16"
     with pytest.raises(ValueError):

@@ -35,6 +35,9 @@ SIGNATURES = {
     "ygg_pauli_grouped_linear": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
                                           _vp, _c_int, _c_int, _vp]),
     "ygg_pauli_rows_from_blade": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
+    "ygg_pauli_grouped_linear_f32": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                              _c_int, _vp]),
+    "ygg_pauli_rows_from_blade_f32": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
     "ygg_moe_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "ygg_moe_forward": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -56,12 +56,16 @@ extern "C" int ygg_grouped_clifford_linear(const void*, int, const void*, int, c
 extern "C" int ygg_pauli_grouped_linear(const void*, int, const int32_t*, int, const void*, const float*,
                                         const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
 extern "C" int ygg_pauli_rows_from_blade(const void*, int, int, void*, hipStream_t);
+extern "C" int ygg_pauli_rows_from_blade_f32(const float*, int, int, float*, hipStream_t);
+extern "C" int ygg_pauli_grouped_linear_f32(const float*, const int32_t*, int, const float*, const float*,
+                                            const int32_t*, int, int, int, int, float*, int, hipStream_t);
 
 // y_sorted region: bf16/fp32 rows, or for the decode-shape int8 path the fp32
 // partial planes of the K-split down product
 static size_t ys_bytes(size_t P, int E, int d, int F, int dtype, int w_format) {
   const size_t es = (dtype == kF32) ? 4 : 2;
   if (decode_shape((int)P, E, w_format)) return (size_t)decode_splits(F) * P * d * 8 * 4;
+  if (w_format == kWPauliF32) return (size_t)pauli_f32_splits((int)P, E, F, d) * P * d * 8 * 4;
   return P * d * 8 * es;
 }
 
@@ -85,7 +89,8 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
                             float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
                             size_t workspace_bytes, hipStream_t stream) {
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
-  YGG_CHECK_ARG(dtype == kF32 ? w_format == kWF32 : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
+  YGG_CHECK_ARG(dtype == kF32 ? (w_format == kWF32 || w_format == kWPauliF32)
+                             : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
                 "ygg_moe_forward: weight format %d does not match dtype %d", w_format, dtype);
   YGG_CHECK_ARG(w_format != kWPauli || (d % 2 == 0 && F % 2 == 0),
                 "ygg_moe_forward: the Pauli weight format needs even d and F (d=%d F=%d)", d, F);
@@ -117,6 +122,20 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
     logits = lg;
   }
   if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
+  if (w_format == kWPauliF32) {
+    // fp32 Pauli: x -> split rows once (x_sorted region), up gathers them through
+    // perm, down in K splits whose partial planes the combine adds in split order
+    const int splits = pauli_f32_splits((int)P, E, F, d);
+    if (ygg_pauli_rows_from_blade_f32(static_cast<const float*>(x), N, d, static_cast<float*>(xs), stream)) return -1;
+    if (ygg_pauli_grouped_linear_f32(static_cast<const float*>(xs), perm, (int)P, static_cast<const float*>(w_up), b_up,
+                                     offsets, E, d, F, act, static_cast<float*>(h), /*Pauli rows*/ 0, stream))
+      return -1;
+    if (pauli_f32_linear_partial(static_cast<const float*>(h), (int)P, static_cast<const float*>(w_down), b_down,
+                                 offsets, E, F, d, splits, static_cast<float*>(ys), stream))
+      return -1;
+    return combine_planes(static_cast<const float*>(ys), splits, (int)P, N, k, d, topk_idx, topk_w, slot_pos,
+                          residual, out, dtype, stream);
+  }
   if (w_format == kWPauli) {
     // x -> Pauli half-rows once (in the x_sorted region: N <= P rows); up: gather those
     // rows through perm inside the product -> h in Pauli half-rows; down: h -> y_sorted

@@ -1,0 +1,275 @@
+// pauli_f32.hip -- fp32 grouped CliffordLinear expert products as complex
+// GEMMs on the fp32 MFMA units of gfx950 (v_mfma_f32_32x32x2_f32).
+//
+// Replaces, for the fp32 layer, CliffordLinear.forward
+// (holograph/layers/clifford_linear.py:101-123) of every expert and the
+// grade-wise activation (holograph/layers/activations.py:15-128).  The algebra
+// is the one of pauli_gemm.hip (Cl(3,0) = 2x2 complex matrices, 32 real
+// multiply-adds per multivector pair); here every operand stays fp32.
+//
+// Layouts
+// -------
+// * Pauli split rows ("PS", fp32): GEMM row (m, b) -- column b of every
+//   multivector of token row m -- is stored as two runs, real parts then
+//   imaginary parts, each d x (c0, c1):
+//   X[(((m * 2 + b) * 2 + k) * d + i) * 2 + c],  k = 0 real, 1 imaginary.
+// * Prepared weights (format 4): per (e, j, k, i) eight floats [c][a][q]:
+//   k = 0: (u, v), k = 1: (-v, u), where u + iv = W_ji[a, c] / 2.  With
+//   v_mfma_f32_32x32x2_f32 (K = 2: lane l holds k = l / 32) the real part
+//   takes q = 0 and the imaginary part q = 1, so both B operands come from
+//   memory as they are.
+//
+// Work decomposition
+// ------------------
+// A workgroup of 4 waves owns a tile of 16 tokens (32 GEMM rows) of one
+// expert x 32 output multivectors; the waves split the contraction and add
+// their four 32x32 accumulators (a = 0, 1 x re, im) in LDS in wave order.
+// blockIdx.z optionally splits the contraction further across workgroups
+// into fp32 partial planes (no activation), which the consumer adds in split
+// order.  Deterministic throughout.
+
+#include <algorithm>
+
+#include "pauli_common.h"
+
+namespace ygg {
+
+typedef float f32x16v_t __attribute__((ext_vector_type(16)));
+
+constexpr int kF32Waves = 4;
+constexpr int kF32Tok = 16;  // tokens per tile (32 GEMM rows)
+constexpr int kF32Cols = 32;  // output multivectors per tile
+
+enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2 };
+
+__device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E, int tile, int& e, int& row0,
+                                     int& row_end) {
+  int acc = 0;
+  int beg = offsets[0];
+  for (int x = 0; x < E; ++x) {
+    const int end = offsets[x + 1];
+    const int nt = (end - beg + kF32Tok - 1) / kF32Tok;
+    if (tile < acc + nt) {
+      e = x;
+      row0 = beg + (tile - acc) * kF32Tok;
+      row_end = end;
+      return true;
+    }
+    acc += nt;
+    beg = end;
+  }
+  return false;
+}
+
+template <int ACT, int OUT>
+__global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
+    const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
+    const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
+    float* __restrict__ Y) {
+  __shared__ float4 part[kF32Waves][2 * kF32Tok][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
+  int e, row0, row_end;
+  if (!f32_find_tile(offsets, E, blockIdx.x, e, row0, row_end)) return;
+  const int col0 = blockIdx.y * kF32Cols;
+  const int split = blockIdx.z, splits = gridDim.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, k = lane >> 5;
+
+  // A operand: GEMM row (t, b) = l32, real (k = 0) or imaginary (k = 1) run
+  int m = row0 + (l32 >> 1);
+  m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
+  const int src = gather ? gather[m] : m;
+  const float* arow = X + ((size_t)(src * 2 + (l32 & 1)) * 2 + k) * d_in * 2;
+  // B operand: output column j (clamped: columns past d_out are not stored)
+  const int jc = min(col0 + l32, d_out - 1);
+  const float* wrow = Wp + ((size_t)(e * d_out + jc) * 2 + k) * d_in * 8;
+  // contraction range of this (split, wave)
+  const int per_split = (d_in + splits - 1) / splits;
+  const int is0 = split * per_split, is1 = min(d_in, is0 + per_split);
+  const int per_wave = (max(is1 - is0, 0) + kF32Waves - 1) / kF32Waves;
+  const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
+
+  f32x16v_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][q][v] = 0.f;
+#pragma unroll 4
+  for (int i = i0; i < i1; ++i) {
+    const float2 xa = *reinterpret_cast<const float2*>(arow + (size_t)i * 2);
+    const float4 w0 = *reinterpret_cast<const float4*>(wrow + (size_t)i * 8);      // c = 0
+    const float4 w1 = *reinterpret_cast<const float4*>(wrow + (size_t)i * 8 + 4);  // c = 1
+    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.x, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.y, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.z, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.w, acc[1][1], 0, 0, 0);
+    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.x, acc[0][0], 0, 0, 0);
+    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.y, acc[0][1], 0, 0, 0);
+    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.z, acc[1][0], 0, 0, 0);
+    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.w, acc[1][1], 0, 0, 0);
+  }
+  // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4
+#pragma unroll
+  for (int v = 0; v < 16; ++v)
+    part[wave][8 * (v >> 2) + 4 * k + (v & 3)][l32] =
+        make_float4(acc[0][0][v], acc[0][1][v], acc[1][0][v], acc[1][1][v]);
+  __syncthreads();
+
+#pragma unroll
+  for (int h = 0; h < (kF32Tok * kF32Cols) / (64 * kF32Waves); ++h) {
+    const int o = tid + h * 64 * kF32Waves;
+    const int t = o / kF32Cols, jj = o % kF32Cols;
+    const int row = row0 + t, j = col0 + jj;
+    if (row >= row_end || j >= d_out) continue;
+    float4 s0 = part[0][2 * t][jj], s1 = part[0][2 * t + 1][jj];  // b = 0, 1
+#pragma unroll
+    for (int w = 1; w < kF32Waves; ++w) {
+      const float4 p0 = part[w][2 * t][jj], p1 = part[w][2 * t + 1][jj];
+      s0.x += p0.x; s0.y += p0.y; s0.z += p0.z; s0.w += p0.w;
+      s1.x += p1.x; s1.y += p1.y; s1.z += p1.z; s1.w += p1.w;
+    }
+    float y[8];
+    // Y[a][b]: a = 0 -> (x, y), a = 1 -> (z, w); b from the row
+    pauli_to_blade(s0.x, s0.y, s1.x, s1.y, s0.z, s0.w, s1.z, s1.w, y);
+    if (bias != nullptr && (OUT != kF32OutPartial || split == 0)) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) y[c] += bias[((size_t)e * d_out + j) * 8 + blade_to_mask(c)];
+    }
+    if constexpr (OUT == kF32OutPauliRows) {
+      activate_blade<ACT>(y);
+      float c0[4], c1[4];
+      blade_to_pauli(y, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
+      const size_t base = (size_t)row * 4;  // (row, b, k) runs
+      *reinterpret_cast<float2*>(Y + ((base + 0) * d_out + j) * 2) = make_float2(c0[0], c0[2]);
+      *reinterpret_cast<float2*>(Y + ((base + 1) * d_out + j) * 2) = make_float2(c0[1], c0[3]);
+      *reinterpret_cast<float2*>(Y + ((base + 2) * d_out + j) * 2) = make_float2(c1[0], c1[2]);
+      *reinterpret_cast<float2*>(Y + ((base + 3) * d_out + j) * 2) = make_float2(c1[1], c1[3]);
+    } else {
+      size_t mv = (size_t)row * d_out + j;
+      if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
+      else activate_blade<ACT>(y);
+      float4* p = reinterpret_cast<float4*>(Y + mv * 8);
+      p[0] = make_float4(y[0], y[1], y[2], y[3]);
+      p[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
+  }
+}
+
+// (E, d_out, d_in, 8) fp32 blade -> format 4; one thread per (e, j, i)
+__global__ __launch_bounds__(256) void pauli_f32_prep_kernel(const float* __restrict__ W, int E, int d_out, int d_in,
+                                                             float* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)E * d_out * d_in) return;
+  const int i = (int)(n % d_in);
+  const size_t ej = n / d_in;
+  float x[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) x[c] = 0.5f * W[n * 8 + c];
+  float c0[4], c1[4];
+  blade_to_pauli(x, c0, c1);
+  // W[a][c]: (a, c) = (0, 0) M00, (0, 1) M01, (1, 0) M10, (1, 1) M11 as (u, v)
+  const float u[2][2] = {{c0[0], c1[0]}, {c0[2], c1[2]}};  // [a][c]
+  const float v[2][2] = {{c0[1], c1[1]}, {c0[3], c1[3]}};
+  float* r0 = out + ((ej * 2 + 0) * d_in + i) * 8;  // k = 0: (u, v)
+  float* r1 = out + ((ej * 2 + 1) * d_in + i) * 8;  // k = 1: (-v, u)
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      r0[(c * 2 + a) * 2 + 0] = u[a][c];
+      r0[(c * 2 + a) * 2 + 1] = v[a][c];
+      r1[(c * 2 + a) * 2 + 0] = -v[a][c];
+      r1[(c * 2 + a) * 2 + 1] = u[a][c];
+    }
+}
+
+// blade fp32 rows (rows, d, 8) -> Pauli split rows; one thread per multivector
+__global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const float* __restrict__ x, int rows, int d,
+                                                                      float* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)rows * d) return;
+  const size_t m = n / d;
+  const int i = (int)(n % d);
+  const float4 p0 = reinterpret_cast<const float4*>(x + n * 8)[0];
+  const float4 p1 = reinterpret_cast<const float4*>(x + n * 8)[1];
+  const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+  float c0[4], c1[4];
+  blade_to_pauli(v, c0, c1);
+  const size_t base = m * 4;
+  *reinterpret_cast<float2*>(out + ((base + 0) * d + i) * 2) = make_float2(c0[0], c0[2]);
+  *reinterpret_cast<float2*>(out + ((base + 1) * d + i) * 2) = make_float2(c0[1], c0[3]);
+  *reinterpret_cast<float2*>(out + ((base + 2) * d + i) * 2) = make_float2(c1[0], c1[2]);
+  *reinterpret_cast<float2*>(out + ((base + 3) * d + i) * 2) = make_float2(c1[1], c1[3]);
+}
+
+}  // namespace ygg
+
+using namespace ygg;
+
+namespace {
+template <int OUT>
+int launch_f32_act(int act, dim3 grid, hipStream_t st, const float* X, const int32_t* gather, const float* W,
+                   const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y) {
+#define YGG_F(A) pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y)
+  switch (act) {
+    case kActNone: YGG_F(kActNone); break;
+    case kActGelu: YGG_F(kActGelu); break;
+    case kActRelu: YGG_F(kActRelu); break;
+    default: YGG_F(kActSigmoid); break;
+  }
+#undef YGG_F
+  return check_launch("pauli_f32");
+}
+
+dim3 f32_grid(int P_max, int E, int d_out, int splits) {
+  return dim3((P_max + kF32Tok - 1) / kF32Tok + E, (d_out + kF32Cols - 1) / kF32Cols, splits);
+}
+}  // namespace
+
+int ygg::pauli_f32_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream) {
+  const size_t total = (size_t)E * d_out * d_in;
+  pauli_f32_prep_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(W, E, d_out, d_in,
+                                                                             static_cast<float*>(out));
+  return check_launch("pauli_f32_prep");
+}
+
+int ygg::pauli_f32_splits(int P_max, int E, int d_in, int d_out) {
+  const long long tiles = ((long long)(P_max + kF32Tok - 1) / kF32Tok + E) * ((d_out + kF32Cols - 1) / kF32Cols);
+  long long s = (256 + tiles - 1) / tiles;  // about one workgroup per CU in total
+  s = std::min<long long>(s, std::max(1, d_in / 16));
+  return (int)std::max<long long>(s, 1);
+}
+
+int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias,
+                                  const int32_t* offsets, int E, int d_in, int d_out, int splits, float* y_planes,
+                                  hipStream_t stream) {
+  if (P_max == 0) return 0;
+  return launch_f32_act<kF32OutPartial>(kActNone, f32_grid(P_max, E, d_out, splits), stream, x, nullptr, w, bias,
+                                        offsets, E, d_in, d_out, P_max, y_planes);
+}
+
+YGG_API int ygg_pauli_rows_from_blade_f32(const float* x, int rows, int d, float* out, hipStream_t stream) {
+  YGG_CHECK_ARG(rows >= 0 && d >= 1, "ygg_pauli_rows_from_blade_f32: rows=%d d=%d", rows, d);
+  if (rows == 0) return 0;
+  YGG_CHECK_ARG(x && out, "ygg_pauli_rows_from_blade_f32: null pointer");
+  const size_t n = (size_t)rows * d;
+  blade_to_pauli_f32_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(x, rows, d, out);
+  return check_launch("blade_to_pauli_f32_rows");
+}
+
+YGG_API int ygg_pauli_grouped_linear_f32(const float* x, const int32_t* gather, int P_max, const float* w,
+                                         const float* bias, const int32_t* offsets, int E, int d_in, int d_out,
+                                         int act, float* y, int y_layout, hipStream_t stream) {
+  YGG_CHECK_ARG(y_layout == kF32OutPauliRows || y_layout == kF32OutBlade,
+                "ygg_pauli_grouped_linear_f32: y layout %d", y_layout);
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_pauli_grouped_linear_f32: activation %d", act);
+  YGG_CHECK_ARG(E >= 1 && E <= 64 && P_max >= 0 && d_in >= 1 && d_out >= 1,
+                "ygg_pauli_grouped_linear_f32: bad sizes E=%d P=%d d_in=%d d_out=%d", E, P_max, d_in, d_out);
+  if (P_max == 0) return 0;
+  YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear_f32: null pointer");
+  const dim3 grid = f32_grid(P_max, E, d_out, 1);
+  if (y_layout == kF32OutPauliRows)
+    return launch_f32_act<kF32OutPauliRows>(act, grid, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
+  return launch_f32_act<kF32OutBlade>(act, grid, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
+}

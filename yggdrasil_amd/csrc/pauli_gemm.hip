@@ -53,100 +53,9 @@
 // Activation rows are gathered through the expert-grouped row index, which
 // fuses the dispatch copy into the up projection.
 
-#include "ygg_common.h"
+#include "pauli_common.h"
 
 namespace ygg {
-
-typedef __bf16 pbf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 pbf16x2_t __attribute__((ext_vector_type(2)));
-typedef float pf32x2_t __attribute__((ext_vector_type(2)));
-typedef float pf32x16_t __attribute__((ext_vector_type(16)));
-
-// ---------------------------------------------------------------------------
-// activations in blade coordinates (hardware exp2 / rcp / sqrt)
-// ---------------------------------------------------------------------------
-// sigma(z) = 1 / (1 + e^-z).  tanh-GELU:  0.5 v (1 + tanh(u)) = v sigma(2u),
-// u = sqrt(2/pi) (v + 0.044715 v^3); the magnitude gate (c / |c|) gelu(|c|)
-// is  c sigma(2 u(|c|)); tanh(t) = 2 sigma(2t) - 1.
-__device__ inline float fsigmoid(float z) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));
-}
-__device__ inline float gelu_gate(float v) {  // gelu(v) / v
-  const float k2 = 2.0f * 0.7978845608028654f;
-  return fsigmoid(k2 * (v + 0.044715f * v * v * v));
-}
-__device__ inline float ftanh(float t) { return 2.0f * fsigmoid(2.0f * t) - 1.0f; }
-
-// y: blade order 1,e1,e2,e3,e12,e13,e23,e123
-template <int ACT>
-__device__ inline void activate_blade(float* y) {
-  if constexpr (ACT == kActNone) {
-    return;
-  } else {
-    const float m1 = __builtin_amdgcn_sqrtf(y[1] * y[1] + y[2] * y[2] + y[3] * y[3] + 1e-12f);
-    const float m2 = __builtin_amdgcn_sqrtf(y[4] * y[4] + y[5] * y[5] + y[6] * y[6] + 1e-12f);
-    float f0, f1, f2;
-    if constexpr (ACT == kActGelu) {
-      f0 = gelu_gate(y[0]);
-      f1 = gelu_gate(m1);
-      f2 = gelu_gate(m2);
-      y[7] = ftanh(y[7]);
-    } else if constexpr (ACT == kActSigmoid) {
-      y[0] = fsigmoid(y[0]);
-      f0 = 1.0f;
-      f1 = fsigmoid(m1) * __builtin_amdgcn_rcpf(m1);
-      f2 = fsigmoid(m2) * __builtin_amdgcn_rcpf(m2);
-      y[7] = ftanh(y[7]);
-    } else {  // relu with zero thresholds: grade 0 clamps, the rest pass through
-      f0 = y[0] > 0.f ? 1.0f : 0.0f;
-      f1 = 1.0f;
-      f2 = 1.0f;
-    }
-    y[0] *= f0;
-    y[1] *= f1;
-    y[2] *= f1;
-    y[3] *= f1;
-    y[4] *= f2;
-    y[5] *= f2;
-    y[6] *= f2;
-  }
-}
-
-// blade -> Pauli columns: col0 = (M00, M10), col1 = (M01, M11), (re, im) each
-__device__ inline void blade_to_pauli(const float* x, float* c0, float* c1) {
-  c0[0] = x[0] + x[3];  // M00 re = s + v3
-  c0[1] = x[7] + x[4];  // M00 im = t + b12
-  c0[2] = x[1] + x[5];  // M10 re = v1 + b13
-  c0[3] = x[6] + x[2];  // M10 im = b23 + v2
-  c1[0] = x[1] - x[5];  // M01 re = v1 - b13
-  c1[1] = x[6] - x[2];  // M01 im = b23 - v2
-  c1[2] = x[0] - x[3];  // M11 re = s - v3
-  c1[3] = x[7] - x[4];  // M11 im = t - b12
-}
-
-// Pauli (already halved by the weights) -> blade.  y00 = (re, im) of Y[0][0], ...
-__device__ inline void pauli_to_blade(float y00r, float y00i, float y01r, float y01i, float y10r, float y10i,
-                                      float y11r, float y11i, float* x) {
-  x[0] = y00r + y11r;  // s
-  x[3] = y00r - y11r;  // v3
-  x[7] = y00i + y11i;  // t
-  x[4] = y00i - y11i;  // b12
-  x[1] = y10r + y01r;  // v1
-  x[5] = y10r - y01r;  // b13
-  x[6] = y10i + y01i;  // b23
-  x[2] = y10i - y01i;  // v2
-}
-
-// two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even)
-__device__ inline uint32_t pack2_bf16(float lo, float hi) {
-  const pf32x2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, pbf16x2_t));
-}
-__device__ inline float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
-__device__ inline float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
-
-// (re, im) -> (im, -re) on each bf16 pair of a dword
-__device__ inline uint32_t rot_conj(uint32_t w) { return __builtin_amdgcn_alignbit(w, w, 16) ^ 0x80000000u; }
 
 enum PauliIn : int { kInBladeGather = 0, kInPauliRows = 1 };
 enum PauliOut : int { kOutPauliRows = 0, kOutBlade = 1 };

@@ -97,10 +97,19 @@ int check_launch(const char* what);
 enum DType : int { kF32 = 0, kBF16 = 1, kI8 = 2 };
 enum Act : int { kActNone = 0, kActGelu = 1, kActRelu = 2, kActSigmoid = 3 };
 // prepared weight formats (ygg_prepare_weights)
-enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3 };
+enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3, kWPauliF32 = 4 };
 
 // bf16 Pauli weight layout (pauli_gemm.hip)
 int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
+
+// fp32 Pauli products (pauli_f32.hip): weight preparation (format 4), the
+// number of K splits the layer uses for a down product, and that K-split
+// product writing fp32 partial planes (splits, P_max, d_out, 8), blade order,
+// bias in split 0, no activation.
+int pauli_f32_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
+int pauli_f32_splits(int P_max, int E, int d_in, int d_out);
+int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias, const int32_t* offsets,
+                             int E, int d_in, int d_out, int splits, float* y_planes, hipStream_t stream);
 
 // decode-shape int8 products (clifford_gemm.hip): whether (P_max rows, E
 // experts, format) takes the weight-streaming kernel, its number of K splits

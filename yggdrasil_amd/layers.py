@@ -38,9 +38,10 @@ class MoEHLMConfig:
     top_k       k (<= 8)
     activation  'gelu' | 'relu' | 'sigmoid' (grade-wise)
     dtype       activation dtype: torch.float32 or torch.bfloat16
-    weight_format  'f32' (fp32 layers); for bf16 layers 'pauli' (the default when d_model and
-                d_ff are even: complex 2x2 weights, 32 multiply-adds per multivector pair),
-                'bf16' (8x8 L(w) blocks, 64) or 'int8' (per-output-channel int8, L(w) blocks)
+    weight_format  fp32 layers: 'pauli_f32' (the default: complex 2x2 weights on the fp32 MFMA
+                units, 32 multiply-adds per multivector pair) or 'f32' (8x8 L(w) blocks on the
+                vector units, 64); bf16 layers: 'pauli' (the default when d_model and d_ff are
+                even), 'bf16' (8x8 L(w) blocks) or 'int8' (per-output-channel int8, L(w) blocks)
     router      'energy' -- CliffordRouter's grade-energy logits (default, the reference);
                 'clifford_head' -- CliffordLinear(d -> E) then the scalar part;
                 'logits' -- the caller passes logits to forward()
@@ -64,11 +65,12 @@ class MoEHLMConfig:
             raise ValueError("dtype must be float32 or bfloat16")
         even = self.d_model % 2 == 0 and self.d_ff % 2 == 0
         if self.weight_format is None:
-            self.weight_format = "f32" if self.dtype == torch.float32 else ("pauli" if even else "bf16")
-        if self.weight_format not in ("f32", "bf16", "int8", "pauli"):
-            raise ValueError("weight_format must be 'f32', 'bf16', 'int8' or 'pauli'")
-        if (self.dtype == torch.float32) != (self.weight_format == "f32"):
-            raise ValueError("fp32 layers use 'f32' weights; bf16 layers use 'pauli', 'bf16' or 'int8'")
+            self.weight_format = "pauli_f32" if self.dtype == torch.float32 else ("pauli" if even else "bf16")
+        if self.weight_format not in ("f32", "pauli_f32", "bf16", "int8", "pauli"):
+            raise ValueError("weight_format must be 'f32', 'pauli_f32', 'bf16', 'int8' or 'pauli'")
+        if (self.dtype == torch.float32) != (self.weight_format in ("f32", "pauli_f32")):
+            raise ValueError("fp32 layers use 'pauli_f32' or 'f32' weights; bf16 layers use 'pauli', 'bf16' or "
+                             "'int8'")
         if self.weight_format == "pauli" and not even:
             raise ValueError("the 'pauli' weight format needs even d_model and d_ff")
         if not 1 <= self.n_experts <= 64 or not 1 <= self.top_k <= min(8, self.n_experts):
@@ -129,7 +131,8 @@ class CliffordMoELayer(nn.Module):
         fmt = self.cfg.weight_format
         head = None
         if self.head_weight is not None:
-            head = ops.prepare_weights(self.head_weight.detach().unsqueeze(0), "f32" if fmt == "f32" else "bf16")
+            head = ops.prepare_weights(self.head_weight.detach().unsqueeze(0),
+                                       "f32" if self.cfg.dtype == torch.float32 else "bf16")
         self._prepared = dict(
             key=self._param_versions(),
             w_up=ops.prepare_weights(self.w_up.detach(), fmt),

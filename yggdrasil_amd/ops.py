@@ -16,7 +16,7 @@ from ._native import check, lib, ptr, stream_handle
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
 ACT_CODE = {"none": 0, "gelu": 1, "relu": 2, "sigmoid": 3}
-WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2, "pauli": 3}
+WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2, "pauli": 3, "pauli_f32": 4}
 # activation row layouts of pauli_grouped_linear
 X_LAYOUT = {"blade": 0, "pauli": 1}
 Y_LAYOUT = {"pauli": 0, "blade": 1}
@@ -164,7 +164,8 @@ class PreparedWeights:
 
 
 def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
-    """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8' | 'pauli')."""
+    """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8' | 'pauli' |
+    'pauli_f32')."""
     dev = _dev(w)
     if w.dim() == 3:
         w = w.unsqueeze(0)
@@ -200,8 +201,8 @@ def grouped_clifford_linear(x_sorted: torch.Tensor, pw: PreparedWeights, offsets
                             bias_prepared: torch.Tensor | None = None, act: str = "none",
                             out_dtype: torch.dtype | None = None, out_blade_order: bool = True) -> torch.Tensor:
     """Per-expert CliffordLinear on expert-grouped rows. x_sorted: (P, d_in, 8) in mask order."""
-    if pw.fmt == "pauli":
-        raise ValueError("Pauli weights run through pauli_grouped_linear")
+    if pw.fmt in ("pauli", "pauli_f32"):
+        raise ValueError("Pauli weights run through pauli_grouped_linear / pauli_grouped_linear_f32")
     dev = _dev(x_sorted, offsets, bias_prepared)
     P = x_sorted.shape[0]
     if x_sorted.shape[1] != pw.d_in:
@@ -248,6 +249,43 @@ def pauli_grouped_linear(x: torch.Tensor, pw: PreparedWeights, offsets: torch.Te
                                          ptr(y), Y_LAYOUT[y_layout], DTYPE_CODE[y.dtype], stream_handle(dev)),
           "pauli_grouped_linear")
     return y
+
+
+def pauli_grouped_linear_f32(x: torch.Tensor, pw: PreparedWeights, offsets: torch.Tensor,
+                             bias_prepared: torch.Tensor | None = None, act: str = "none",
+                             gather: torch.Tensor | None = None, rows: int | None = None,
+                             y_layout: str = "blade") -> torch.Tensor:
+    """fp32 per-expert CliffordLinear with Pauli weights (``fmt='pauli_f32'``).
+
+    x: (rows, 2, 2, d_in, 2) fp32 Pauli split rows (see :func:`pauli_rows_from_blade_f32`);
+    output row r reads x[gather[r]] (or x[r]).  y_layout 'blade' -> (P, d_out, 8),
+    'pauli' -> (P, 2, 2, d_out, 2).
+    """
+    if pw.fmt != "pauli_f32":
+        raise ValueError("pauli_grouped_linear_f32 needs weights prepared with fmt='pauli_f32'")
+    dev = _dev(x, offsets, bias_prepared, gather)
+    if x.dtype != torch.float32 or x.dim() != 5 or x.shape[3] != pw.d_in:
+        raise ValueError(f"x must be fp32 Pauli split rows (rows, 2, 2, {pw.d_in}, 2)")
+    if rows is None:
+        rows = gather.shape[0] if gather is not None else x.shape[0]
+    shape = (rows, 2, 2, pw.d_out, 2) if y_layout == "pauli" else (rows, pw.d_out, 8)
+    y = torch.empty(shape, device=dev, dtype=torch.float32)
+    check(lib().ygg_pauli_grouped_linear_f32(ptr(x), ptr(gather), rows, ptr(pw.data), ptr(bias_prepared),
+                                             ptr(offsets), pw.E, pw.d_in, pw.d_out, ACT_CODE[act], ptr(y),
+                                             Y_LAYOUT[y_layout], stream_handle(dev)), "pauli_grouped_linear_f32")
+    return y
+
+
+def pauli_rows_from_blade_f32(x: torch.Tensor) -> torch.Tensor:
+    """(rows, d, 8) fp32 blade order -> (rows, 2, 2, d, 2) fp32 Pauli split rows."""
+    dev = _dev(x)
+    if x.dtype != torch.float32:
+        raise ValueError("fp32 rows only")
+    rows, d = x.shape[0], x.shape[1]
+    out = torch.empty((rows, 2, 2, d, 2), device=dev, dtype=torch.float32)
+    check(lib().ygg_pauli_rows_from_blade_f32(ptr(x), rows, d, ptr(out), stream_handle(dev)),
+          "pauli_rows_from_blade_f32")
+    return out
 
 
 def pauli_rows_from_blade(x: torch.Tensor) -> torch.Tensor:
