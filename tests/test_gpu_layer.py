@@ -38,7 +38,9 @@ def test_geom_matmul_operator(name):
     ("bf16", "none", 16, 64, 4, 200), ("bf16", "gelu", 128, 512, 3, 300), ("bf16", "sigmoid", 9, 40, 5, 77),
     ("int8", "gelu", 32, 64, 4, 100), ("int8", "none", 128, 96, 2, 70),
     # at most 16 rows per expert on average: the decode-shape (weight-streaming) kernel
-    ("int8", "gelu", 128, 512, 8, 60), ("int8", "sigmoid", 10, 40, 5, 30), ("int8", "none", 64, 130, 4, 50)])
+    ("int8", "gelu", 128, 512, 8, 60), ("int8", "sigmoid", 10, 40, 5, 30), ("int8", "none", 64, 130, 4, 50),
+    # decode shape with d_in above one 128-input chunk (the chunk walk), odd d_in tails
+    ("int8", "gelu", 300, 72, 4, 60), ("int8", "relu", 129, 33, 2, 30)])
 def test_grouped_clifford_linear(fmt, act, d_in, d_out, E, P):
     _, ops = _mods()
     g = np.random.default_rng(d_in * 7 + d_out + E)

@@ -67,7 +67,9 @@ def test_route_dispatch_combine_against_reference_golden():
 
 
 @pytest.mark.parametrize("N,E,k,seed", [(1, 4, 1, 0), (255, 8, 2, 1), (257, 16, 4, 2), (1000, 64, 8, 3),
-                                        (16384, 16, 2, 4), (8192, 32, 4, 5), (4096, 64, 2, 6)])
+                                        (16384, 16, 2, 4), (8192, 32, 4, 5), (4096, 64, 2, 6),
+                                        # either side of the one-workgroup path's limit (1024 tokens)
+                                        (64, 32, 2, 7), (1024, 64, 8, 8), (1025, 33, 3, 9)])
 def test_route_random_sizes(N, E, k, seed):
     r = np.random.default_rng(seed)
     _check_route(r.standard_normal((N, E), dtype=np.float32), k, E, f"random seed={seed}")

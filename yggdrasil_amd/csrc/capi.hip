@@ -149,12 +149,12 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
       return -1;
     return ygg_combine(ys, kBF16, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
   }
-  if (ygg_dispatch(x, dtype, N, k, d, slot_pos, xs, /*to_mask_order=*/1, stream)) return -1;
   if (decode_shape((int)P, E, w_format)) {
-    // decode: weight-streaming products; the down product in K splits whose fp32
-    // partial planes the combine adds in split order
-    if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
-                                    /*blade=*/0, stream))
+    // decode: weight-streaming products; the up product reads x through perm (no
+    // dispatch copy), the down product runs in K splits whose fp32 partial planes
+    // the combine adds in split order
+    if (decode_linear_gather(static_cast<const uint16_t*>(x), perm, (int)P, static_cast<const int8_t*>(w_up), s_up,
+                             b_up, offsets, E, d, F, act, static_cast<uint16_t*>(h), stream))
       return -1;
     if (decode_linear_partial(static_cast<const uint16_t*>(h), (int)P, static_cast<const int8_t*>(w_down), s_down,
                               b_down, offsets, E, F, d, static_cast<float*>(ys), stream))
@@ -162,6 +162,7 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
     return combine_planes(static_cast<const float*>(ys), decode_splits(F), (int)P, N, k, d, topk_idx, topk_w,
                           slot_pos, residual, out, dtype, stream);
   }
+  if (ygg_dispatch(x, dtype, N, k, d, slot_pos, xs, /*to_mask_order=*/1, stream)) return -1;
   if (ygg_grouped_clifford_linear(xs, (int)P, w_up, w_format, s_up, b_up, offsets, E, d, F, act, h, dtype,
                                   /*blade=*/0, stream))
     return -1;

@@ -309,103 +309,219 @@ __global__ __launch_bounds__(256, 2) void grouped_cl_mfma(const uint16_t* __rest
 // decode-shape kernel: int8 weights, a few rows per expert
 // ---------------------------------------------------------------------------
 // Weight bytes, not FLOPs, bound this shape, so the work is cut for memory
-// parallelism: one 512-thread workgroup per (expert, 16 output multivectors,
-// K split); the eight waves split the split's contraction, and every lane
-// issues all its weight loads at once (one memory latency, no serial K loop).
-// int8 is widened to bf16 in registers (exact), the 8x8 L(w) rows are built
-// as in the prefill kernel, and v_mfma_f32_16x16x32_bf16 runs over 16-row
-// blocks of the expert's rows.  The waves' partial sums are added in LDS in
-// fixed wave order.  With more than one K split each split writes an fp32
-// partial plane (scale applied, bias in split 0) and the consumer adds the
-// planes in split order -- deterministic either way.
-constexpr int kDecWaves = 8;
-constexpr int kDecJ = 16;     // output multivectors per workgroup
-constexpr int kDecRows = 16;  // rows per MFMA block
-constexpr int kDecKPW = 4;    // K steps (4 input multivectors each) per wave
+// parallelism: one 256-thread workgroup per (expert, 32 output multivectors,
+// K split).  Each wave takes 32 input multivectors of a 128-input chunk for
+// both 16-column blocks, and every lane issues its eight 16-byte weight loads
+// (input multivectors i and i + 1 of two output columns) as soon as the
+// expert's row range is known: one launch keeps the whole weight stream in
+// flight (2 workgroups per CU).  int8 is widened to bf16 in registers
+// (exact) and v_mfma_f32_16x16x32_bf16 runs over 16-row blocks of the
+// expert's rows.
+//
+// Here the 8x8 block L(w) is applied by permuting the A fragment instead of
+// the weights: with q the weight component (mask order) at a K position,
+//   y_r = kOutFold(r) * sum_q  sigma_r(q) x[q ^ r] * W'[q],
+// W' the folded prepared weights (ygg_common.h), and sigma_r(q) = -1 on
+// exactly one aligned pair of q (decode_neg_pair).  So one raw weight
+// fragment serves all eight output blades, and the eight signed permutations
+// of an A fragment (a register selection plus one XOR each) are shared by
+// the two column blocks.
+//
+// The waves' partial sums are added in LDS in fixed wave order.  The A
+// operand is either expert-grouped rows in mask order or (GATHER) the layer
+// input in blade order read through the routing permutation, the e3 / e12
+// exchange done in registers: no dispatch copy.  A split wider than one
+// chunk walks its chunks in order.  With several K splits each split writes
+// an fp32 partial plane (scale applied, bias in split 0) and the consumer
+// adds the planes in split order -- deterministic either way.
+constexpr int kDecWaves = 4;
+constexpr int kDecCB = 2;                 // 16-column blocks per workgroup
+constexpr int kDecJ = 16 * kDecCB;        // output multivectors per workgroup
+constexpr int kDecRows = 16;              // rows per MFMA block
+constexpr int kDecSteps = 4;              // steps of 8 input multivectors per wave and chunk
+constexpr int kDecChunk = kDecWaves * kDecSteps * 8;  // 128 input multivectors
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-template <int ACT, bool OUT_BLADE, int OUT_DT, bool PARTIAL>
-__global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(const uint16_t* __restrict__ A,
-                                                                      const int8_t* __restrict__ Wq,
-                                                                      const float* __restrict__ wscale,
-                                                                      const float* __restrict__ bias,
-                                                                      const int32_t* __restrict__ offsets, int d_in,
-                                                                      int d_out, int P_max, void* __restrict__ Y) {
+// residual sign of the permuted-A form: the aligned pair of K positions q
+// that is negated for output blade r
+__host__ __device__ constexpr int decode_neg_pair(int r) {
+  for (int t = 0; t < 4; ++t)
+    if (kOutFold(r) * kWFold(2 * t) * mask_product_sign(2 * t, (2 * t) ^ r) < 0) return t;
+  return -1;
+}
+constexpr bool check_decode_folding() {
+  for (int r = 0; r < 8; ++r) {
+    const int t = decode_neg_pair(r);
+    if (t < 0) return false;
+    for (int q = 0; q < 8; ++q) {
+      const int sgn = kOutFold(r) * kWFold(q) * mask_product_sign(q, q ^ r);
+      if (sgn != ((q / 2 == t) ? -1 : 1)) return false;
+    }
+  }
+  return true;
+}
+static_assert(check_decode_folding(), "permuted-A form must leave one negative aligned pair per output blade");
+
+// A_r[q] = sigma_r(q) a[q ^ r] from the packed fragment (raw) and its
+// pair-swapped copy (sw)
+template <int R>
+__device__ inline bf16x8_t permuted_a(const uint32_t (&raw)[4], const uint32_t (&sw)[4]) {
+  constexpr int tneg = decode_neg_pair(R);
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    d[t] = (R & 1) ? sw[t ^ (R >> 1)] : raw[t ^ (R >> 1)];
+    if (t == tneg) d[t] ^= 0x80008000u;
+  }
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+// bf16 components (c0 c1 | c2 c3 | c4 c5 | c6 c7) in blade order -> mask order
+// (c0 c1 | c2 c4 | c3 c5 | c6 c7)
+__device__ inline uint4 bf16x8_blade_to_mask(uint4 q) {
+  return make_uint4(q.x, (q.y & 0xffffu) | (q.z << 16), (q.y >> 16) | (q.z & 0xffff0000u), q.w);
+}
+
+// eight int8 weight components -> eight bf16 (exact)
+__device__ inline bf16x8_t i8x8_to_bf16(uint32_t lo, uint32_t hi) {
+  uint32_t d[4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t w = t == 0 ? lo : hi;
+    d[2 * t] = i8pair_to_bf16x2((int)(int8_t)(w & 0xff), (int)(int8_t)((w >> 8) & 0xff));
+    d[2 * t + 1] = i8pair_to_bf16x2((int)(int8_t)((w >> 16) & 0xff), (int)(int8_t)(w >> 24));
+  }
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+// one K step: A fragment a (mask order) against the weight fragments of both column blocks
+__device__ inline void decode_step(f32x4_t (&acc)[kDecCB][8], const uint4 a, const bf16x8_t (&b)[kDecCB]) {
+  const uint32_t raw[4] = {a.x, a.y, a.z, a.w};
+  uint32_t sw[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) sw[t] = (raw[t] >> 16) | (raw[t] << 16);
+#define YGG_STEP(R)                                                                      \
+  {                                                                                      \
+    const bf16x8_t ar = permuted_a<R>(raw, sw);                                          \
+    _Pragma("unroll") for (int cb = 0; cb < kDecCB; ++cb) acc[cb][R] =                   \
+        __builtin_amdgcn_mfma_f32_16x16x32_bf16(ar, b[cb], acc[cb][R], 0, 0, 0);         \
+  }
+  YGG_STEP(0) YGG_STEP(1) YGG_STEP(2) YGG_STEP(3) YGG_STEP(4) YGG_STEP(5) YGG_STEP(6) YGG_STEP(7)
+#undef YGG_STEP
+}
+
+template <int ACT, bool GATHER, bool OUT_BLADE, int OUT_DT, bool PARTIAL, bool MULTI>
+__global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(
+    const uint16_t* __restrict__ A, const int32_t* __restrict__ gather, const int8_t* __restrict__ Wq,
+    const float* __restrict__ wscale, const float* __restrict__ bias, const int32_t* __restrict__ offsets, int d_in,
+    int d_out, int k_split, int P_max, void* __restrict__ Y) {
   __shared__ float part[kDecWaves][kDecRows][kDecJ][9];  // +1 float of padding per multivector
   const int e = blockIdx.x, split = blockIdx.z;
   const int row_beg = offsets[e], row_end = offsets[e + 1];
   if (row_beg >= row_end) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int jl = lane & 15, g = lane >> 4;  // output column (B) / row (A) within the block; k group
-  const int j = blockIdx.y * kDecJ + jl;
+  const int jl = lane & 15, g = lane >> 4;  // output column (B) / row (A) within a block; K group
+  const int col0 = blockIdx.y * kDecJ;
   const int JB = (d_out + 31) >> 5, IP = (d_in + 1) >> 1;
-  const int KS = (d_in + 3) >> 2;  // K steps of 4 input multivectors
-  const int ks_split = kDecWaves * kDecKPW;
-  const int ks0 = split * ks_split + wave * kDecKPW;
+  const int k_lo = split * k_split, k_hi = min(d_in, k_lo + k_split);
+  const int nchunks = (k_hi - k_lo + kDecChunk - 1) / kDecChunk;
+  // Raw buffer loads (zero past the range): the weights of this expert's 32-column
+  // block (col0 is a multiple of 32; columns past d_out hold zero padding), and x.
+  const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(Wq) + (((size_t)e * JB + (col0 >> 5)) * IP) * 512, (short)0, (uint32_t)IP * 512,
+      kBufferFlags);
+  const __amdgpu_buffer_rsrc_t a_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(A), (short)0, 0x7fffffff, kBufferFlags);
 
-  // all weight loads of this lane: multivector (j, i = 4 ks + g) of expert e
-  uint2 wq[kDecKPW];
+  // weights of one chunk: step s holds input multivectors i, i + 1 (i even) of both
+  // columns (16 bytes at pair i / 2, slot 2 (16 cb + jl)); steps past k_hi read zero
+  uint4 wq[kDecSteps][kDecCB];
+  auto load_w = [&](int kc) {
 #pragma unroll
-  for (int u = 0; u < kDecKPW; ++u) {
-    const int i = 4 * (ks0 + u) + g;
-    wq[u] = make_uint2(0, 0);
-    if (ks0 + u < KS && i < d_in && j < d_out) {
-      const size_t slot = (((size_t)e * JB + (j >> 5)) * IP + (i >> 1)) * 64 + (j & 31) * 2 + (i & 1);
-      wq[u] = *reinterpret_cast<const uint2*>(Wq + slot * 8);
+    for (int s = 0; s < kDecSteps; ++s) {
+      const int i = kc + wave * (kDecSteps * 8) + 8 * s + 2 * g;
+#pragma unroll
+      for (int cb = 0; cb < kDecCB; ++cb) {
+        const uint32_t off = i < k_hi ? (uint32_t)(i >> 1) * 512 + (uint32_t)(16 * cb + jl) * 16 : kBufferOff;
+        wq[s][cb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, off, 0, 0));
+      }
     }
-  }
+  };
 
-  for (int r0 = row_beg; r0 < row_end; r0 += kDecRows) {
-    const int arow = min(r0 + jl, row_end - 1);  // rows past the expert's range are not stored
-    f32x4_t acc[8];
+  // epilogue operands, independent of the rows: thread tid owns outputs
+  // (r0 + rl, col0 + jj) for o = tid + 256 h, rl = o / kDecJ, jj = o % kDecJ
+  constexpr int kOut = kDecRows * kDecJ / (64 * kDecWaves);
+  float sc[kOut], bv[kOut][8];
+  // (raw buffer loads with no branch: a column past d_out, or no bias, reads zero,
+  // so every path issues the same loads and the waits stay exact)
+  const bool with_bias = bias != nullptr && (!PARTIAL || split == 0);
+  const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(wscale) + (size_t)e * d_out, (short)0, (uint32_t)d_out * 4, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      with_bias ? const_cast<float*>(bias) + (size_t)e * d_out * 8 : nullptr, (short)0,
+      with_bias ? (uint32_t)d_out * 32 : 0u, kBufferFlags);
+  auto load_epilogue = [&]() {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < kDecKPW; ++u) {
-      const int i = 4 * (ks0 + u) + g;
-      uint4 a = make_uint4(0, 0, 0, 0);
-      if (ks0 + u < KS && i < d_in) a = *reinterpret_cast<const uint4*>(A + ((size_t)arow * d_in + i) * 8);
-      int c[8];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        c[p] = (int)(int8_t)((wq[u].x >> (8 * p)) & 0xff);
-        c[4 + p] = (int)(int8_t)((wq[u].y >> (8 * p)) & 0xff);
-      }
-      uint32_t raw[4], sw[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        raw[t] = i8pair_to_bf16x2(c[2 * t], c[2 * t + 1]);
-        sw[t] = (raw[t] >> 16) | (raw[t] << 16);
-      }
-      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
-      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<0>(raw, sw), acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<1>(raw, sw), acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<2>(raw, sw), acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<3>(raw, sw), acc[3], 0, 0, 0);
-      acc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<4>(raw, sw), acc[4], 0, 0, 0);
-      acc[5] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<5>(raw, sw), acc[5], 0, 0, 0);
-      acc[6] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<6>(raw, sw), acc[6], 0, 0, 0);
-      acc[7] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blade_operand<7>(raw, sw), acc[7], 0, 0, 0);
+    for (int h = 0; h < kOut; ++h) {
+      const uint32_t jo = (uint32_t)(col0 + (tid + 64 * kDecWaves * h) % kDecJ);  // past d_out: reads zero
+      sc[h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rsrc, jo * 4, 0, 0));
+      const float4 b0 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, jo * 32, 0, 0));
+      const float4 b1 = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(b_rsrc, jo * 32 + 16, 0, 0));
+      bv[h][0] = b0.x; bv[h][1] = b0.y; bv[h][2] = b0.z; bv[h][3] = b0.w;
+      bv[h][4] = b1.x; bv[h][5] = b1.y; bv[h][6] = b1.z; bv[h][7] = b1.w;
     }
-    // lane holds column jl, rows 4 g + v, all 8 output blades
+  };
+
+  // one chunk of a row block: every A load goes out before the first MFMA
+  auto chunk = [&](f32x4_t (&acc)[kDecCB][8], int kc, uint32_t arow_off) {
+    uint4 af[kDecSteps][2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+    for (int s = 0; s < kDecSteps; ++s) {
+      const int i = kc + wave * (kDecSteps * 8) + 8 * s + 2 * g;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) part[wave][4 * g + v][jl][r] = acc[r][v];
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t off = i + h < k_hi ? arow_off + (uint32_t)(i + h) * 16 : kBufferOff;
+        af[s][h] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, off, 0, 0));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kDecSteps; ++s) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 a = GATHER ? bf16x8_blade_to_mask(af[s][h]) : af[s][h];
+        bf16x8_t b[kDecCB];
+#pragma unroll
+        for (int cb = 0; cb < kDecCB; ++cb)
+          b[cb] = h == 0 ? i8x8_to_bf16(wq[s][cb].x, wq[s][cb].y) : i8x8_to_bf16(wq[s][cb].z, wq[s][cb].w);
+        decode_step(acc, a, b);
+      }
+    }
+  };
+
+  // the waves' partial sums of a row block -> LDS -> scaled, biased, stored
+  auto finish = [&](f32x4_t (&acc)[kDecCB][8], int r0) {
+    // lane holds columns 16 cb + jl, rows 4 g + v, all 8 output blades
+#pragma unroll
+    for (int cb = 0; cb < kDecCB; ++cb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) part[wave][4 * g + v][16 * cb + jl][r] = acc[cb][r][v];
     __syncthreads();
-    if (tid < kDecRows * kDecJ) {
-      const int rl = tid / kDecJ, jj = tid % kDecJ;
-      const int row = r0 + rl, jo = blockIdx.y * kDecJ + jj;
+#pragma unroll
+    for (int h = 0; h < kOut; ++h) {
+      const int o = tid + 64 * kDecWaves * h;
+      const int rl = o / kDecJ, jj = o % kDecJ;
+      const int row = r0 + rl, jo = col0 + jj;
       if (row < row_end && jo < d_out) {
-        const float sc = wscale[(size_t)e * d_out + jo];
-        const bool with_bias = bias != nullptr && (!PARTIAL || split == 0);
         float y[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          float s = 0.f;
+          float sum = 0.f;
 #pragma unroll
-          for (int w = 0; w < kDecWaves; ++w) s += part[w][rl][jj][r];
-          y[r] = (float)kOutFold(r) * s * sc + (with_bias ? bias[((size_t)e * d_out + jo) * 8 + r] : 0.f);
+          for (int w = 0; w < kDecWaves; ++w) sum += part[w][rl][jj][r];
+          y[r] = (float)kOutFold(r) * sum * sc[h] + bv[h][r];
         }
         if constexpr (PARTIAL) {
           store_out8<kF32>(Y, ((size_t)split * P_max + row) * d_out + jo, y, /*blade_order=*/true);
@@ -416,6 +532,54 @@ __global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(const uin
       }
     }
     __syncthreads();
+  };
+  auto zero = [](f32x4_t (&acc)[kDecCB][8]) {
+#pragma unroll
+    for (int cb = 0; cb < kDecCB; ++cb)
+#pragma unroll
+      for (int r = 0; r < 8; ++r) acc[cb][r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  // lane row of the block at r0 (rows past the expert's range repeat its last
+  // row and are not stored); its byte offset into x is src * d_in * 16
+  auto row_src = [&](int r0) {
+    int src = min(r0 + jl, row_end - 1);
+    if constexpr (GATHER) src = gather[src];
+    return src;
+  };
+
+  if constexpr (!MULTI) {
+    // one chunk (the decode case): the weights stay in registers for every row
+    // block, and the first block's row index is loaded ahead of them (vmcnt
+    // retires in order, so its wait does not wait for the weight stream)
+    const int first = row_src(row_beg);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(k_lo);
+    load_epilogue();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      f32x4_t acc[kDecCB][8];
+      zero(acc);
+      chunk(acc, k_lo, (uint32_t)first * d_in * 16);
+      finish(acc, row_beg);
+    }
+    for (int r0 = row_beg + kDecRows; r0 < row_end; r0 += kDecRows) {
+      f32x4_t acc[kDecCB][8];
+      zero(acc);
+      chunk(acc, k_lo, (uint32_t)row_src(r0) * d_in * 16);
+      finish(acc, r0);
+    }
+  } else {
+    load_epilogue();
+    for (int r0 = row_beg; r0 < row_end; r0 += kDecRows) {
+      const uint32_t off = (uint32_t)row_src(r0) * d_in * 16;
+      f32x4_t acc[kDecCB][8];
+      zero(acc);
+      for (int c = 0; c < nchunks; ++c) {
+        load_w(k_lo + c * kDecChunk);
+        chunk(acc, k_lo + c * kDecChunk, off);
+      }
+      finish(acc, r0);
+    }
   }
 }
 
@@ -589,15 +753,44 @@ static void launch_mfma(dim3 grid, hipStream_t st, bool out_blade, bool wi8, int
 #undef YGG_L
 }
 
-template <int ACT>
-static void launch_decode(dim3 grid, hipStream_t st, bool out_blade, int out_dt, const uint16_t* A, const int8_t* W,
-                          const float* sc, const float* bias, const int32_t* off, int d_in, int d_out, int P_max,
-                          void* Y) {
-#define YGG_D(OB, OD) \
-  grouped_cl_decode_i8<ACT, OB, OD, false><<<grid, 64 * kDecWaves, 0, st>>>(A, W, sc, bias, off, d_in, d_out, P_max, Y)
-  if (out_dt == kBF16) { if (out_blade) YGG_D(true, kBF16); else YGG_D(false, kBF16); }
-  else { if (out_blade) YGG_D(true, kF32); else YGG_D(false, kF32); }
+template <int ACT, bool MULTI>
+static void launch_decode_m(dim3 grid, hipStream_t st, bool out_blade, int out_dt, const uint16_t* A,
+                            const int32_t* gather, const int8_t* W, const float* sc, const float* bias,
+                            const int32_t* off, int d_in, int d_out, int k_split, int P_max, void* Y) {
+#define YGG_D(G, OB, OD)                                                                                  \
+  grouped_cl_decode_i8<ACT, G, OB, OD, false, MULTI><<<grid, 64 * kDecWaves, 0, st>>>(A, gather, W, sc, bias, \
+                                                                                     off, d_in, d_out,     \
+                                                                                     k_split, P_max, Y)
+  if (gather) YGG_D(true, false, kBF16);  // the layer's up product: blade-order input, mask-order bf16 h
+  else if (out_dt == kBF16) { if (out_blade) YGG_D(false, true, kBF16); else YGG_D(false, false, kBF16); }
+  else { if (out_blade) YGG_D(false, true, kF32); else YGG_D(false, false, kF32); }
 #undef YGG_D
+}
+
+// the decode kernel addresses x with 32-bit byte offsets
+static bool decode_offsets_fit(int rows, int d_in) { return (long long)rows * d_in * 16 < 0x7fffffffLL; }
+
+// one 128-input chunk per workgroup (the decode case) or a walk over several
+template <int ACT>
+static void launch_decode(dim3 grid, hipStream_t st, bool out_blade, int out_dt, const uint16_t* A,
+                          const int32_t* gather, const int8_t* W, const float* sc, const float* bias,
+                          const int32_t* off, int d_in, int d_out, int k_split, int P_max, void* Y) {
+  if (k_split <= kDecChunk)
+    launch_decode_m<ACT, false>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y);
+  else
+    launch_decode_m<ACT, true>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y);
+}
+
+static int decode_dispatch(int act, dim3 grid, hipStream_t st, bool out_blade, int out_dt, const uint16_t* A,
+                           const int32_t* gather, const int8_t* W, const float* sc, const float* bias,
+                           const int32_t* off, int d_in, int d_out, int k_split, int P_max, void* Y) {
+  switch (act) {
+    case kActNone: launch_decode<kActNone>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y); break;
+    case kActGelu: launch_decode<kActGelu>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y); break;
+    case kActRelu: launch_decode<kActRelu>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y); break;
+    default: launch_decode<kActSigmoid>(grid, st, out_blade, out_dt, A, gather, W, sc, bias, off, d_in, d_out, k_split, P_max, Y); break;
+  }
+  return check_launch("grouped_cl_decode_i8");
 }
 
 template <int ACT>
@@ -637,17 +830,11 @@ YGG_API int ygg_grouped_clifford_linear(const void* x, int P_max, const void* Wp
   }
   const uint16_t* A = static_cast<const uint16_t*>(x);
   const bool wi8 = format == kWI8;
-  // decode shape (at most 16 rows per expert on average, one K split): weight-streaming kernel
-  if (wi8 && P_max <= kDecRows * E && (d_in + 3) / 4 <= kDecWaves * kDecKPW) {
-    dim3 dgrid(E, (d_out + kDecJ - 1) / kDecJ, 1);
-    const int8_t* Wq = static_cast<const int8_t*>(Wp);
-    switch (act) {
-      case kActNone: launch_decode<kActNone>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
-      case kActGelu: launch_decode<kActGelu>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
-      case kActRelu: launch_decode<kActRelu>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
-      default: launch_decode<kActSigmoid>(dgrid, stream, ob, y_dtype, A, Wq, scales, bias, offsets, d_in, d_out, P_max, y); break;
-    }
-    return check_launch("grouped_cl_decode_i8");
+  // decode shape (at most 16 rows per expert on average): weight-streaming kernel, one K split
+  if (decode_shape(P_max, E, format) && decode_offsets_fit(P_max, d_in)) {
+    const int k_split = decode_splits(d_in) * kDecChunk;
+    return decode_dispatch(act, dim3(E, (d_out + kDecJ - 1) / kDecJ, 1), stream, ob, y_dtype, A, nullptr,
+                           static_cast<const int8_t*>(Wp), scales, bias, offsets, d_in, d_out, k_split, P_max, y);
   }
   dim3 grid((P_max + kMfmaBM - 1) / kMfmaBM + E, (d_out + kMfmaBN - 1) / kMfmaBN);
   switch (act) {
@@ -659,19 +846,32 @@ YGG_API int ygg_grouped_clifford_linear(const void* x, int P_max, const void* Wp
   return check_launch("grouped_cl_mfma");
 }
 
-// Decode-shape int8 product with the contraction cut into ygg::decode_splits()
-// splits: y_planes (splits, P_max, d_out, 8) fp32 blade order, to be summed in
-// split order (no activation).  Used by ygg_moe_forward for the down product.
-int ygg::decode_splits(int d_in) { return ((d_in + 3) / 4 + kDecWaves * kDecKPW - 1) / (kDecWaves * kDecKPW); }
+// Decode-shape int8 products inside ygg_moe_forward.  decode_linear_gather:
+// the up product on the layer input (blade order, rows gathered through the
+// routing permutation), one K split, output mask-order bf16.
+// decode_linear_partial: the contraction cut into decode_splits() splits of
+// one chunk; y_planes (splits, P_max, d_out, 8) fp32 blade order, to be summed
+// in split order (no activation).
+int ygg::decode_splits(int d_in) { return (d_in + kDecChunk - 1) / kDecChunk; }
 bool ygg::decode_shape(int P_max, int E, int format) { return format == kWI8 && P_max <= kDecRows * E; }
+
+int ygg::decode_linear_gather(const uint16_t* x, const int32_t* perm, int P_max, const int8_t* Wq,
+                              const float* scales, const float* bias, const int32_t* offsets, int E, int d_in,
+                              int d_out, int act, uint16_t* h, hipStream_t stream) {
+  if (P_max == 0) return 0;
+  YGG_CHECK_ARG(decode_offsets_fit(P_max, d_in), "decode up product: %d rows x %d inputs too large", P_max, d_in);
+  return decode_dispatch(act, dim3(E, (d_out + kDecJ - 1) / kDecJ, 1), stream, false, kBF16, x, perm, Wq, scales,
+                         bias, offsets, d_in, d_out, decode_splits(d_in) * kDecChunk, P_max, h);
+}
 
 int ygg::decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
                                const int32_t* offsets, int E, int d_in, int d_out, float* y_planes,
                                hipStream_t stream) {
   if (P_max == 0) return 0;
+  YGG_CHECK_ARG(decode_offsets_fit(P_max, d_in), "decode down product: %d rows x %d inputs too large", P_max, d_in);
   dim3 grid(E, (d_out + kDecJ - 1) / kDecJ, decode_splits(d_in));
-  grouped_cl_decode_i8<kActNone, true, kF32, true>
-      <<<grid, 64 * kDecWaves, 0, stream>>>(x, Wq, scales, bias, offsets, d_in, d_out, P_max, y_planes);
+  grouped_cl_decode_i8<kActNone, false, true, kF32, true, false><<<grid, 64 * kDecWaves, 0, stream>>>(
+      x, nullptr, Wq, scales, bias, offsets, d_in, d_out, kDecChunk, P_max, y_planes);
   return check_launch("grouped_cl_decode_i8 (K split)");
 }
 

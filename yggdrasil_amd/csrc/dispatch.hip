@@ -126,8 +126,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_w,
                                                       const int32_t* __restrict__ slot_pos,
-                                                      const void* __restrict__ resid, void* __restrict__ out,
-                                                      int planes, size_t plane_stride) {
+                                                      const void* __restrict__ resid, void* __restrict__ out) {
   // every product is rounded before its add, as in the reference: no contraction to fma
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -159,12 +158,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s < k) {
-        MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
-        for (int p = 1; p < planes; ++p) {  // K-split partial planes, added in plane order
-          const MV yp = load_mv<YT>(ys, p * plane_stride + (size_t)row[s] * d + i);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) y.v[c] = y.v[c] + yp.v[c];
-        }
+        const MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc.v[c] = acc.v[c] + w[s] * y.v[c];
       }
@@ -181,6 +175,95 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     }
     store_mv<OT>(out, (size_t)t * d + i, acc);
   }
+}
+
+// Combine of K-split partial planes (fp32, blade order): one thread per
+// (token, multivector), for the small token counts of decode.  The planes of
+// a row are added in plane order, then  w_s * y_s  in ascending expert order
+// as in combine_kernel.  The loads of two slots x four planes are issued
+// together: a thread waits for memory twice (routing, then rows).
+constexpr int kPlaneBatch = 4;
+
+template <int OT, bool RESID>
+__global__ __launch_bounds__(256) void combine_planes_kernel(const float* __restrict__ ys, int N, int k, int d,
+                                                             const int32_t* __restrict__ topk_idx,
+                                                             const float* __restrict__ topk_w,
+                                                             const int32_t* __restrict__ slot_pos,
+                                                             const void* __restrict__ resid, void* __restrict__ out,
+                                                             int planes, size_t plane_stride) {
+#pragma clang fp contract(off)
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)N * d) return;
+  const int t = (int)(n / d), i = (int)(n % d);
+  int ex[8], row[8];
+  float w[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const bool on = s < k;
+    ex[s] = on ? topk_idx[(size_t)t * k + s] : 0x7fffffff;
+    row[s] = on ? slot_pos[(size_t)t * k + s] : 0;
+    w[s] = on ? topk_w[(size_t)t * k + s] : 0.f;
+  }
+  MV r;
+  if constexpr (RESID) r = load_mv<OT>(resid, n);
+#pragma unroll
+  for (int a = 1; a < 8; ++a)
+#pragma unroll
+    for (int b = a; b > 0; --b)
+      if (ex[b] < ex[b - 1]) {
+        int te = ex[b]; ex[b] = ex[b - 1]; ex[b - 1] = te;
+        int tr = row[b]; row[b] = row[b - 1]; row[b - 1] = tr;
+        float tw = w[b]; w[b] = w[b - 1]; w[b - 1] = tw;
+      }
+  MV acc;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
+  for (int s0 = 0; s0 < k; s0 += 2) {
+    MV y[2];
+    for (int p0 = 0; p0 < planes; p0 += kPlaneBatch) {
+      MV v[2][kPlaneBatch];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int su = min(s0 + u, k - 1);
+        int rs = row[0];  // row[su] without indexing the register array
+#pragma unroll
+        for (int q = 1; q < 8; ++q)
+          if (q == su) rs = row[q];
+#pragma unroll
+        for (int b = 0; b < kPlaneBatch; ++b) {  // in-range loads only; the unused ones are not added
+          const int p = min(p0 + b, planes - 1);
+          v[u][b] = load_mv<kF32>(ys, p * plane_stride + (size_t)rs * d + i);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int b = 0; b < kPlaneBatch; ++b) {
+          if (p0 + b >= planes) continue;
+          if (p0 + b == 0) {
+            y[u] = v[u][b];
+          } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) y[u].v[c] = y[u].v[c] + v[u][b].v[c];
+          }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (s0 + u >= k) continue;
+      float ws = w[0];
+#pragma unroll
+      for (int s = 1; s < 8; ++s)
+        if (s == s0 + u) ws = w[s];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc.v[c] = acc.v[c] + ws * y[u].v[c];
+    }
+  }
+  if constexpr (RESID) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc.v[c] = r.v[c] + acc.v[c];
+  }
+  store_mv<OT>(out, n, acc);
 }
 
 }  // namespace ygg
@@ -206,10 +289,8 @@ YGG_API int ygg_dispatch(const void* x, int dtype, int N, int k, int d, const in
 
 template <int YT, int OT>
 static void launch_combine(int grid, hipStream_t st, const void* ys, int N, int k, int d, const int32_t* idx,
-                           const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask,
-                           int planes = 1, size_t plane_stride = 0) {
-#define YGG_C(YM, RS) \
-  combine_kernel<YT, YM, OT, RS><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out, planes, plane_stride)
+                           const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask) {
+#define YGG_C(YM, RS) combine_kernel<YT, YM, OT, RS><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out)
   if (y_mask) {
     if (resid) YGG_C(true, true);
     else YGG_C(true, false);
@@ -224,14 +305,14 @@ int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int
                         const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
                         hipStream_t stream) {
   if (N == 0) return 0;
-  const int grid = (N + kTokPerBlock - 1) / kTokPerBlock;
+  const unsigned grid = (unsigned)(((size_t)N * d + 255) / 256);
   const size_t stride = (size_t)P_max * d;
-  if (out_dtype == kF32)
-    launch_combine<kF32, kF32>(grid, stream, y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, out, false,
-                               planes, stride);
-  else
-    launch_combine<kF32, kBF16>(grid, stream, y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, out, false,
-                                planes, stride);
+#define YGG_CP(OT, RS)                                                                                            \
+  combine_planes_kernel<OT, RS><<<grid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, \
+                                                          out, planes, stride)
+  if (out_dtype == kF32) { if (residual) YGG_CP(kF32, true); else YGG_CP(kF32, false); }
+  else { if (residual) YGG_CP(kBF16, true); else YGG_CP(kBF16, false); }
+#undef YGG_CP
   return check_launch("combine (partial planes)");
 }
 

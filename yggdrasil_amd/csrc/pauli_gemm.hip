@@ -61,8 +61,6 @@ enum PauliIn : int { kInBladeGather = 0, kInPauliRows = 1 };
 enum PauliOut : int { kOutPauliRows = 0, kOutBlade = 1 };
 
 constexpr int kPauliMaxExperts = 64;
-// buffer descriptor word 3 for gfx9-family raw buffers (32-bit data format)
-constexpr int kBufferFlags = 0x00020000;
 
 template <int WR_, int WC_, int BWT_, int BWJ_, int KC_>
 struct PauliTile {

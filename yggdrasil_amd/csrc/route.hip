@@ -40,19 +40,12 @@ constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
 constexpr int kScanMaxThreads = 1024;
 
+// The selection of one token, eight lanes per token (lane j = tid % 8):
+// probabilities, top-k and renormalised weights; lane j returns slot j
+// (expert, weight), or expert -1 for j >= k or an inactive token.
 template <int Q>  // Q = ceil(E / 8) logits per lane
-__global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
-                                                          int32_t* __restrict__ topk_idx,
-                                                          float* __restrict__ topk_w,
-                                                          int32_t* __restrict__ slot_rank,
-                                                          int32_t* __restrict__ block_hist) {
-  __shared__ int32_t wave_cnt[kSelBlock / 64][kMaxExperts];
-  const int tid = threadIdx.x;
-  const int j = tid & (kSelLanes - 1);
-  const int t = blockIdx.x * kSelTokens + tid / kSelLanes;
-  const bool active = t < N;
-  const int lane = tid & 63, wave = tid >> 6;
-
+__device__ inline void select_token(const float* __restrict__ logits, int E, int k, int t, bool active, int j,
+                                    int lane, int& out_e, float& out_w) {
   // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
   float p[Q];
   float m = -INFINITY;
@@ -148,7 +141,26 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
       my_e = sel[s];
       my_w = __fdiv_rn(wsel[s], ssum);
     }
-  if (!active) my_e = -1;
+  out_e = active ? my_e : -1;
+  out_w = my_w;
+}
+
+
+template <int Q>  // Q = ceil(E / 8) logits per lane
+__global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
+                                                          int32_t* __restrict__ topk_idx,
+                                                          float* __restrict__ topk_w,
+                                                          int32_t* __restrict__ slot_rank,
+                                                          int32_t* __restrict__ block_hist) {
+  __shared__ int32_t wave_cnt[kSelBlock / 64][kMaxExperts];
+  const int tid = threadIdx.x;
+  const int j = tid & (kSelLanes - 1);
+  const int t = blockIdx.x * kSelTokens + tid / kSelLanes;
+  const bool active = t < N;
+  const int lane = tid & 63, wave = tid >> 6;
+  int my_e;
+  float my_w;
+  select_token<Q>(logits, E, k, t, active, j, lane, my_e, my_w);
   if (my_e >= 0) {
     topk_idx[(size_t)t * k + j] = my_e;
     topk_w[(size_t)t * k + j] = my_w;
@@ -235,6 +247,103 @@ __global__ __launch_bounds__(256) void route_place(const int32_t* __restrict__ t
   perm[pos] = t;
 }
 
+// Small token counts (decode): the three steps above in one workgroup of
+// 1024 threads, with the group histograms in LDS.  Wave w selects the
+// 8-token groups w, w + 16, ...; each group's slots are ranked per expert by
+// ballot in token order, the per-expert exclusive scan over groups (a wave
+// per expert, shuffle scan) and the scan over experts follow, and every lane
+// then places its slots --
+// the same counts, offsets, permutation and slot positions as the
+// multi-block path, from one launch.
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallWaves = kSmallThreads / 64;
+constexpr int kSmallIters = 8;                                     // groups per wave
+constexpr int kSmallGroups = kSmallWaves * kSmallIters;            // 8-token groups
+constexpr int kSmallMaxN = kSmallGroups * (64 / kSelLanes);        // 1024 tokens
+
+template <int Q>
+__global__ __launch_bounds__(kSmallThreads) void route_small(const float* __restrict__ logits, int N, int E, int k,
+                                                             int32_t* __restrict__ topk_idx,
+                                                             float* __restrict__ topk_w,
+                                                             int32_t* __restrict__ counts,
+                                                             int32_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ perm,
+                                                             int32_t* __restrict__ slot_pos) {
+  __shared__ int32_t cnt[kMaxExperts][kSmallGroups];  // slots per (expert, group), then their base
+  __shared__ int32_t tot[kMaxExperts];
+  __shared__ int32_t eoff[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int j = tid & (kSelLanes - 1);
+  const int ngroups = (N + 7) / 8;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int my_e[kSmallIters], rank[kSmallIters];
+#pragma unroll
+  for (int it = 0; it < kSmallIters; ++it) {
+    const int grp = it * kSmallWaves + wave;
+    my_e[it] = -1;
+    rank[it] = 0;
+    if (grp < ngroups) {  // wave-uniform
+      const int t = grp * 8 + lane / kSelLanes;
+      float w;
+      select_token<Q>(logits, E, k, t, t < N, j, lane, my_e[it], w);
+      if (my_e[it] >= 0) {
+        topk_idx[(size_t)t * k + j] = my_e[it];
+        topk_w[(size_t)t * k + j] = w;
+      }
+      for (int x = 0; x < E; ++x) {
+        const uint64_t bal = __ballot(my_e[it] == x);
+        if (my_e[it] == x) rank[it] = __popcll(bal & lt_mask);
+        if (lane == 0) cnt[x][grp] = __popcll(bal);
+      }
+    }
+  }
+  __syncthreads();
+  // per expert (one wave each): exclusive scan of its group counts in group
+  // order; lane l holds groups 2l and 2l + 1
+  for (int x = wave; x < E; x += kSmallWaves) {
+    const int g0 = 2 * lane, g1 = g0 + 1;
+    const int c0 = g0 < ngroups ? cnt[x][g0] : 0;
+    const int c1 = g1 < ngroups ? cnt[x][g1] : 0;
+    int incl = c0 + c1;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    const int excl = incl - c0 - c1;
+    if (g0 < ngroups) cnt[x][g0] = excl;
+    if (g1 < ngroups) cnt[x][g1] = excl + c0;
+    if (lane == 63) tot[x] = incl;
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan over experts
+    const int c = lane < E ? tot[lane] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    if (lane < E) {
+      eoff[lane] = incl - c;
+      counts[lane] = c;
+      offsets[lane] = incl - c;
+    }
+    if (lane == E - 1) offsets[E] = incl;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kSmallIters; ++it) {
+    const int grp = it * kSmallWaves + wave;
+    if (my_e[it] >= 0) {
+      const int t = grp * 8 + lane / kSelLanes;
+      const int pos = eoff[my_e[it]] + cnt[my_e[it]][grp] + rank[it];
+      slot_pos[(size_t)t * k + j] = pos;
+      perm[pos] = t;
+    }
+  }
+}
+
 // Grade energy of one token -> normalised -> logits.  One wave per token;
 // lanes stride over the d multivectors, a 64-lane tree reduces the 4 sums.
 __global__ __launch_bounds__(256) void router_energy_logits_kernel(const void* __restrict__ x, int x_dtype, int N,
@@ -301,6 +410,18 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   YGG_CHECK_ARG(N == 0 || (logits && topk_idx && topk_w && perm && slot_pos && workspace),
                 "ygg_route: null pointer argument");
   YGG_CHECK_ARG(counts && offsets, "ygg_route: null counts/offsets");
+  if (N > 0 && N <= kSmallMaxN) {
+    switch ((E + 7) / 8) {
+#define YGG_SMALL(Q)                                                                                             \
+  case Q:                                                                                                        \
+    route_small<Q><<<1, kSmallThreads, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm,   \
+                                                    slot_pos);                                                   \
+    break;
+      YGG_SMALL(1) YGG_SMALL(2) YGG_SMALL(3) YGG_SMALL(4) YGG_SMALL(5) YGG_SMALL(6) YGG_SMALL(7) YGG_SMALL(8)
+#undef YGG_SMALL
+    }
+    return check_launch("route_small");
+  }
   const int nb = (N + kSelTokens - 1) / kSelTokens;
   int32_t* block_hist = static_cast<int32_t*>(workspace);
   if (nb > 0) {

@@ -90,6 +90,13 @@ __device__ inline uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
+// --- raw buffer loads ----------------------------------------------------
+// Descriptor word 3 for gfx9-family raw buffers (32-bit data format).  A raw
+// buffer load whose offset lies past the descriptor's range reads zero, so
+// tails and out-of-range lanes need no branch and no select on loaded data.
+constexpr int kBufferFlags = 0x00020000;
+constexpr uint32_t kBufferOff = 0x80000000u;  // an offset that reads zero
+
 // --- error reporting ------------------------------------------------------
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
@@ -113,10 +120,15 @@ int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const fl
 
 // decode-shape int8 products (clifford_gemm.hip): whether (P_max rows, E
 // experts, format) takes the weight-streaming kernel, its number of K splits
-// for a given d_in, and the K-split product writing fp32 partial planes
-// (splits, P_max, d_out, 8) in blade order, bias in split 0, no activation.
+// for a given d_in, the up product reading blade-order rows of x through the
+// routing permutation (mask-order bf16 output, activation fused), and the
+// K-split product writing fp32 partial planes (splits, P_max, d_out, 8) in
+// blade order, bias in split 0, no activation.
 bool decode_shape(int P_max, int E, int format);
 int decode_splits(int d_in);
+int decode_linear_gather(const uint16_t* x, const int32_t* perm, int P_max, const int8_t* Wq, const float* scales,
+                         const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act, uint16_t* h,
+                         hipStream_t stream);
 int decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
                           const int32_t* offsets, int E, int d_in, int d_out, float* y_planes, hipStream_t stream);
 
