@@ -32,6 +32,8 @@ sys.path.insert(0, ROOT)
 PEAK_BF16 = 2.5e15  # dense bf16 MFMA, FLOP/s
 PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
+# measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
+PAULI_C3_TRAFFIC_BYTES = 410.9e6
 SEEDS = {"c1": 1, "c1l": 1, "c2": 2, "c3": 3, "c3l": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
@@ -373,6 +375,11 @@ def main():
             # achieved counts the algorithmic 64 multiply-adds per multivector pair; the complex
             # (Pauli) form issues 32, so the MFMA pipes run at half that rate
             roof["mfma_issued_frac"] = ach / 2 / peak
+            if head_name == "c3":
+                # HBM bytes per launch (mean of the two products) from rocprofv3 FETCH_SIZE x 2 +
+                # WRITE_SIZE, calibrated on a device copy: profiles/pauli_gemm_c3_traffic.md
+                roof["traffic"] = PAULI_C3_TRAFFIC_BYTES
+                roof["traffic_unit"] = "bytes per launch"
     for r in results.values():
         r.pop("_flops_per_launch", None)
         r.pop("_ms_per_launch", None)
