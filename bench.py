@@ -61,6 +61,9 @@ def parse():
     # a plain device copy of this many MiB, run (3 times) before the configs: the reference
     # point that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc profile
     ap.add_argument("--calib-copy-mb", type=int, default=0)
+    # library GEMM rates (hipBLASLt through torch.matmul) on random bf16 operands at the dense
+    # shapes the C3 Pauli products issue: the practical reference for the MFMA roofline
+    ap.add_argument("--calibrate", action="store_true")
     return ap.parse_args()
 
 
@@ -241,6 +244,20 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     return res
 
 
+def calibrate_gemm(torch):
+    """hipBLASLt (torch.matmul) bf16 GEMM rates on N(0,1) operands, two timed passes per shape."""
+    out = []
+    for (M, K, N) in [(16384, 16384, 16384), (8192, 8192, 8192), (65536, 512, 2048), (65536, 2048, 512)]:
+        a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(K, N, device="cuda", dtype=torch.bfloat16)
+        for _ in range(2):
+            ms = time_fn(torch, lambda: a @ b, 20, 5)
+            out.append(dict(M=M, K=K, N=N, us=ms * 1e3, tflops=2.0 * M * K * N / (ms * 1e-3) / 1e12))
+            print(f"[calibrate] {out[-1]}", file=sys.stderr, flush=True)
+        del a, b
+    return out
+
+
 def run_c2(torch, ops, c, steps, warmup):
     x, layers = make_inputs(torch, c, seed=2)
     logits = layers[0]["logits"]
@@ -339,6 +356,9 @@ def main():
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU"}))
         sys.exit(1)
+    if args.calibrate:
+        print(json.dumps({"calibration": calibrate_gemm(torch)}))
+        return
     names = [s.strip() for s in args.configs.split(",") if s.strip()]
     if args.calib_copy_mb:
         n = args.calib_copy_mb << 18  # fp32 elements
