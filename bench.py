@@ -207,14 +207,16 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
 
     ms_up = time_fn(torch, up, steps, warmup)
     ms_down = time_fn(torch, down, steps, warmup)
-    ms_route = time_fn(torch, lambda: ops.route(logits, k), steps, warmup)
+    ms_route = time_route(torch, ops, logits, k, steps, warmup)
     if c["fmt"] == "pauli":  # the only pass over x before the products: the Pauli conversion
         ms_disp = time_fn(torch, lambda: ops.pauli_rows_from_blade(x), steps, warmup)
     elif c["fmt"] == "pauli_f32":
         ms_disp = time_fn(torch, lambda: ops.pauli_rows_from_blade_f32(x), steps, warmup)
     else:
-        ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, mask_order=True), steps, warmup)
-    ms_comb = time_fn(torch, lambda: ops.combine(ys, r), steps, warmup)
+        xs_t = ops.dispatch(x, r, mask_order=True)
+        ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, mask_order=True, out=xs_t), steps, warmup)
+    out_t = torch.empty_like(x)
+    ms_comb = time_fn(torch, lambda: ops.combine(ys, r, out=out_t), steps, warmup)
 
     P = N * k
     flops_proj = 128.0 * d * F * P  # per projection (algorithmic)
@@ -258,22 +260,38 @@ def calibrate_gemm(torch):
     return out
 
 
+def time_route(torch, ops, logits, k, steps, warmup):
+    """ygg_route alone, through the C ABI with preallocated outputs (no per-call allocation)."""
+    N, E = logits.shape
+    r = ops.route(logits, k)
+    L = ops.lib()
+    ws_bytes = L.ygg_route_workspace_bytes(N, E, k)
+    ws = torch.empty((max(ws_bytes, 1),), device="cuda", dtype=torch.uint8)
+    args = (logits.data_ptr(), N, E, k, r.topk_idx.data_ptr(), r.topk_w.data_ptr(), r.counts.data_ptr(),
+            r.offsets.data_ptr(), r.perm.data_ptr(), r.slot_pos.data_ptr(), ws.data_ptr(), ws_bytes,
+            ops.stream_handle())
+    return time_fn(torch, lambda: L.ygg_route(*args), steps, warmup)
+
+
 def run_c2(torch, ops, c, steps, warmup):
     x, layers = make_inputs(torch, c, seed=2)
     logits = layers[0]["logits"]
     N, E, k, d = c["N"], c["E"], c["k"], c["d"]
+    # buffers allocated once, as a caller of the path would: the step is route -> dispatch -> combine
     r = ops.route(logits, k)
+    ws = torch.empty((max(ops.lib().ygg_route_workspace_bytes(N, E, k), 1),), device="cuda", dtype=torch.uint8)
     xs = ops.dispatch(x, r)
+    out = torch.empty_like(x)
 
     def step():
-        rr = ops.route(logits, k)
-        xx = ops.dispatch(x, rr)
-        ops.combine(xx, rr)
+        ops.route(logits, k, out=r, workspace=ws)
+        ops.dispatch(x, r, out=xs)
+        ops.combine(xs, r, out=out)
 
     ms = time_fn(torch, step, steps, warmup)
-    ms_route = time_fn(torch, lambda: ops.route(logits, k), steps, warmup)
-    ms_disp = time_fn(torch, lambda: ops.dispatch(x, r), steps, warmup)
-    ms_comb = time_fn(torch, lambda: ops.combine(xs, r), steps, warmup)
+    ms_route = time_route(torch, ops, logits, k, steps, warmup)
+    ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, out=xs), steps, warmup)
+    ms_comb = time_fn(torch, lambda: ops.combine(xs, r, out=out), steps, warmup)
     R = d * 8 * 4
     P = N * k
     b_route = 4 * N * E + 8 * N * k + 4 * N * k

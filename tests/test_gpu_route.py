@@ -167,3 +167,29 @@ def test_route_rejects_bad_arguments():
         ops.route(torch.zeros((4, 65), device="cuda"), 2)  # E > 64
     with pytest.raises(NativeLibraryError):
         ops.route(torch.zeros((4, 8), device="cuda"), 9)  # k > 8
+
+
+def test_route_dispatch_combine_reuse_out_buffers():
+    """out= / workspace= buffers are filled in place and give the same results as fresh ones."""
+    ops = _ops()
+    r = np.random.default_rng(31)
+    N, E, k, d = 300, 16, 2, 5
+    logits = torch.from_numpy(r.standard_normal((N, E), dtype=np.float32)).cuda()
+    x = torch.from_numpy(r.standard_normal((N, d, 8), dtype=np.float32)).cuda()
+    say("route/dispatch/combine out= buffers")
+    fresh = ops.route(logits, k)
+    xs_f = ops.dispatch(x, fresh)
+    out_f = ops.combine(xs_f, fresh)
+    reuse = ops.route(torch.zeros_like(logits), k)  # filled with other values first
+    ws = torch.empty(ops.lib().ygg_route_workspace_bytes(N, E, k), device="cuda", dtype=torch.uint8)
+    xs = torch.full_like(xs_f, 7.0)
+    out = torch.full_like(out_f, 7.0)
+    got = ops.route(logits, k, out=reuse, workspace=ws)
+    assert got is reuse
+    assert ops.dispatch(x, got, out=xs) is xs
+    assert ops.combine(xs, got, out=out) is out
+    for a, b in [(got.topk_idx, fresh.topk_idx), (got.perm, fresh.perm), (got.slot_pos, fresh.slot_pos),
+                 (got.counts, fresh.counts), (got.offsets, fresh.offsets), (xs, xs_f), (out, out_f)]:
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        ops.dispatch(x, got, out=torch.empty(N, d, 8, device="cuda"))

@@ -102,6 +102,7 @@ __device__ inline void store_raw(void* base, size_t mv_index, const RawMV<DT>& r
 }
 
 constexpr int kTokPerBlock = 4;  // one wave per token
+constexpr int kDispU = 4;        // multivectors per lane per dispatch round
 
 template <int DT, bool TO_MASK>
 __global__ __launch_bounds__(256) void dispatch_kernel(const void* __restrict__ x, int N, int k, int d,
@@ -110,14 +111,23 @@ __global__ __launch_bounds__(256) void dispatch_kernel(const void* __restrict__ 
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * kTokPerBlock + (threadIdx.x >> 6);
   if (t >= N) return;
-  int dst[8];
+  int dst[8];  // slots past k repeat the last one (unconditional loads: one round trip)
 #pragma unroll
-  for (int s = 0; s < 8; ++s) dst[s] = (s < k) ? slot_pos[(size_t)t * k + s] : 0;
-  for (int i = lane; i < d; i += 64) {
-    const RawMV<DT> r = load_raw<DT, TO_MASK>(x, (size_t)t * d + i);
+  for (int s = 0; s < 8; ++s) dst[s] = slot_pos[(size_t)t * k + min(s, k - 1)];
+  // kDispU multivectors per lane are loaded before any is stored, so a wave
+  // keeps that many 16/32-byte reads in flight instead of one
+  for (int i0 = lane; i0 < d; i0 += 64 * kDispU) {
+    RawMV<DT> r[kDispU];
+#pragma unroll
+    for (int u = 0; u < kDispU; ++u)
+      if (i0 + 64 * u < d) r[u] = load_raw<DT, TO_MASK>(x, (size_t)t * d + i0 + 64 * u);
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      if (s < k) store_raw<DT>(xs, (size_t)dst[s] * d + i, r);
+      if (s < k) {
+#pragma unroll
+        for (int u = 0; u < kDispU; ++u)
+          if (i0 + 64 * u < d) store_raw<DT>(xs, (size_t)dst[s] * d + i0 + 64 * u, r[u]);
+      }
   }
 }
 
@@ -135,11 +145,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
   int ex[8], row[8];
   float w[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
+    const size_t f = (size_t)t * k + min(s, k - 1);
+    const int e = topk_idx[f], rw = slot_pos[f];
+    const float ws = topk_w[f];
     const bool on = s < k;
-    ex[s] = on ? topk_idx[(size_t)t * k + s] : 0x7fffffff;
-    row[s] = on ? slot_pos[(size_t)t * k + s] : 0;
-    w[s] = on ? topk_w[(size_t)t * k + s] : 0.f;
+    ex[s] = on ? e : 0x7fffffff;
+    row[s] = on ? rw : 0;
+    w[s] = on ? ws : 0.f;
   }
   // ascending expert order (insertion sort over <= 8 slots; distinct experts)
 #pragma unroll
@@ -198,11 +211,14 @@ __global__ __launch_bounds__(256) void combine_planes_kernel(const float* __rest
   int ex[8], row[8];
   float w[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
+    const size_t f = (size_t)t * k + min(s, k - 1);
+    const int e = topk_idx[f], rw = slot_pos[f];
+    const float ws = topk_w[f];
     const bool on = s < k;
-    ex[s] = on ? topk_idx[(size_t)t * k + s] : 0x7fffffff;
-    row[s] = on ? slot_pos[(size_t)t * k + s] : 0;
-    w[s] = on ? topk_w[(size_t)t * k + s] : 0.f;
+    ex[s] = on ? e : 0x7fffffff;
+    row[s] = on ? rw : 0;
+    w[s] = on ? ws : 0.f;
   }
   MV r;
   if constexpr (RESID) r = load_mv<OT>(resid, n);

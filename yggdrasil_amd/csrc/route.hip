@@ -23,7 +23,8 @@
 //                    in token order; the rank goes to slot_pos and the block
 //                    histogram to the workspace.
 //   K2 route_scan    one workgroup: for every expert, the exclusive scan of the
-//                    block histograms over blocks (in place), counts, offsets.
+//                    block histograms over blocks (in place; a wave per expert,
+//                    shuffle scans), counts, offsets.
 //   K3 route_place   one thread per slot: slot_pos += offsets[e] + block base;
 //                    perm[slot_pos] = token.
 // Within an expert the rows are in ascending token order, the reference's
@@ -184,65 +185,68 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
     int c = 0;
 #pragma unroll
     for (int w = 0; w < kSelBlock / 64; ++w) c += wave_cnt[w][tid];
-    block_hist[(size_t)blockIdx.x * E + tid] = c;
+    block_hist[(size_t)tid * gridDim.x + blockIdx.x] = c;  // expert-major: [E][blocks]
   }
 }
 
-// One workgroup of EP x G threads (EP = E rounded up to a power of two, G <= 64
-// threads per expert).  Thread (g, e) owns a contiguous range of blocks.
+// One workgroup of 1024 threads.  Wave w scans experts w, w + 16, ...: lane l
+// owns the contiguous blocks [l per, (l + 1) per) of the expert-major block
+// histograms, sums them, a shuffle scan over the lanes gives each lane's base,
+// and the lane rewrites its blocks with their exclusive prefix.  Wave 0 then
+// scans the expert totals into counts and offsets.
 __global__ __launch_bounds__(kScanMaxThreads) void route_scan(int32_t* __restrict__ block_hist, int nblocks, int E,
-                                                              int EP, int32_t* __restrict__ counts,
+                                                              int32_t* __restrict__ counts,
                                                               int32_t* __restrict__ offsets) {
-  __shared__ int32_t part[kScanMaxThreads];
   __shared__ int32_t tot[kMaxExperts];
-  const int tid = threadIdx.x;
-  const int e = tid % EP, g = tid / EP;
-  const int G = blockDim.x / EP;
-  const int per = (nblocks + G - 1) / G;
-  const int b0 = g * per, b1 = min(nblocks, b0 + per);
-  int s = 0;
-  if (e < E)
-    for (int b = b0; b < b1; ++b) s += block_hist[(size_t)b * E + e];
-  part[tid] = s;
-  __syncthreads();
-  if (g == 0) {  // exclusive scan over the G ranges of expert e
-    int run = 0;
-    for (int h = 0; h < G; ++h) {
-      const int v = part[h * EP + e];
-      part[h * EP + e] = run;
-      run += v;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (nblocks + 63) / 64;
+  for (int x = wave; x < E; x += kScanMaxThreads / 64) {
+    int32_t* h = block_hist + (size_t)x * nblocks;
+    const int b0 = min(nblocks, lane * per), b1 = min(nblocks, b0 + per);
+    int sum = 0;
+#pragma unroll 8
+    for (int b = b0; b < b1; ++b) sum += h[b];
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
     }
-    if (e < E) tot[e] = run;
-  }
-  __syncthreads();
-  if (e < E) {
-    int run = part[tid];
+    if (lane == 63) tot[x] = incl;
+    int run = incl - sum;
+#pragma unroll 8
     for (int b = b0; b < b1; ++b) {
-      const int v = block_hist[(size_t)b * E + e];
-      block_hist[(size_t)b * E + e] = run;
+      const int v = h[b];
+      h[b] = run;
       run += v;
     }
   }
-  if (tid == 0) {
-    int acc = 0;
-    for (int x = 0; x < E; ++x) {
-      counts[x] = tot[x];
-      offsets[x] = acc;
-      acc += tot[x];
+  __syncthreads();
+  if (wave == 0) {
+    const int c = lane < E ? tot[lane] : 0;
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
     }
-    offsets[E] = acc;
+    if (lane < E) {
+      counts[lane] = c;
+      offsets[lane] = incl - c;
+    }
+    if (lane == E - 1) offsets[E] = incl;
   }
 }
 
 __global__ __launch_bounds__(256) void route_place(const int32_t* __restrict__ topk_idx,
                                                    const int32_t* __restrict__ block_base,
-                                                   const int32_t* __restrict__ offsets, int N, int E, int k,
+                                                   const int32_t* __restrict__ offsets, int N, int nblocks, int k,
                                                    int32_t* __restrict__ perm, int32_t* __restrict__ slot_pos) {
   const size_t f = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (f >= (size_t)N * k) return;
   const int t = (int)(f / k);
   const int e = topk_idx[f];
-  const int pos = offsets[e] + block_base[(size_t)(t / kSelTokens) * E + e] + slot_pos[f];
+  const int pos = offsets[e] + block_base[(size_t)e * nblocks + t / kSelTokens] + slot_pos[f];
   slot_pos[f] = pos;
   perm[pos] = t;
 }
@@ -436,14 +440,11 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
     }
     if (check_launch("route_select")) return -1;
   }
-  int EP = 1;
-  while (EP < E) EP <<= 1;
-  const int G = min(64, kScanMaxThreads / EP);
-  route_scan<<<1, EP * G, 0, stream>>>(block_hist, nb, E, EP, counts, offsets);
+  route_scan<<<1, kScanMaxThreads, 0, stream>>>(block_hist, nb, E, counts, offsets);
   if (check_launch("route_scan")) return -1;
   if (nb > 0) {
     const size_t slots = (size_t)N * k;
-    route_place<<<(unsigned)((slots + 255) / 256), 256, 0, stream>>>(topk_idx, block_hist, offsets, N, E, k, perm,
+    route_place<<<(unsigned)((slots + 255) / 256), 256, 0, stream>>>(topk_idx, block_hist, offsets, N, nb, k, perm,
                                                                      slot_pos);
     if (check_launch("route_place")) return -1;
   }

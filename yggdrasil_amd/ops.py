@@ -96,8 +96,12 @@ def router_energy_logits(x: torch.Tensor, router_weight: torch.Tensor, router_bi
     return (logits, energy) if return_energy else logits
 
 
-def route(logits: torch.Tensor, k: int) -> Routing:
-    """Softmax, top-k (lowest index wins ties) and the expert counting sort."""
+def route(logits: torch.Tensor, k: int, out: Routing | None = None, workspace: torch.Tensor | None = None) -> Routing:
+    """Softmax, top-k (lowest index wins ties) and the expert counting sort.
+
+    ``out`` (a Routing of the right shapes) and ``workspace`` (at least
+    ``ygg_route_workspace_bytes`` bytes) are reused when given: no allocation then.
+    """
     dev = _dev(logits)
     if logits.dtype != torch.float32 or logits.dim() != 2:
         raise ValueError("logits must be (N, E) float32")
@@ -105,33 +109,44 @@ def route(logits: torch.Tensor, k: int) -> Routing:
     L = lib()
     ws_bytes = L.ygg_route_workspace_bytes(Nt, E, k)
     i32 = dict(device=dev, dtype=torch.int32)
-    r = Routing(
-        topk_idx=torch.empty((Nt, k), **i32),
-        topk_w=torch.empty((Nt, k), device=dev, dtype=torch.float32),
-        counts=torch.empty((E,), **i32),
-        offsets=torch.empty((E + 1,), **i32),
-        perm=torch.empty((Nt * k,), **i32),
-        slot_pos=torch.empty((Nt, k), **i32),
-    )
-    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    if out is not None:
+        if tuple(out.topk_idx.shape) != (Nt, k) or out.counts.numel() != E:
+            raise ValueError("out routing buffers do not match (N, E, k)")
+        r = out
+    else:
+        r = Routing(
+            topk_idx=torch.empty((Nt, k), **i32),
+            topk_w=torch.empty((Nt, k), device=dev, dtype=torch.float32),
+            counts=torch.empty((E,), **i32),
+            offsets=torch.empty((E + 1,), **i32),
+            perm=torch.empty((Nt * k,), **i32),
+            slot_pos=torch.empty((Nt, k), **i32),
+        )
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else \
+        torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     check(L.ygg_route(ptr(logits), Nt, E, k, ptr(r.topk_idx), ptr(r.topk_w), ptr(r.counts), ptr(r.offsets),
                       ptr(r.perm), ptr(r.slot_pos), ptr(ws), ws_bytes, stream_handle(dev)), "route")
     return r
 
 
-def dispatch(x: torch.Tensor, routing: Routing, mask_order: bool = False) -> torch.Tensor:
+def dispatch(x: torch.Tensor, routing: Routing, mask_order: bool = False,
+             out: torch.Tensor | None = None) -> torch.Tensor:
     """Expert-grouped copy of the token rows: ``out[slot_pos[t, s]] = x[t]``. x: (N, d, 8)."""
     dev = _dev(x)
     Nt, d = x.shape[0], x.shape[1]
     k = routing.k
-    out = torch.empty((Nt * k, d, 8), device=dev, dtype=x.dtype)
+    if out is None:
+        out = torch.empty((Nt * k, d, 8), device=dev, dtype=x.dtype)
+    elif tuple(out.shape) != (Nt * k, d, 8) or out.dtype != x.dtype:
+        raise ValueError("out must be (N*k, d, 8) of x's dtype")
     check(lib().ygg_dispatch(ptr(x), _dtype_code(x), Nt, k, d, ptr(routing.slot_pos), ptr(out), int(mask_order),
                              stream_handle(dev)), "dispatch")
     return out
 
 
 def combine(y_sorted: torch.Tensor, routing: Routing, residual: torch.Tensor | None = None,
-            y_mask_order: bool = False, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+            y_mask_order: bool = False, out_dtype: torch.dtype | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
     """Weighted combine in ascending expert order (+ residual). y_sorted: (N*k, d, 8)."""
     dev = _dev(y_sorted, residual)
     Nt, k = routing.topk_idx.shape
@@ -139,7 +154,10 @@ def combine(y_sorted: torch.Tensor, routing: Routing, residual: torch.Tensor | N
     out_dtype = out_dtype or y_sorted.dtype
     if residual is not None and residual.dtype != out_dtype:
         raise ValueError("residual dtype must equal the output dtype")
-    out = torch.empty((Nt, d, 8), device=dev, dtype=out_dtype)
+    if out is None:
+        out = torch.empty((Nt, d, 8), device=dev, dtype=out_dtype)
+    elif tuple(out.shape) != (Nt, d, 8) or out.dtype != out_dtype:
+        raise ValueError("out must be (N, d, 8) of the output dtype")
     check(lib().ygg_combine(ptr(y_sorted), _dtype_code(y_sorted), int(y_mask_order), Nt, k, d,
                             ptr(routing.topk_idx), ptr(routing.topk_w), ptr(routing.slot_pos), ptr(residual),
                             ptr(out), DTYPE_CODE[out_dtype], stream_handle(dev)), "combine")
