@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void route_place(const int32_t* __restrict__ t
 // multi-block path, from one launch.
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallWaves = kSmallThreads / 64;
-constexpr int kSmallIters = 8;                                     // groups per wave
+constexpr int kSmallIters = 8;                                     // groups per wave at most
 constexpr int kSmallGroups = kSmallWaves * kSmallIters;            // 8-token groups
 constexpr int kSmallMaxN = kSmallGroups * (64 / kSelLanes);        // 1024 tokens
 
@@ -280,25 +280,24 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
   const int j = tid & (kSelLanes - 1);
   const int ngroups = (N + 7) / 8;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int my_e[kSmallIters], rank[kSmallIters];
-#pragma unroll
-  for (int it = 0; it < kSmallIters; ++it) {
-    const int grp = it * kSmallWaves + wave;
-    my_e[it] = -1;
-    rank[it] = 0;
-    if (grp < ngroups) {  // wave-uniform
-      const int t = grp * 8 + lane / kSelLanes;
-      float w;
-      select_token<Q>(logits, E, k, t, t < N, j, lane, my_e[it], w);
-      if (my_e[it] >= 0) {
-        topk_idx[(size_t)t * k + j] = my_e[it];
-        topk_w[(size_t)t * k + j] = w;
-      }
-      for (int x = 0; x < E; ++x) {
-        const uint64_t bal = __ballot(my_e[it] == x);
-        if (my_e[it] == x) rank[it] = __popcll(bal & lt_mask);
-        if (lane == 0) cnt[x][grp] = __popcll(bal);
-      }
+  // a real loop (not unrolled): this kernel runs once per layer call, cold, and
+  // its instruction fetch, not its arithmetic, sets its latency
+#pragma unroll 1
+  for (int grp = wave; grp < ngroups; grp += kSmallWaves) {
+    const int t = grp * 8 + lane / kSelLanes;
+    int e;
+    float w;
+    select_token<Q>(logits, E, k, t, t < N, j, lane, e, w);
+    int rank = 0;
+    for (int x = 0; x < E; ++x) {
+      const uint64_t bal = __ballot(e == x);
+      if (e == x) rank = __popcll(bal & lt_mask);
+      if (lane == 0) cnt[x][grp] = __popcll(bal);
+    }
+    if (e >= 0) {  // rank within the group for now; the placement below turns it into the row
+      topk_idx[(size_t)t * k + j] = e;
+      topk_w[(size_t)t * k + j] = w;
+      slot_pos[(size_t)t * k + j] = rank;
     }
   }
   __syncthreads();
@@ -336,13 +335,15 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
     if (lane == E - 1) offsets[E] = incl;
   }
   __syncthreads();
-#pragma unroll
-  for (int it = 0; it < kSmallIters; ++it) {
-    const int grp = it * kSmallWaves + wave;
-    if (my_e[it] >= 0) {
-      const int t = grp * 8 + lane / kSelLanes;
-      const int pos = eoff[my_e[it]] + cnt[my_e[it]][grp] + rank[it];
-      slot_pos[(size_t)t * k + j] = pos;
+  // each thread revisits exactly the slots it selected above (same group order)
+#pragma unroll 1
+  for (int grp = wave; grp < ngroups; grp += kSmallWaves) {
+    const int t = grp * 8 + lane / kSelLanes;
+    if (t < N && j < k) {
+      const size_t f = (size_t)t * k + j;
+      const int e = topk_idx[f];
+      const int pos = eoff[e] + cnt[e][grp] + slot_pos[f];
+      slot_pos[f] = pos;
       perm[pos] = t;
     }
   }
