@@ -77,6 +77,16 @@ int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float
               int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
               ygg_stream_t stream);
 
+/* CliffordRouter.forward end to end (holograph/layers/clifford_router.py:54-104)
+ * plus the slot grouping of hlm_block.py:165-177: the grade-energy logits of
+ * ygg_router_energy_logits followed by ygg_route, with the same outputs.  Up to
+ * 1024 tokens this is a single launch and logits_scratch is not touched; beyond,
+ * logits_scratch (N x E fp32) and the ygg_route workspace carry the logits. */
+int ygg_route_energy(const void* x, int x_dtype, int N, int d, const float* router_w, const float* router_b, int E,
+                     int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                     int32_t* slot_pos, float* logits_scratch, void* workspace, size_t workspace_bytes,
+                     ygg_stream_t stream);
+
 /* ---- dispatch / combine ----------------------------------------------------
  * x_sorted[slot_pos[t, s]] = x[t]  (rows of d multivectors, dtype 0/1);
  * to_mask_order != 0 stores the rows in mask order.

@@ -193,3 +193,30 @@ def test_route_dispatch_combine_reuse_out_buffers():
         assert torch.equal(a, b)
     with pytest.raises(ValueError):
         ops.dispatch(x, got, out=torch.empty(N, d, 8, device="cuda"))
+
+
+@pytest.mark.parametrize("N,d,E,k,dtype", [(256, 64, 8, 2, "f32"), (1024, 16, 64, 8, "f32"), (37, 9, 5, 3, "bf16"),
+                                           (1500, 32, 16, 2, "f32"), (700, 128, 32, 4, "bf16")])
+def test_route_energy_fused_against_oracle(N, d, E, k, dtype):
+    """CliffordRouter.forward in one call: indices exact, weights to 1e-5 against the oracle's
+    energy logits; up to 1024 tokens the logits are computed inside the routing kernel."""
+    ops = _ops()
+    r = np.random.default_rng(N + d + E)
+    x = r.standard_normal((N, d, 8), dtype=np.float32) * r.uniform(0.2, 3.0, size=(1, 1, 8)).astype(np.float32)
+    rw = (0.5 * r.standard_normal((E, 4))).astype(np.float32)
+    rb = (0.1 * r.standard_normal(E)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    if dtype == "bf16":
+        xt = xt.bfloat16()
+        x = xt.float().cpu().numpy()
+    say(f"route_energy N={N} d={d} E={E} k={k} {dtype}")
+    got = ops.route_energy(xt, torch.from_numpy(rw).cuda(), torch.from_numpy(rb).cuda(), k)
+    logits, _ = moe.router_logits(x, rw, rb)
+    idx_o, w_o = moe.route_topk(moe.softmax(logits), k)
+    assert np.array_equal(got.topk_idx.cpu().numpy(), idx_o)
+    assert np.allclose(got.topk_w.cpu().numpy(), w_o, rtol=1e-5, atol=1e-7)
+    # the counting sort matches the one run on the oracle's logits through ygg_route
+    ref = ops.route(torch.from_numpy(logits.astype(np.float32)).cuda(), k)
+    for a, b in [(got.perm, ref.perm), (got.slot_pos, ref.slot_pos), (got.counts, ref.counts),
+                 (got.offsets, ref.offsets)]:
+        assert torch.equal(a, b)

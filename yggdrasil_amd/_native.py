@@ -25,6 +25,8 @@ SIGNATURES = {
     "ygg_router_energy_logits": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "ygg_route_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "ygg_route": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "ygg_route_energy": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _vp, _vp, _c_size, _vp]),
     "ygg_dispatch": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp]),
     "ygg_combine": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp]),
     "ygg_prepared_weight_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),

@@ -46,8 +46,8 @@ YGG_API int ygg_version(void) { return 1; }
 extern "C" size_t ygg_route_workspace_bytes(int N, int E, int k);
 extern "C" int ygg_route(const float*, int, int, int, int32_t*, float*, int32_t*, int32_t*, int32_t*, int32_t*, void*,
                          size_t, hipStream_t);
-extern "C" int ygg_router_energy_logits(const void*, int, int, int, const float*, const float*, int, float*, float*,
-                                        hipStream_t);
+extern "C" int ygg_route_energy(const void*, int, int, int, const float*, const float*, int, int, int32_t*, float*,
+                                int32_t*, int32_t*, int32_t*, int32_t*, float*, void*, size_t, hipStream_t);
 extern "C" int ygg_dispatch(const void*, int, int, int, int, const int32_t*, void*, int, hipStream_t);
 extern "C" int ygg_combine(const void*, int, int, int, int, int, const int32_t*, const float*, const int32_t*,
                            const void*, void*, int, hipStream_t);
@@ -117,11 +117,13 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
   p += align256(P * F * 8 * es);
   void* ys = p;
 
-  if (!logits) {
-    if (ygg_router_energy_logits(x, dtype, N, d, router_w, router_b, E, lg, nullptr, stream)) return -1;
-    logits = lg;
+  if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
+    if (ygg_route_energy(x, dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos,
+                         lg, rws, rws_bytes, stream))
+      return -1;
+  } else if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) {
+    return -1;
   }
-  if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
   if (w_format == kWPauliF32) {
     // fp32 Pauli: x -> split rows once (x_sorted region), up gathers them through
     // perm, down in K splits whose partial planes the combine adds in split order

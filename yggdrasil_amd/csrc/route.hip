@@ -41,22 +41,67 @@ constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
 constexpr int kScanMaxThreads = 1024;
 
-// The selection of one token, eight lanes per token (lane j = tid % 8):
-// probabilities, top-k and renormalised weights; lane j returns slot j
-// (expert, weight), or expert -1 for j >= k or an inactive token.
-template <int Q>  // Q = ceil(E / 8) logits per lane
-__device__ inline void select_token(const float* __restrict__ logits, int E, int k, int t, bool active, int j,
-                                    int lane, int& out_e, float& out_w) {
-  // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
-  float p[Q];
-  float m = -INFINITY;
-  const float* row = logits + (size_t)(active ? t : 0) * E;
+// The logits of one token straight from its activation row (the reference's
+// CliffordRouter energy signature, clifford_router.py:54-90): per-grade sums of
+// squares over the row (lane j takes multivectors j, j + 8, ...; the eight lanes
+// of the token are combined by a shuffle tree), normalised by their sum + 1e-12,
+// then the (E, 4) map and bias.  Lane j returns the logits of experts j + 8 q.
+template <int Q>
+__device__ inline void energy_logits(const void* __restrict__ x, int x_dtype, int d, const float* __restrict__ rw,
+                                     const float* __restrict__ rb, int E, int t, bool active, int j, float (&p)[Q]) {
+  float gs[4] = {0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    for (int i = j; i < d; i += kSelLanes) {
+      float v[8];
+      if (x_dtype == kF32) {
+        const float4* q4 = reinterpret_cast<const float4*>(static_cast<const float*>(x) + ((size_t)t * d + i) * 8);
+        const float4 a = q4[0], b = q4[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + ((size_t)t * d + i) * 8);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[2 * c] = bf16_bits_to_f32((uint16_t)(w[c] & 0xffff));
+          v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(w[c] >> 16));
+        }
+      }
+      gs[0] += v[0] * v[0];
+      gs[1] += v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      gs[2] += v[4] * v[4] + v[5] * v[5] + v[6] * v[6];
+      gs[3] += v[7] * v[7];
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < kSelLanes; o <<= 1)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) gs[c] += __shfl_xor(gs[c], o);
+  const float tot = gs[0] + gs[1] + gs[2] + gs[3] + 1e-12f;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int e = j + kSelLanes * q;
-    p[q] = (active && e < E) ? row[e] : -INFINITY;
-    m = fmaxf(m, p[q]);
+    float l = -INFINITY;
+    if (active && e < E) {
+      l = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) l += (gs[c] / tot) * rw[e * 4 + c];
+      l += rb[e];
+    }
+    p[q] = l;
   }
+}
+
+// The selection of one token, eight lanes per token (lane j = tid % 8), from
+// its logits p (lane j: experts j + 8 q, -inf past E or for an inactive token):
+// probabilities, top-k and renormalised weights; lane j returns slot j
+// (expert, weight), or expert -1 for j >= k or an inactive token.
+template <int Q>  // Q = ceil(E / 8) logits per lane
+__device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool active, int j, int lane, int& out_e,
+                                          float& out_w) {
+  // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) m = fmaxf(m, p[q]);
 #pragma unroll
   for (int o = 1; o < kSelLanes; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
 #pragma unroll
@@ -144,6 +189,19 @@ __device__ inline void select_token(const float* __restrict__ logits, int E, int
     }
   out_e = active ? my_e : -1;
   out_w = my_w;
+}
+
+template <int Q>
+__device__ inline void select_token(const float* __restrict__ logits, int E, int k, int t, bool active, int j,
+                                    int lane, int& out_e, float& out_w) {
+  float p[Q];
+  const float* row = logits + (size_t)(active ? t : 0) * E;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    p[q] = (active && e < E) ? row[e] : -INFINITY;
+  }
+  select_from_logits<Q>(p, E, k, active, j, lane, out_e, out_w);
 }
 
 
@@ -265,8 +323,10 @@ constexpr int kSmallIters = 8;                                     // groups per
 constexpr int kSmallGroups = kSmallWaves * kSmallIters;            // 8-token groups
 constexpr int kSmallMaxN = kSmallGroups * (64 / kSelLanes);        // 1024 tokens
 
-template <int Q>
-__global__ __launch_bounds__(kSmallThreads) void route_small(const float* __restrict__ logits, int N, int E, int k,
+template <int Q, bool FROM_X>
+__global__ __launch_bounds__(kSmallThreads) void route_small(const float* __restrict__ logits, const void* __restrict__ x,
+                                                             int x_dtype, int d, const float* __restrict__ rw,
+                                                             const float* __restrict__ rb, int N, int E, int k,
                                                              int32_t* __restrict__ topk_idx,
                                                              float* __restrict__ topk_w,
                                                              int32_t* __restrict__ counts,
@@ -287,7 +347,13 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
     const int t = grp * 8 + lane / kSelLanes;
     int e;
     float w;
-    select_token<Q>(logits, E, k, t, t < N, j, lane, e, w);
+    if constexpr (FROM_X) {
+      float p[Q];
+      energy_logits<Q>(x, x_dtype, d, rw, rb, E, t, t < N, j, p);
+      select_from_logits<Q>(p, E, k, t < N, j, lane, e, w);
+    } else {
+      select_token<Q>(logits, E, k, t, t < N, j, lane, e, w);
+    }
     int rank = 0;
     for (int x = 0; x < E; ++x) {
       const uint64_t bal = __ballot(e == x);
@@ -398,6 +464,24 @@ __global__ __launch_bounds__(256) void router_energy_logits_kernel(const void* _
 
 using namespace ygg;
 
+namespace {
+template <bool FROM_X>
+int launch_route_small(const float* logits, const void* x, int x_dtype, int d, const float* rw, const float* rb, int N,
+                       int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
+                       int32_t* perm, int32_t* slot_pos, hipStream_t stream) {
+  switch ((E + 7) / 8) {
+#define YGG_SMALL(Q)                                                                                              \
+  case Q:                                                                                                         \
+    route_small<Q, FROM_X><<<1, kSmallThreads, 0, stream>>>(logits, x, x_dtype, d, rw, rb, N, E, k, topk_idx,     \
+                                                            topk_w, counts, offsets, perm, slot_pos);            \
+    break;
+    YGG_SMALL(1) YGG_SMALL(2) YGG_SMALL(3) YGG_SMALL(4) YGG_SMALL(5) YGG_SMALL(6) YGG_SMALL(7) YGG_SMALL(8)
+#undef YGG_SMALL
+  }
+  return check_launch("route_small");
+}
+}  // namespace
+
 YGG_API size_t ygg_route_workspace_bytes(int N, int E, int k) {
   (void)k;
   const size_t nb = (size_t)(N + kSelTokens - 1) / kSelTokens;
@@ -415,18 +499,9 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   YGG_CHECK_ARG(N == 0 || (logits && topk_idx && topk_w && perm && slot_pos && workspace),
                 "ygg_route: null pointer argument");
   YGG_CHECK_ARG(counts && offsets, "ygg_route: null counts/offsets");
-  if (N > 0 && N <= kSmallMaxN) {
-    switch ((E + 7) / 8) {
-#define YGG_SMALL(Q)                                                                                             \
-  case Q:                                                                                                        \
-    route_small<Q><<<1, kSmallThreads, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm,   \
-                                                    slot_pos);                                                   \
-    break;
-      YGG_SMALL(1) YGG_SMALL(2) YGG_SMALL(3) YGG_SMALL(4) YGG_SMALL(5) YGG_SMALL(6) YGG_SMALL(7) YGG_SMALL(8)
-#undef YGG_SMALL
-    }
-    return check_launch("route_small");
-  }
+  if (N > 0 && N <= kSmallMaxN)
+    return launch_route_small<false>(logits, nullptr, 0, 0, nullptr, nullptr, N, E, k, topk_idx, topk_w, counts,
+                                     offsets, perm, slot_pos, stream);
   const int nb = (N + kSelTokens - 1) / kSelTokens;
   int32_t* block_hist = static_cast<int32_t*>(workspace);
   if (nb > 0) {
@@ -462,4 +537,32 @@ YGG_API int ygg_router_energy_logits(const void* x, int x_dtype, int N, int d, c
   router_energy_logits_kernel<<<(N + 3) / 4, 256, 0, stream>>>(x, x_dtype, N, d, router_w, router_b, E, logits,
                                                                 energy);
   return check_launch("router_energy_logits");
+}
+
+// CliffordRouter.forward end to end (clifford_router.py:54-104) plus the expert
+// counting sort (hlm_block.py:165-177): grade energies of x, the (E, 4) map and
+// bias, softmax, top-k, renormalisation, counts, offsets, perm and slot rows.
+// Up to 1024 tokens it is one launch (the logits never leave the chip); beyond,
+// the logits go through `logits_scratch` (N x E fp32) and ygg_route.
+YGG_API int ygg_route_energy(const void* x, int x_dtype, int N, int d, const float* router_w, const float* router_b,
+                             int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
+                             int32_t* perm, int32_t* slot_pos, float* logits_scratch, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
+  YGG_CHECK_ARG(x_dtype == kF32 || x_dtype == kBF16, "ygg_route_energy: x dtype %d unsupported", x_dtype);
+  YGG_CHECK_ARG(N >= 0 && d >= 1, "ygg_route_energy: bad sizes N=%d d=%d", N, d);
+  YGG_CHECK_ARG(E >= 1 && E <= kMaxExperts, "ygg_route_energy: E=%d out of range [1, %d]", E, kMaxExperts);
+  YGG_CHECK_ARG(k >= 1 && k <= kMaxTopK && k <= E, "ygg_route_energy: k=%d out of range [1, min(%d, E=%d)]", k,
+                kMaxTopK, E);
+  YGG_CHECK_ARG(counts && offsets, "ygg_route_energy: null counts/offsets");
+  if (N > 0 && N <= kSmallMaxN) {
+    YGG_CHECK_ARG(x && router_w && router_b && topk_idx && topk_w && perm && slot_pos,
+                  "ygg_route_energy: null pointer argument");
+    return launch_route_small<true>(nullptr, x, x_dtype, d, router_w, router_b, N, E, k, topk_idx, topk_w, counts,
+                                    offsets, perm, slot_pos, stream);
+  }
+  YGG_CHECK_ARG(N == 0 || logits_scratch, "ygg_route_energy: %d tokens need logits_scratch (N x E fp32)", N);
+  if (N > 0 && ygg_router_energy_logits(x, x_dtype, N, d, router_w, router_b, E, logits_scratch, nullptr, stream))
+    return -1;
+  return ygg_route(logits_scratch, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, workspace,
+                   workspace_bytes, stream);
 }

@@ -90,8 +90,9 @@ def router_energy_logits(x: torch.Tensor, router_weight: torch.Tensor, router_bi
     E = router_weight.shape[0]
     logits = torch.empty((Nt, E), device=dev, dtype=torch.float32)
     energy = torch.empty((Nt, 4), device=dev, dtype=torch.float32) if return_energy else None
-    check(lib().ygg_router_energy_logits(ptr(x), _dtype_code(x), Nt, d, ptr(router_weight.float().contiguous()),
-                                         ptr(router_bias.float().contiguous()), E, ptr(logits), ptr(energy),
+    # named so the fp32 copies live until the launch has been queued
+    rw, rb = router_weight.float().contiguous(), router_bias.float().contiguous()
+    check(lib().ygg_router_energy_logits(ptr(x), _dtype_code(x), Nt, d, ptr(rw), ptr(rb), E, ptr(logits), ptr(energy),
                                          stream_handle(dev)), "router_energy_logits")
     return (logits, energy) if return_energy else logits
 
@@ -126,6 +127,34 @@ def route(logits: torch.Tensor, k: int, out: Routing | None = None, workspace: t
         torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     check(L.ygg_route(ptr(logits), Nt, E, k, ptr(r.topk_idx), ptr(r.topk_w), ptr(r.counts), ptr(r.offsets),
                       ptr(r.perm), ptr(r.slot_pos), ptr(ws), ws_bytes, stream_handle(dev)), "route")
+    return r
+
+
+def route_energy(x: torch.Tensor, router_weight: torch.Tensor, router_bias: torch.Tensor, k: int) -> Routing:
+    """CliffordRouter.forward (``clifford_router.py:54-104``) and the counting sort in one call.
+
+    x: (N, d, 8); router_weight (E, 4), router_bias (E,).  Up to 1024 tokens the
+    grade-energy logits are computed inside the routing kernel.
+    """
+    dev = _dev(x, router_weight, router_bias)
+    if x.dim() != 3 or x.shape[2] != 8 or not x.is_contiguous():
+        raise ValueError(f"route_energy: x must be contiguous (N, d, 8), got {tuple(x.shape)}")
+    Nt, d = x.shape[0], x.shape[1]
+    E = router_weight.shape[0]
+    if tuple(router_weight.shape) != (E, 4) or tuple(router_bias.shape) != (E,):
+        raise ValueError("route_energy: router_weight must be (E, 4) and router_bias (E,)")
+    L = lib()
+    ws_bytes = L.ygg_route_workspace_bytes(Nt, E, k)
+    i32 = dict(device=dev, dtype=torch.int32)
+    r = Routing(topk_idx=torch.empty((Nt, k), **i32), topk_w=torch.empty((Nt, k), device=dev, dtype=torch.float32),
+                counts=torch.empty((E,), **i32), offsets=torch.empty((E + 1,), **i32),
+                perm=torch.empty((Nt * k,), **i32), slot_pos=torch.empty((Nt, k), **i32))
+    scratch = torch.empty((max(Nt * E, 1),), device=dev, dtype=torch.float32)
+    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    rw, rb = router_weight.float().contiguous(), router_bias.float().contiguous()
+    check(L.ygg_route_energy(ptr(x), _dtype_code(x), Nt, d, ptr(rw), ptr(rb), E, k, ptr(r.topk_idx), ptr(r.topk_w),
+                             ptr(r.counts), ptr(r.offsets), ptr(r.perm), ptr(r.slot_pos), ptr(scratch), ptr(ws),
+                             ws_bytes, stream_handle(dev)), "route_energy")
     return r
 
 
