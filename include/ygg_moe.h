@@ -186,6 +186,30 @@ int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k,
                     const void* residual, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
                     int32_t* offsets, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
 
+/* ---- the pre-norm and the FFN half of the block ------------------------------
+ * CliffordLayerNorm.forward (holograph/layers/normalization.py:44-67):
+ * y = gamma x_hat + beta with x_hat = x / sqrt(mean_i |x_i|^2 + 2 eps), the mean
+ * over the d multivectors of each token and the product gamma x_hat the
+ * geometric product with gamma on the left.  x (N, d, 8) of x_dtype (f32 or
+ * bf16), gamma and beta (d, 8) fp32, y (N, d, 8) of y_dtype; eps is the
+ * reference's Python float (default 1e-6).  d <= 4096; y must not alias x. */
+int ygg_clifford_layer_norm(const void* x, int x_dtype, int N, int d, const float* gamma, const float* beta,
+                            double eps, void* y, int y_dtype, ygg_stream_t stream);
+
+/* Workspace bytes of ygg_moe_block_ffn. */
+size_t ygg_moe_block_ffn_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format);
+
+/* The FFN half of HLMBlock.forward (holograph/models/hlm_block.py:144-151):
+ * out = x + moe(ffn_norm(x)).  The router sees the normed tokens, as the
+ * reference's _moe_forward does.  Arguments as in ygg_moe_forward, with the
+ * norm's gamma, beta and eps in place of the residual; out must not alias x. */
+int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int E, int k, int act, const float* norm_gamma,
+                      const float* norm_beta, double norm_eps, const float* logits, const float* router_w,
+                      const float* router_b, const void* w_up, const float* s_up, const float* b_up,
+                      const void* w_down, const float* s_down, const float* b_down, int w_format, void* out,
+                      int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
+                      size_t workspace_bytes, ygg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -137,3 +137,23 @@ def test_product_never_imports_oracle():
             if f.endswith(".py"):
                 src = open(os.path.join(dirpath, f)).read()
                 assert "oracle" not in re.findall(r"^\s*(?:from|import)\s+(\w+)", src, flags=re.M), f
+
+
+def test_norm_and_block_argument_checks():
+    """Rejections happen on the host, before any launch (no GPU needed)."""
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    assert L.ygg_clifford_layer_norm(None, 3, 4, 8, None, None, 1e-6, None, 0, None) == -1
+    assert L.ygg_clifford_layer_norm(None, 0, 4, 0, None, None, 1e-6, None, 0, None) == -1
+    assert L.ygg_clifford_layer_norm(None, 0, 4, 4097, None, None, 1e-6, None, 0, None) == -1
+    assert L.ygg_clifford_layer_norm(None, 0, 4, 8, None, None, -1.0, None, 0, None) == -1
+    assert L.ygg_clifford_layer_norm(None, 0, 4, 8, None, None, 1e-6, None, 0, None) == -1  # null pointers
+    assert b"null" in L.ygg_last_error()
+    assert L.ygg_clifford_layer_norm(None, 1, 0, 8, None, None, 1e-6, None, 1, None) == 0  # empty: nothing to do
+    N, d, F, E, k = 300, 64, 256, 8, 2
+    for dt, fmt, es in ((0, 4, 4), (1, 3, 2), (1, 2, 2)):
+        moe = L.ygg_moe_workspace_bytes(N, d, F, E, k, dt, fmt)
+        assert L.ygg_moe_block_ffn_workspace_bytes(N, d, F, E, k, dt, fmt) == (N * d * 8 * es + 255) // 256 * 256 + moe

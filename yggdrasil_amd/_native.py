@@ -15,7 +15,7 @@ import torch  # noqa: F401  (must precede loading the library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libygg_moe.so")
 
-_c_int, _c_size, _vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+_c_int, _c_size, _vp, _c_double = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_double
 
 # symbol -> (restype, argtypes); must match include/ygg_moe.h
 SIGNATURES = {
@@ -44,6 +44,11 @@ SIGNATURES = {
     "ygg_moe_forward": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _c_size, _vp]),
+    "ygg_clifford_layer_norm": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_double, _vp, _c_int, _vp]),
+    "ygg_moe_block_ffn_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "ygg_moe_block_ffn": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_double,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _c_size, _vp]),
 }
 
 

@@ -49,6 +49,8 @@ extern "C" int ygg_route(const float*, int, int, int, int32_t*, float*, int32_t*
 extern "C" int ygg_route_energy(const void*, int, int, int, const float*, const float*, int, int, int32_t*, float*,
                                 int32_t*, int32_t*, int32_t*, int32_t*, float*, void*, size_t, hipStream_t);
 extern "C" int ygg_dispatch(const void*, int, int, int, int, const int32_t*, void*, int, hipStream_t);
+extern "C" int ygg_clifford_layer_norm(const void*, int, int, int, const float*, const float*, double, void*, int,
+                                       hipStream_t);
 extern "C" int ygg_combine(const void*, int, int, int, int, int, const int32_t*, const float*, const int32_t*,
                            const void*, void*, int, hipStream_t);
 extern "C" int ygg_grouped_clifford_linear(const void*, int, const void*, int, const float*, const float*,
@@ -172,4 +174,30 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
                                   /*blade=*/1, stream))
     return -1;
   return ygg_combine(ys, dtype, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
+}
+
+YGG_API size_t ygg_moe_block_ffn_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format) {
+  const size_t es = (dtype == kF32) ? 4 : 2;
+  return align256((size_t)N * d * 8 * es) + ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format);
+}
+
+YGG_API int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
+                              const float* norm_gamma, const float* norm_beta, double norm_eps, const float* logits,
+                              const float* router_w, const float* router_b, const void* w_up, const float* s_up,
+                              const float* b_up, const void* w_down, const float* s_down, const float* b_down,
+                              int w_format, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                              int32_t* offsets, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_block_ffn: dtype %d unsupported", dtype);
+  const size_t need = ygg_moe_block_ffn_workspace_bytes(N, d, F, E, k, dtype, w_format);
+  YGG_CHECK_ARG(workspace_bytes >= need, "ygg_moe_block_ffn: workspace of %zu bytes, need %zu", workspace_bytes, need);
+  YGG_CHECK_ARG(out != x, "ygg_moe_block_ffn: out must not alias x");
+  if (N == 0) return 0;
+  // x_norm = ffn_norm(x) at the front of the workspace; the MoE layer gets the
+  // rest, and adds x back in its combine
+  const size_t xn_bytes = align256((size_t)N * d * 8 * ((dtype == kF32) ? 4 : 2));
+  void* xn = workspace;
+  if (ygg_clifford_layer_norm(x, dtype, N, d, norm_gamma, norm_beta, norm_eps, xn, dtype, stream)) return -1;
+  return ygg_moe_forward(xn, dtype, N, d, F, E, k, act, logits, router_w, router_b, w_up, s_up, b_up, w_down, s_down,
+                         b_down, w_format, /*residual=*/x, out, topk_idx, topk_w, counts, offsets,
+                         static_cast<char*>(workspace) + xn_bytes, workspace_bytes - xn_bytes, stream);
 }

@@ -242,3 +242,73 @@ class CliffordLinear(nn.Module):
         offsets = torch.tensor([0, flat.shape[0]], device=x.device, dtype=torch.int32)
         y = ops.grouped_clifford_linear(flat, pw, offsets, pb, "none", out_dtype=self.dtype)
         return y.reshape(*batch, self.d_out, 8)
+
+
+class CliffordLayerNorm(nn.Module):
+    """CliffordLayerNorm (``normalization.py:19-67``): y = gamma x_hat + beta (geometric product).
+
+    gamma starts as the scalar 1 and beta at zero, as in the reference
+    (``normalization.py:33-41``).  x: (..., d, 8), fp32 or bf16.
+    """
+
+    def __init__(self, d_model: int, eps: float = 1e-6, device=None):
+        super().__init__()
+        self.d_model, self.eps = d_model, eps
+        gamma = torch.zeros(d_model, 8)
+        gamma[:, 0] = 1.0
+        self.gamma = nn.Parameter(gamma)
+        self.beta = nn.Parameter(torch.zeros(d_model, 8))
+        if device is not None:
+            self.to(device)
+
+    def forward(self, x: torch.Tensor, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        return ops.clifford_layer_norm(x.contiguous(), self.gamma.detach(), self.beta.detach(), self.eps,
+                                       out_dtype=out_dtype)
+
+
+class CliffordMoEBlockFFN(nn.Module):
+    """The FFN half of ``HLMBlock.forward`` (``hlm_block.py:144-151``): ``x + moe(ffn_norm(x))``.
+
+    With the energy router or caller logits the whole sub-layer is one library
+    call (``ygg_moe_block_ffn``): the norm, then the MoE layer on the normed
+    tokens with x added back in its combine.
+    """
+
+    def __init__(self, cfg: MoEHLMConfig, device=None, generator: torch.Generator | None = None,
+                 norm_eps: float = 1e-6):
+        super().__init__()
+        self.cfg = cfg
+        self.ffn_norm = CliffordLayerNorm(cfg.d_model, norm_eps, device=device)
+        self.moe = CliffordMoELayer(cfg, device=device, generator=generator)
+        self._workspace = None
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
+        """x (B, T, d, 8) -> (B, T, d, 8)."""
+        cfg, moe = self.cfg, self.moe
+        if x.dim() != 4 or x.shape[-1] != 8 or x.shape[-2] != cfg.d_model:
+            raise ValueError(f"expected (B, T, {cfg.d_model}, 8), got {tuple(x.shape)}")
+        if x.dtype != cfg.dtype:
+            raise ValueError(f"layer dtype is {cfg.dtype}, input is {x.dtype}")
+        if cfg.router == "clifford_head" and logits is None:
+            x_norm = self.ffn_norm(x)
+            return moe.moe_forward(x_norm, logits=moe._head_logits(
+                x_norm.reshape(-1, cfg.d_model, 8), moe._get_prepared()), residual=x)
+        if cfg.router == "logits" and logits is None:
+            raise ValueError("router='logits' needs logits")
+        B, T = x.shape[:2]
+        flat = x.reshape(B * T, cfg.d_model, 8).contiguous()
+        prep = moe._get_prepared()
+        if logits is not None:
+            logits = logits.reshape(B * T, cfg.n_experts).float().contiguous()
+        ws_bytes = ops.moe_block_ffn_workspace_bytes(B * T, cfg.d_model, cfg.d_ff, cfg.n_experts, cfg.top_k,
+                                                     cfg.dtype, cfg.weight_format)
+        if self._workspace is None or self._workspace.numel() < ws_bytes or self._workspace.device != x.device:
+            self._workspace = torch.empty((max(ws_bytes, 1),), device=x.device, dtype=torch.uint8)
+        out, routing = ops.moe_block_ffn(
+            flat, cfg.top_k, self.ffn_norm.gamma.detach(), self.ffn_norm.beta.detach(), prep["w_up"],
+            prep["w_down"], prep["b_up"], prep["b_down"], cfg.activation, logits=logits,
+            router_weight=moe.router_weight.detach() if logits is None else None,
+            router_bias=moe.router_bias.detach() if logits is None else None, norm_eps=self.ffn_norm.eps,
+            workspace=self._workspace)
+        moe.last_routing = routing
+        return out.reshape(B, T, cfg.d_model, 8)

@@ -383,6 +383,68 @@ def moe_forward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: Prepared
     return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets)
 
 
+def clifford_layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-6,
+                        out_dtype: torch.dtype | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """CliffordLayerNorm.forward (``normalization.py:44-67``). x: (..., d, 8); gamma, beta: (d, 8)."""
+    dev = _dev(x, gamma, beta)
+    if x.dim() < 2 or x.shape[-1] != 8 or not x.is_contiguous():
+        raise ValueError(f"clifford_layer_norm: x must be contiguous (..., d, 8), got {tuple(x.shape)}")
+    d = x.shape[-2]
+    if tuple(gamma.shape) != (d, 8) or tuple(beta.shape) != (d, 8):
+        raise ValueError(f"clifford_layer_norm: gamma and beta must be ({d}, 8)")
+    Nt = x.numel() // (8 * d) if d else 0
+    if out is None:
+        out = torch.empty(x.shape, device=dev, dtype=out_dtype or x.dtype)
+    elif tuple(out.shape) != tuple(x.shape) or not out.is_contiguous():
+        raise ValueError("clifford_layer_norm: out must be a contiguous tensor of x's shape")
+    g, b = gamma.float().contiguous(), beta.float().contiguous()
+    check(lib().ygg_clifford_layer_norm(ptr(x), _dtype_code(x), Nt, d, ptr(g), ptr(b), float(eps), ptr(out),
+                                        _dtype_code(out), stream_handle(dev)), "clifford_layer_norm")
+    return out
+
+
+def moe_block_ffn_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype, fmt: str) -> int:
+    return lib().ygg_moe_block_ffn_workspace_bytes(Nt, d, F, E, k, DTYPE_CODE[dtype], WFORMAT_CODE[fmt])
+
+
+def moe_block_ffn(x: torch.Tensor, k: int, norm_gamma: torch.Tensor, norm_beta: torch.Tensor, w_up: PreparedWeights,
+                  w_down: PreparedWeights, b_up: torch.Tensor | None = None, b_down: torch.Tensor | None = None,
+                  act: str = "gelu", logits: torch.Tensor | None = None, router_weight: torch.Tensor | None = None,
+                  router_bias: torch.Tensor | None = None, norm_eps: float = 1e-6,
+                  workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """``x + moe(ffn_norm(x))`` in one call (``ygg_moe_block_ffn``, ``hlm_block.py:144-151``). x: (N, d, 8)."""
+    dev = _dev(x, logits, norm_gamma, norm_beta)
+    if x.dim() != 3 or x.shape[2] != 8 or not x.is_contiguous():
+        raise ValueError(f"moe_block_ffn: x must be contiguous (N, d, 8), got {tuple(x.shape)}")
+    Nt, d = x.shape[0], x.shape[1]
+    E, F = w_up.E, w_up.d_out
+    if w_down.d_in != F or w_down.d_out != d or w_up.d_in != d or w_down.E != E:
+        raise ValueError("expert weight shapes do not chain d -> F -> d")
+    if w_up.fmt != w_down.fmt:
+        raise ValueError("up and down weights must share a format")
+    if tuple(norm_gamma.shape) != (d, 8) or tuple(norm_beta.shape) != (d, 8):
+        raise ValueError(f"moe_block_ffn: norm gamma and beta must be ({d}, 8)")
+    ws_bytes = moe_block_ffn_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    if out is None:
+        out = torch.empty_like(x)
+    i32 = dict(device=dev, dtype=torch.int32)
+    topk_idx = torch.empty((Nt, k), **i32)
+    topk_w = torch.empty((Nt, k), device=dev, dtype=torch.float32)
+    counts = torch.empty((E,), **i32)
+    offsets = torch.empty((E + 1,), **i32)
+    g, nb = norm_gamma.float().contiguous(), norm_beta.float().contiguous()
+    rw = router_weight.float().contiguous() if router_weight is not None else None
+    rb = router_bias.float().contiguous() if router_bias is not None else None
+    check(lib().ygg_moe_block_ffn(ptr(x), _dtype_code(x), Nt, d, F, E, k, ACT_CODE[act], ptr(g), ptr(nb),
+                                  float(norm_eps), ptr(logits), ptr(rw), ptr(rb), ptr(w_up.data), ptr(w_up.scales),
+                                  ptr(b_up), ptr(w_down.data), ptr(w_down.scales), ptr(b_down),
+                                  WFORMAT_CODE[w_up.fmt], ptr(out), ptr(topk_idx), ptr(topk_w), ptr(counts),
+                                  ptr(offsets), ptr(workspace), ws_bytes, stream_handle(dev)), "moe_block_ffn")
+    return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets)
+
+
 def to_mask_order(x: torch.Tensor) -> torch.Tensor:
     """Blade order -> mask order (exchange components 3 and 4)."""
     return x[..., [0, 1, 2, 4, 3, 5, 6, 7]].contiguous()
