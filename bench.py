@@ -1,13 +1,15 @@
 """Benchmark of the MoE-HLM expert layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5,c3b] [--no-cpu-baseline]
 
 A step is one forward pass of the layer over one batch of synthetic input
 (inputs resident in HBM before timing starts).  The headline workload is
 the bf16 prefill-shape layer, N=8192 tokens, d=128
 multivectors, E=32 experts, top-4, expert FFN 128 -> 512 -> 128 with the
 grade-wise GELU, Zipf(1.2) expert load.  Configs 1, 2, 4 and 5 are timed in
-the same run and reported under "configs".
+the same run and reported under "configs", with "c3b": config 3 inside the
+FFN half of the block, x + moe(ffn_norm(x)) (CliffordLayerNorm in front, the
+residual added in the combine).
 
 One JSON line is printed.  ``roofline`` covers the dominant kernel, the
 grouped CliffordLinear MFMA kernel (both expert products), from HIP events
@@ -34,7 +36,7 @@ PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
 # measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
 PAULI_C3_TRAFFIC_BYTES = 410.9e6
-SEEDS = {"c1": 1, "c1l": 1, "c2": 2, "c3": 3, "c3l": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1l": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
@@ -47,6 +49,8 @@ CONFIGS = {
     "c3l": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="bf16", logits="zipf", layers=1),
     "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1),
     "c5": dict(N=4096, d=256, E=64, k=2, F=1024, dtype="bf16", fmt="pauli", logits="normal_bias", layers=12),
+    # the FFN half of the block around config 3: x + moe(ffn_norm(x)) (pre-norm, residual)
+    "c3b": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, block=True),
 }
 
 
@@ -55,7 +59,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c3,c1,c2,c4,c5")
+    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=256)
     # a plain device copy of this many MiB, run (3 times) before the configs: the reference
@@ -246,6 +250,40 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     return res
 
 
+def run_block_config(torch, ops, name, c, steps, warmup):
+    """x + moe(ffn_norm(x)) through ygg_moe_block_ffn; the norm kernel also timed alone."""
+    x, layers = make_inputs(torch, c, seed=SEEDS[name])
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    L0 = layers[0]
+    wu, wd = ops.prepare_weights(L0.pop("w_up"), c["fmt"]), ops.prepare_weights(L0.pop("w_down"), c["fmt"])
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEEDS[name] + 100)
+    gamma = torch.zeros(d, 8, device="cuda")
+    gamma[:, 0] = 1.0
+    gamma += 0.1 * torch.randn(d, 8, generator=g, device="cuda")
+    beta = 0.1 * torch.randn(d, 8, generator=g, device="cuda")
+    ws = torch.empty(ops.moe_block_ffn_workspace_bytes(N, d, F, E, k, x.dtype, c["fmt"]), device="cuda",
+                     dtype=torch.uint8)
+    out = torch.empty_like(x)
+    logits = L0.get("logits")
+
+    def step():
+        ops.moe_block_ffn(x, k, gamma, beta, wu, wd, None, None, "gelu", logits=logits,
+                          router_weight=L0.get("router_w"), router_bias=L0.get("router_b"), workspace=ws, out=out)
+
+    ms = time_fn(torch, step, steps, warmup)
+    xn = torch.empty_like(x)
+    Lb = ops.lib()
+    args = (x.data_ptr(), ops.DTYPE_CODE[x.dtype], N, d, gamma.data_ptr(), beta.data_ptr(), 1e-6, xn.data_ptr(),
+            ops.DTYPE_CODE[x.dtype], ops.stream_handle())
+    ms_norm = time_fn(torch, lambda: ops.check(Lb.ygg_clifford_layer_norm(*args)), steps, warmup)
+    R = d * 8 * x.element_size()
+    norm_bytes = 2 * N * R + 2 * d * 32  # x in, x_norm out, gamma and beta
+    return dict(workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"],
+                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), kernels_ms=dict(norm=ms_norm),
+                norm_bytes=norm_bytes, norm_hbm_frac=norm_bytes / (ms_norm * 1e-3) / PEAK_HBM)
+
+
 def calibrate_gemm(torch):
     """hipBLASLt (torch.matmul) bf16 GEMM rates on N(0,1) operands, two timed passes per shape."""
     out = []
@@ -392,6 +430,8 @@ def main():
         print(f"[bench] {name} {config_label(c)}", file=sys.stderr, flush=True)
         if name == "c2":
             results[name] = run_c2(torch, ops, c, args.steps, args.warmup)
+        elif c.get("block"):
+            results[name] = run_block_config(torch, ops, name, c, args.steps, args.warmup)
         else:
             results[name] = run_layer_config(torch, ops, name, c, args.steps, args.warmup)
         torch.cuda.empty_cache()

@@ -5,8 +5,9 @@
 // The norm is HBM-bound: one read and one write of each token row (R bytes
 // each) plus the (d, 8) gamma and beta, which stay in L2.  One wave owns one
 // token: lane l holds multivectors l, l+64, ...; the per-multivector squared
-// norms go to LDS, every lane of the wave then forms the same mean in NumPy's
-// pairwise order, and the second pass writes gamma x_hat + beta.
+// norms go to LDS, groups of 8 lanes sum the runs of NumPy's pairwise order,
+// every lane combines the run sums into the mean, and the second pass writes
+// gamma x_hat + beta.
 //
 // Bit-level parity with the reference's fp32 NumPy expression:
 //  * |x_i|^2 = sum over the 8 components of the rounded squares, in NumPy's
@@ -28,72 +29,108 @@ namespace ygg {
 namespace {
 
 constexpr int kNormWaves = 4;       // tokens per 256-thread workgroup, one wave each
-constexpr int kNormMaxD = 4096;     // the pairwise recursion below covers this length
-constexpr int kNormCache = 4;       // multivectors per lane kept in registers between the passes
+constexpr int kNormMaxD = 4096;     // the pairwise plan below covers this length
 constexpr int kPwBlock = 128;       // NumPy's pairwise block
+constexpr int kMaxLeaves = 40;      // runs of at most 128 values in the plan for d <= 4096 (33 at most)
 
-// ---- NumPy pairwise sum over LDS (all lanes read the same addresses) ----------
-__device__ inline float pw_leaf(const float* a, int n) {
+// ---- NumPy's pairwise sum, spread over the lanes of a wave ------------------------
+// The recursion (split n > 128 at n/2 rounded down to a multiple of 8) depends
+// on d only, so the host lists its leaves -- runs of at most 128 values -- in
+// order.  Eight lanes sum one leaf: lane j holds accumulator j (elements j,
+// j+8, ... below the last full row of 8, added in order), three xor shuffles
+// form ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), and the remaining n % 8 values are
+// added in order.  The leaf sums are then combined along the recursion.
+struct PwPlan {
+  int n_leaves;
+  uint16_t start[kMaxLeaves];
+  uint16_t len[kMaxLeaves];
+};
+
+constexpr int kPwDepth = 6;  // recursion levels pw_combine unrolls; d <= 4096 needs 6
+
+// Appends the leaves of a run of n values at s; false if the plan would need
+// more than kMaxLeaves leaves or kPwDepth levels.
+bool pw_plan_add(PwPlan& p, int s, int n, int depth = 0) {
+  if (n <= kPwBlock) {
+    if (p.n_leaves >= kMaxLeaves) return false;
+    p.start[p.n_leaves] = (uint16_t)s;
+    p.len[p.n_leaves] = (uint16_t)n;
+    ++p.n_leaves;
+    return true;
+  }
+  if (depth >= kPwDepth) return false;
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  return pw_plan_add(p, s, n2, depth + 1) && pw_plan_add(p, s + n2, n - n2, depth + 1);
+}
+
+// Sum of one leaf of n values at a (LDS) by the 8 lanes j = 0..7 of a group;
+// every lane of the group returns the sum.
+__device__ inline float pw_leaf_lanes(const float* a, int n, int j) {
 #pragma clang fp contract(off)
-  if (n < 8) {
+  if (n < 8) {  // only d < 8: one leaf, summed in order from zero
     float s = 0.f;
     for (int i = 0; i < n; ++i) s = s + a[i];
     return s;
   }
-  float r[8];
+  const int rows = n >> 3;  // 1..16
+  float t[kPwBlock / 8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = a[j];
-  const int n8 = n - (n & 7);
-  for (int i = 8; i < n8; i += 8) {
+  for (int q = 0; q < kPwBlock / 8; ++q) t[q] = (q < rows) ? a[8 * q + j] : 0.f;
+  float r = t[0];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = r[j] + a[i + j];
-  }
-  float s = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  for (int i = n8; i < n; ++i) s = s + a[i];
-  return s;
+  for (int q = 1; q < kPwBlock / 8; ++q)
+    if (q < rows) r = r + t[q];
+  r = r + __shfl_xor(r, 1);
+  r = r + __shfl_xor(r, 2);
+  r = r + __shfl_xor(r, 4);
+  for (int i = 8 * rows; i < n; ++i) r = r + a[i];
+  return r;
 }
 
-// Each split leaves pieces of at most n/2 + 8 values, so 6 levels take 4096
-// values down to runs of at most 128.
+// The leaf sums (in order) combined along the recursion over n.
 template <int DEPTH>
-__device__ float pw_sum(const float* a, int n) {
+__device__ float pw_combine(const float* leaf, int n, int& next) {
 #pragma clang fp contract(off)
   if constexpr (DEPTH == 0) {
-    return pw_leaf(a, n);
+    return leaf[next++];
   } else {
-    if (n <= kPwBlock) return pw_leaf(a, n);
+    if (n <= kPwBlock) return leaf[next++];
     int n2 = n >> 1;
     n2 -= n2 & 7;
-    return pw_sum<DEPTH - 1>(a, n2) + pw_sum<DEPTH - 1>(a + n2, n - n2);
+    const float l = pw_combine<DEPTH - 1>(leaf, n2, next);
+    const float r = pw_combine<DEPTH - 1>(leaf, n - n2, next);
+    return l + r;
   }
 }
 
-constexpr int kPwDepth = 6;
-
-constexpr bool pw_depth_covers(int n, int depth) {
-  if (n <= kPwBlock) return true;
-  if (depth == 0) return false;
-  int n2 = n / 2;
-  n2 -= n2 % 8;
-  return pw_depth_covers(n2, depth - 1) && pw_depth_covers(n - n2, depth - 1);
-}
-constexpr bool pw_depth_covers_all(int n_max, int depth) {
-  for (int n = 1; n <= n_max; ++n)
-    if (!pw_depth_covers(n, depth)) return false;
-  return true;
-}
-static_assert(pw_depth_covers_all(kNormMaxD, kPwDepth), "pairwise recursion depth must cover every d <= kNormMaxD");
-
 // ---- one multivector in and out ------------------------------------------------
-__device__ inline void load_mv(const float* row, int i, float v[8]) {
+// Raw storage of one input multivector: the loads are issued early and the
+// values unpacked only when used, so bf16 rows hold 4 registers, not 8.
+template <typename IT>
+struct Mv;
+template <>
+struct Mv<float> {
+  float4 a, b;
+};
+template <>
+struct Mv<uint16_t> {
+  uint4 a;
+};
+
+__device__ inline Mv<float> load_raw(const float* row, int i) {
   const float4* p = reinterpret_cast<const float4*>(row + (size_t)i * 8);
-  const float4 a = p[0], b = p[1];
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  return Mv<float>{p[0], p[1]};
 }
-__device__ inline void load_mv(const uint16_t* row, int i, float v[8]) {
-  const uint4 u = *reinterpret_cast<const uint4*>(row + (size_t)i * 8);
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+__device__ inline Mv<uint16_t> load_raw(const uint16_t* row, int i) {
+  return Mv<uint16_t>{*reinterpret_cast<const uint4*>(row + (size_t)i * 8)};
+}
+__device__ inline void unpack(const Mv<float>& m, float v[8]) {
+  v[0] = m.a.x; v[1] = m.a.y; v[2] = m.a.z; v[3] = m.a.w;
+  v[4] = m.b.x; v[5] = m.b.y; v[6] = m.b.z; v[7] = m.b.w;
+}
+__device__ inline void unpack(const Mv<uint16_t>& m, float v[8]) {
+  const uint32_t w[4] = {m.a.x, m.a.y, m.a.z, m.a.w};
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     v[2 * q] = __builtin_bit_cast(float, w[q] << 16);
@@ -119,13 +156,11 @@ __device__ inline float squared_norm(const float v[8]) {
 }
 
 // y = gamma x_hat + beta for one multivector, x_hat = v / rms.
-__device__ inline void scale_shift(float v[8], float rms, const float* __restrict__ g, const float* __restrict__ bt) {
+__device__ inline void scale_shift(float v[8], float rms, const Mv<float>& g, const Mv<float>& bt) {
 #pragma clang fp contract(off)
   float xh[8], ga[8], be[8];
-  const float4 g0 = reinterpret_cast<const float4*>(g)[0], g1 = reinterpret_cast<const float4*>(g)[1];
-  const float4 b0 = reinterpret_cast<const float4*>(bt)[0], b1 = reinterpret_cast<const float4*>(bt)[1];
-  ga[0] = g0.x; ga[1] = g0.y; ga[2] = g0.z; ga[3] = g0.w; ga[4] = g1.x; ga[5] = g1.y; ga[6] = g1.z; ga[7] = g1.w;
-  be[0] = b0.x; be[1] = b0.y; be[2] = b0.z; be[3] = b0.w; be[4] = b1.x; be[5] = b1.y; be[6] = b1.z; be[7] = b1.w;
+  unpack(g, ga);
+  unpack(bt, be);
 #pragma unroll
   for (int c = 0; c < 8; ++c) xh[c] = v[c] / rms;
 #pragma unroll
@@ -143,64 +178,99 @@ __device__ inline void scale_shift(float v[8], float rms, const float* __restric
   }
 }
 
-template <typename IT, typename OT>
+// One wave normalises one token.  Every load of the wave -- the first 64 CACHE
+// multivectors of the row and of gamma and beta -- is issued before any
+// arithmetic.  Multivectors past 64 CACHE (d > 256) are read again from L2 in
+// the second pass.
+template <typename IT, typename OT, int CACHE>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const IT* __restrict__ x, int N, int d,
                                                          const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float two_eps,
-                                                         OT* __restrict__ y) {
+                                                         const PwPlan plan, OT* __restrict__ y) {
 #pragma clang fp contract(off)
-  extern __shared__ float norm_sq[];  // (kNormWaves, d)
+  extern __shared__ float lds[];  // per wave: d squared norms, then kMaxLeaves leaf sums
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kNormWaves + wave;
   const bool live = t < N;
   const IT* xr = x + (size_t)(live ? t : 0) * d * 8;
-  float* ns = norm_sq + wave * d;
+  float* ns = lds + wave * (d + kMaxLeaves);
+  float* ls = ns + d;
 
-  float v[kNormCache][8];
+  Mv<IT> raw[CACHE];
+  Mv<float> g[CACHE], bt[CACHE];
 #pragma unroll
-  for (int q = 0; q < kNormCache; ++q) {
-    const int i = lane + 64 * q;
-    if (live && i < d) {
-      load_mv(xr, i, v[q]);
-      ns[i] = squared_norm(v[q]);
+  for (int q = 0; q < CACHE; ++q)
+    if (live && lane + 64 * q < d) raw[q] = load_raw(xr, lane + 64 * q);
+#pragma unroll
+  for (int q = 0; q < CACHE; ++q)
+    if (lane + 64 * q < d) {
+      g[q] = load_raw(gamma, lane + 64 * q);
+      bt[q] = load_raw(beta, lane + 64 * q);
+    }
+
+  // pass 1: |x_i|^2 of every multivector into LDS
+  if (live) {
+#pragma unroll
+    for (int q = 0; q < CACHE; ++q)
+      if (lane + 64 * q < d) {
+        float v[8];
+        unpack(raw[q], v);
+        ns[lane + 64 * q] = squared_norm(v);
+      }
+    for (int i = lane + 64 * CACHE; i < d; i += 64) {
+      float v[8];
+      unpack(load_raw(xr, i), v);
+      ns[i] = squared_norm(v);
     }
   }
+  __syncthreads();
+  // the pairwise sum: 8 leaves at a time, one per group of 8 lanes
+  const int grp = lane >> 3, j = lane & 7;
   if (live) {
-    for (int i = lane + 64 * kNormCache; i < d; i += 64) {
-      float w[8];
-      load_mv(xr, i, w);
-      ns[i] = squared_norm(w);
+    for (int L = grp; L < plan.n_leaves; L += 8) {
+      const float r = pw_leaf_lanes(ns + plan.start[L], plan.len[L], j);
+      if (j == 0) ls[L] = r;
     }
   }
   __syncthreads();
   if (!live) return;
-  const float mean = pw_sum<kPwDepth>(ns, d) / (float)d;
+  int next = 0;
+  const float mean = pw_combine<kPwDepth>(ls, d, next) / (float)d;
   const float rms = sqrtf(mean + two_eps);
 
+  // pass 2: gamma x_hat + beta
   OT* yr = y + (size_t)t * d * 8;
 #pragma unroll
-  for (int q = 0; q < kNormCache; ++q) {
+  for (int q = 0; q < CACHE; ++q) {
     const int i = lane + 64 * q;
     if (i < d) {
-      scale_shift(v[q], rms, gamma + (size_t)i * 8, beta + (size_t)i * 8);
-      store_mv(yr, i, v[q]);
+      float v[8];
+      unpack(raw[q], v);
+      scale_shift(v, rms, g[q], bt[q]);
+      store_mv(yr, i, v);
     }
   }
-  for (int i = lane + 64 * kNormCache; i < d; i += 64) {
-    float w[8];
-    load_mv(xr, i, w);
-    scale_shift(w, rms, gamma + (size_t)i * 8, beta + (size_t)i * 8);
-    store_mv(yr, i, w);
+  for (int i = lane + 64 * CACHE; i < d; i += 64) {
+    float v[8];
+    unpack(load_raw(xr, i), v);
+    scale_shift(v, rms, load_raw(gamma, i), load_raw(beta, i));
+    store_mv(yr, i, v);
   }
 }
 
 template <typename IT, typename OT>
 int launch_norm(const void* x, int N, int d, const float* gamma, const float* beta, float two_eps, void* y,
                 hipStream_t stream) {
+  PwPlan plan{};
+  YGG_CHECK_ARG(pw_plan_add(plan, 0, d), "ygg_clifford_layer_norm: no pairwise plan for d=%d", d);
   const int blocks = (N + kNormWaves - 1) / kNormWaves;
-  const size_t lds = (size_t)kNormWaves * d * sizeof(float);
-  hipLaunchKernelGGL((layer_norm_kernel<IT, OT>), dim3(blocks), dim3(64 * kNormWaves), lds, stream,
-                     static_cast<const IT*>(x), N, d, gamma, beta, two_eps, static_cast<OT*>(y));
+  const size_t lds = (size_t)kNormWaves * (d + kMaxLeaves) * sizeof(float);
+  if (d <= 128)
+    hipLaunchKernelGGL((layer_norm_kernel<IT, OT, 2>), dim3(blocks), dim3(64 * kNormWaves), lds, stream,
+                       static_cast<const IT*>(x), N, d, gamma, beta, two_eps, plan, static_cast<OT*>(y));
+  else
+    hipLaunchKernelGGL((layer_norm_kernel<IT, OT, 4>), dim3(blocks), dim3(64 * kNormWaves), lds, stream,
+                       static_cast<const IT*>(x), N, d, gamma, beta, two_eps, plan, static_cast<OT*>(y));
   return check_launch("ygg_clifford_layer_norm");
 }
 
