@@ -279,9 +279,15 @@ def run_block_config(torch, ops, name, c, steps, warmup):
     ms_norm = time_fn(torch, lambda: ops.check(Lb.ygg_clifford_layer_norm(*args)), steps, warmup)
     R = d * 8 * x.element_size()
     norm_bytes = 2 * N * R + 2 * d * 32  # x in, x_norm out, gamma and beta
+    # weight import: grade-aware quantization of this config's up weights (E fp32 tensors),
+    # codes and fp32 values written; the weights are read twice (extrema, then codes)
+    w = torch.randn(E, F, d, 8, generator=g, device="cuda")
+    ms_gq = time_fn(torch, lambda: ops.grade_quantize(w, (8, 6, 6, 4), True), steps, warmup)
+    gq_bytes = w.numel() * (4 + 4 + 2 + 4)
     return dict(workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"],
-                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), kernels_ms=dict(norm=ms_norm),
-                norm_bytes=norm_bytes, norm_hbm_frac=norm_bytes / (ms_norm * 1e-3) / PEAK_HBM)
+                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), kernels_ms=dict(norm=ms_norm, grade_quantize=ms_gq),
+                norm_bytes=norm_bytes, norm_hbm_frac=norm_bytes / (ms_norm * 1e-3) / PEAK_HBM,
+                grade_quantize_bytes=gq_bytes, grade_quantize_hbm_frac=gq_bytes / (ms_gq * 1e-3) / PEAK_HBM)
 
 
 def calibrate_gemm(torch):

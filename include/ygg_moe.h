@@ -186,6 +186,18 @@ int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k,
                     const void* residual, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
                     int32_t* offsets, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
 
+/* ---- weight import: grade-aware quantization -----------------------------------
+ * quantize_multivector / dequantize_multivector
+ * (bifrost/quantization/grade_quantize.py:86-118,153-238) on T tensors of
+ * mv_per_tensor multivectors each (fp32, blade order; e.g. T experts of
+ * (d_out, d_in) weights): per tensor and grade g a bit width grade_bits[g] in
+ * [2, 16] (host array of 4), a scale and, unless symmetric, a zero point, all
+ * in float64 as the reference.  Writes scales (T, 4) fp64 and zero_points
+ * (T, 4) int32; codes (T * mv_per_tensor * 8) int16 and dequant (same count,
+ * (q - zp) * scale rounded to fp32) when not NULL. */
+int ygg_grade_quantize(const float* W, int T, size_t mv_per_tensor, const int32_t* grade_bits, int symmetric,
+                       int16_t* codes, double* scales, int32_t* zero_points, float* dequant, ygg_stream_t stream);
+
 /* ---- the pre-norm and the FFN half of the block ------------------------------
  * CliffordLayerNorm.forward (holograph/layers/normalization.py:44-67):
  * y = gamma x_hat + beta with x_hat = x / sqrt(mean_i |x_i|^2 + 2 eps), the mean

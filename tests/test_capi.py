@@ -157,3 +157,20 @@ def test_norm_and_block_argument_checks():
     for dt, fmt, es in ((0, 4, 4), (1, 3, 2), (1, 2, 2)):
         moe = L.ygg_moe_workspace_bytes(N, d, F, E, k, dt, fmt)
         assert L.ygg_moe_block_ffn_workspace_bytes(N, d, F, E, k, dt, fmt) == (N * d * 8 * es + 255) // 256 * 256 + moe
+
+
+def test_grade_quantize_argument_checks():
+    import ctypes
+
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    bits = (ctypes.c_int32 * 4)(8, 6, 6, 4)
+    bad = (ctypes.c_int32 * 4)(8, 1, 6, 4)
+    assert L.ygg_grade_quantize(None, 0, 0, ctypes.addressof(bits), 1, None, None, None, None, None) == 0
+    assert L.ygg_grade_quantize(None, 2, 4, ctypes.addressof(bad), 1, None, None, None, None, None) == -1
+    assert b"bit width" in L.ygg_last_error()
+    assert L.ygg_grade_quantize(None, 2, 4, ctypes.addressof(bits), 1, None, None, None, None, None) == -1
+    assert L.ygg_grade_quantize(None, 2, 4, None, 1, None, None, None, None, None) == -1

@@ -113,13 +113,27 @@ class CliffordMoELayer(nn.Module):
     # -- parameters ----------------------------------------------------------
     @torch.no_grad()
     def load_reference_weights(self, router_weight=None, router_bias=None, w_up=None, b_up=None, w_down=None,
-                               b_down=None, head_weight=None):
-        """Copy weights given in the reference's layouts (blade order, fp32)."""
+                               b_down=None, head_weight=None, grade_quant=None):
+        """Copy weights given in the reference's layouts (blade order, fp32).
+
+        ``grade_quant`` (a ``checkpoint.GradeQuantConfig``) passes each expert's
+        up and down weight through grade-aware quantization on the GPU
+        (``ygg_grade_quantize``, one scale per expert and grade, as the
+        reference's mixed-precision layers) and keeps the dequantized values,
+        which ``prepare()`` then lays out in the configured device format.
+        """
         for name, val in (("router_weight", router_weight), ("router_bias", router_bias), ("w_up", w_up),
                           ("b_up", b_up), ("w_down", w_down), ("b_down", b_down), ("head_weight", head_weight)):
             if val is not None:
                 p = getattr(self, name)
                 p.copy_(torch.as_tensor(val, dtype=p.dtype, device=p.device).reshape(p.shape))
+        if grade_quant is not None:
+            if not self.w_up.is_cuda:
+                raise ValueError("grade-aware quantization runs on the GPU: move the layer to the device first")
+            for p in (self.w_up, self.w_down):
+                deq, _, _, _ = ops.grade_quantize(p.detach().contiguous(), grade_quant.bits(), grade_quant.symmetric,
+                                                  codes=False)
+                p.copy_(deq)
         self._prepared = None
 
     def _param_versions(self):
@@ -281,6 +295,27 @@ class CliffordMoEBlockFFN(nn.Module):
         self.ffn_norm = CliffordLayerNorm(cfg.d_model, norm_eps, device=device)
         self.moe = CliffordMoELayer(cfg, device=device, generator=generator)
         self._workspace = None
+
+    @torch.no_grad()
+    def load_reference_checkpoint(self, path: str, ffn_norm_index: int, grade_quant=None):
+        """Load the FFN half of one ``HLMBlock`` from a reference checkpoint.
+
+        Any of the reference's ``.npz`` layouts (``checkpoint.read_reference_checkpoint``);
+        ``ffn_norm_index`` is the position of the block's ``ffn_norm.gamma`` in
+        ``model.parameters()``, the rest follows ``HLMBlock.parameters()``
+        (``hlm_block.py:230-241``).
+        """
+        from .checkpoint import hlm_block_ffn_state, read_reference_checkpoint
+
+        st = hlm_block_ffn_state(read_reference_checkpoint(path), ffn_norm_index, self.cfg.n_experts)
+        if st["w_up"].shape[1:3] != (self.cfg.d_ff, self.cfg.d_model):
+            raise ValueError(f"checkpoint experts are {st['w_up'].shape[1:3]}, layer is "
+                             f"{(self.cfg.d_ff, self.cfg.d_model)}")
+        self.ffn_norm.gamma.copy_(torch.from_numpy(st["gamma"]))
+        self.ffn_norm.beta.copy_(torch.from_numpy(st["beta"]))
+        self.moe.load_reference_weights(router_weight=st["router_weight"], router_bias=st["router_bias"],
+                                        w_up=st["w_up"], b_up=st["b_up"], w_down=st["w_down"], b_down=st["b_down"],
+                                        grade_quant=grade_quant)
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
         """x (B, T, d, 8) -> (B, T, d, 8)."""

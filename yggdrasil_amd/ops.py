@@ -7,6 +7,7 @@ There is no CPU path: CPU tensors are rejected.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -443,6 +444,31 @@ def moe_block_ffn(x: torch.Tensor, k: int, norm_gamma: torch.Tensor, norm_beta: 
                                   WFORMAT_CODE[w_up.fmt], ptr(out), ptr(topk_idx), ptr(topk_w), ptr(counts),
                                   ptr(offsets), ptr(workspace), ws_bytes, stream_handle(dev)), "moe_block_ffn")
     return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets)
+
+
+def grade_quantize(w: torch.Tensor, grade_bits=(8, 6, 6, 4), symmetric: bool = True, codes: bool = True):
+    """Grade-aware quantization per leading index (``grade_quantize.py:153-238``).
+
+    w: (T, ..., 8) fp32; each w[t] is one tensor with its own per-grade scale and
+    zero point.  Returns ``(dequantized fp32 like w, codes int16 like w or None,
+    scales (T, 4) float64, zero_points (T, 4) int32)``.
+    """
+    dev = _dev(w)
+    if w.dtype != torch.float32 or w.dim() < 2 or w.shape[-1] != 8:
+        raise ValueError("grade_quantize: w must be fp32 (T, ..., 8)")
+    bits = [int(b) for b in grade_bits]
+    if len(bits) != 4:
+        raise ValueError("grade_quantize: need one bit width per grade (4)")
+    T = w.shape[0]
+    mv = w.numel() // (8 * T) if T else 0
+    deq = torch.empty_like(w)
+    cd = torch.empty(w.shape, device=dev, dtype=torch.int16) if codes else None
+    sc = torch.empty((T, 4), device=dev, dtype=torch.float64)
+    zp = torch.empty((T, 4), device=dev, dtype=torch.int32)
+    host_bits = (ctypes.c_int32 * 4)(*bits)
+    check(lib().ygg_grade_quantize(ptr(w), T, mv, ctypes.addressof(host_bits), int(symmetric), ptr(cd), ptr(sc),
+                                   ptr(zp), ptr(deq), stream_handle(dev)), "grade_quantize")
+    return deq, cd, sc, zp
 
 
 def to_mask_order(x: torch.Tensor) -> torch.Tensor:
