@@ -186,6 +186,45 @@ int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k,
                     const void* residual, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
                     int32_t* offsets, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
 
+/* ---- backward (fp32) ---------------------------------------------------------------
+ * The reference has no MoE backward (hlm_block.py:202-206); these follow
+ * CliffordLinear.backward (holograph/layers/clifford_linear.py:125-163) and
+ * the activations' backward (holograph/layers/activations.py:135-287).
+ *
+ * W_adj (E, d_in, d_out, 8) = reverse of W (E, d_out, d_in, 8) with the two
+ * channel axes exchanged: the weights whose forward product is grad_x. */
+int ygg_adjoint_weights_f32(const float* W, int E, int d_out, int d_in, float* W_adj, ygg_stream_t stream);
+
+/* dW[e, j, i] = sum over rows r of expert e (offsets) of dy[r, j] ~a[src, i],
+ * src = gather[r] or r; db[e, j] = sum dy[r, j] when db is not NULL.  dy
+ * (rows, d_out, 8), a (.., d_in, 8), dW (E, d_out, d_in, 8): fp32 blade order. */
+int ygg_grouped_weight_grad_f32(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
+                                int d_in, int d_out, float* dW, float* db, ygg_stream_t stream);
+
+/* Gradient w.r.t. the input h of a grade-wise activation (act as in
+ * ygg_grouped_clifford_linear) given grad_out; n_mv multivectors, fp32 blade
+ * order; grad_in may alias grad_out. */
+int ygg_activation_backward(const float* h, const float* grad_out, size_t n_mv, int act, float* grad_in,
+                            ygg_stream_t stream);
+
+/* Workspace bytes of ygg_moe_backward. */
+size_t ygg_moe_backward_workspace_bytes(int N, int d, int F, int E, int k);
+
+/* Backward of ygg_moe_forward for fp32 layers with fp32 Pauli weights (format
+ * 4): the routing and the activations are recomputed from x and the same
+ * logits / router parameters the forward took.  w_*_adj are the format-4
+ * preparation of ygg_adjoint_weights_f32's output; b_up, b_down prepared
+ * biases or NULL; residual: the forward added x to its output.  Writes dx
+ * (N, d, 8), dw_up (E, F, d, 8), dw_down (E, d, F, 8) (blade order), db_up
+ * (E, F, 8), db_down (E, d, 8) and dtopk_w (N, k, the gradient of the routing
+ * weights, slots as ygg_route) when not NULL.  No gradient flows into the
+ * router. */
+int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
+                     const float* router_w, const float* router_b, const float* w_up, const float* w_up_adj,
+                     const float* b_up, const float* w_down, const float* w_down_adj, const float* b_down,
+                     int residual, const float* dout, float* dx, float* dw_up, float* db_up, float* dw_down,
+                     float* db_down, float* dtopk_w, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
+
 /* ---- weight import: grade-aware quantization -----------------------------------
  * quantize_multivector / dequantize_multivector
  * (bifrost/quantization/grade_quantize.py:86-118,153-238) on T tensors of

@@ -1,0 +1,337 @@
+// backward.hip -- the expert-FFN backward pass of the MoE layer, fp32.
+//
+// The reference's CliffordLinear.backward (holograph/layers/clifford_linear.py:125-163)
+// is two geometric matmuls with reversed operands: for y_j = sum_i W_ji x_i + b_j,
+//   dx_i = sum_j ~W_ji dy_j        (the forward product with the adjoint weights
+//                                   Wadj_ij = ~W_ji: the forward kernels run it)
+//   dW_ji = sum_rows dy_j ~x_i     (a reduction over the rows of one expert)
+//   db_j = sum_rows dy_j
+// With the Pauli map (the algebra isomorphism Cl(3,0) -> 2x2 complex matrices
+// of pauli_common.h), reversion is the conjugate transpose, so dW_ji is the
+// complex matrix sum  sum_r M(dy_rj) M(x_ri)^H: 32 real multiply-adds per row
+// and (j, i) pair instead of the 64 of the blade form.
+//
+// The activations' backward (holograph/layers/activations.py:135-287), the
+// combine's (the routing weight times the output gradient, and <dout, y> for
+// the routing weights) and the dispatch's (a sum of a token's rows) are
+// elementwise kernels here.  The reference has no MoE backward
+// (hlm_block.py:202-206); ygg_moe_backward composes these pieces for the layer.
+
+#include <hip/hip_runtime.h>
+
+#include "pauli_common.h"
+#include "ygg_common.h"
+
+namespace ygg {
+namespace {
+
+__host__ __device__ constexpr float rev_sign(int c) { return c >= 4 ? -1.f : 1.f; }  // grades 2, 3 flip
+
+// Wadj[e, i, j] = ~W[e, j, i]; one thread per output multivector.
+__global__ __launch_bounds__(256) void adjoint_kernel(const float* __restrict__ W, int E, int d_out, int d_in,
+                                                      float* __restrict__ Wadj) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)E * d_out * d_in) return;
+  const int j = (int)(n % d_out);
+  const int i = (int)((n / d_out) % d_in);
+  const int e = (int)(n / ((size_t)d_out * d_in));
+  const float* src = W + (((size_t)e * d_out + j) * d_in + i) * 8;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) Wadj[n * 8 + c] = rev_sign(c) * src[c];
+}
+
+// ---- activation backward -----------------------------------------------------
+__device__ inline float gelu_f(float v) { return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * (v + 0.044715f * v * v * v))); }
+__device__ inline float gelu_d(float v) {
+  const float c = 0.7978845608028654f;
+  const float t = tanhf(c * (v + 0.044715f * v * v * v));
+  return 0.5f * (1.0f + t) + 0.5f * v * (1.0f - t * t) * (c * (1.0f + 3.0f * 0.044715f * v * v));
+}
+__device__ inline float sigm_f(float v) { return v >= 0.f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v)); }
+__device__ inline float sigm_d(float v) {
+  const float s = sigm_f(v);
+  return s * (1.0f - s);
+}
+
+// _magnitude_gate_backward (activations.py:150-178) on the 3 components at c
+template <int ACT>
+__device__ inline void gate_backward(const float* c, const float* g, float* out) {
+  const float mag = sqrtf(c[0] * c[0] + c[1] * c[1] + c[2] * c[2] + 1e-12f);
+  const float dir[3] = {c[0] / mag, c[1] / mag, c[2] / mag};
+  const float dot = dir[0] * g[0] + dir[1] * g[1] + dir[2] * g[2];
+  float gated, deriv;
+  if constexpr (ACT == kActGelu) {
+    gated = gelu_f(mag);
+    deriv = gelu_d(mag);
+  } else {
+    gated = sigm_f(mag);
+    deriv = sigm_d(mag);
+  }
+  const float a = gated / mag, b = (deriv - gated / mag) * dot;
+#pragma unroll
+  for (int q = 0; q < 3; ++q) out[q] = a * g[q] + b * dir[q];
+}
+
+// out may alias g (each thread reads its multivector before writing it)
+template <int ACT>
+__global__ __launch_bounds__(256) void act_backward_kernel(const float* __restrict__ h, const float* g, size_t n_mv,
+                                                           float* out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= n_mv) return;
+  float x[8], gr[8], o[8];
+  const float4* hp = reinterpret_cast<const float4*>(h + n * 8);
+  const float4* gp = reinterpret_cast<const float4*>(g + n * 8);
+  const float4 h0 = hp[0], h1 = hp[1], g0 = gp[0], g1 = gp[1];
+  x[0] = h0.x; x[1] = h0.y; x[2] = h0.z; x[3] = h0.w; x[4] = h1.x; x[5] = h1.y; x[6] = h1.z; x[7] = h1.w;
+  gr[0] = g0.x; gr[1] = g0.y; gr[2] = g0.z; gr[3] = g0.w; gr[4] = g1.x; gr[5] = g1.y; gr[6] = g1.z; gr[7] = g1.w;
+  if constexpr (ACT == kActNone) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[c] = gr[c];
+  } else if constexpr (ACT == kActRelu) {
+    // zero thresholds: grade 0 passes where positive, grades 1 and 2 (|c| >= 1e-6
+    // > 0) pass through, grade 3 where non-zero
+    o[0] = x[0] > 0.f ? gr[0] : 0.f;
+#pragma unroll
+    for (int c = 1; c < 7; ++c) o[c] = gr[c];
+    o[7] = x[7] != 0.f ? gr[7] : 0.f;
+  } else {
+    o[0] = gr[0] * (ACT == kActGelu ? gelu_d(x[0]) : sigm_d(x[0]));
+    gate_backward<ACT>(x + 1, gr + 1, o + 1);
+    gate_backward<ACT>(x + 4, gr + 4, o + 4);
+    const float t = tanhf(x[7]);
+    o[7] = gr[7] * (1.0f - t * t);
+  }
+  float4* op = reinterpret_cast<float4*>(out + n * 8);
+  op[0] = make_float4(o[0], o[1], o[2], o[3]);
+  op[1] = make_float4(o[4], o[5], o[6], o[7]);
+}
+
+// ---- combine backward: dy[slot] = w dout_t; dw[t, s] = <dout_t, y[slot]> ----------
+// One wave per token.
+__global__ __launch_bounds__(256) void combine_backward_kernel(const float* __restrict__ dout,
+                                                               const float* __restrict__ y_sorted, int N, int k,
+                                                               int d, const float* __restrict__ topk_w,
+                                                               const int32_t* __restrict__ slot_pos,
+                                                               float* __restrict__ dy_sorted,
+                                                               float* __restrict__ dtopk_w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;
+  const float* go = dout + (size_t)t * d * 8;
+  for (int s = 0; s < k; ++s) {
+    const size_t row = (size_t)slot_pos[(size_t)t * k + s];
+    const float w = topk_w[(size_t)t * k + s];
+    float acc = 0.f;
+    for (int u = lane; u < d * 8; u += 64) {
+      const float gv = go[u];
+      dy_sorted[row * d * 8 + u] = w * gv;
+      if (y_sorted) acc += gv * y_sorted[row * d * 8 + u];
+    }
+    if (dtopk_w) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+      if (lane == 0) dtopk_w[(size_t)t * k + s] = acc;
+    }
+  }
+}
+
+// ---- dispatch backward: dx_t = (dout_t) + sum_s dxs[slot_pos[t, s]] ---------------
+__global__ __launch_bounds__(256) void dispatch_backward_kernel(const float* __restrict__ dxs, int N, int k, int d,
+                                                                const int32_t* __restrict__ slot_pos,
+                                                                const float* __restrict__ residual_grad,
+                                                                float* __restrict__ dx) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;  // (token, component)
+  if (n >= (size_t)N * d * 8) return;
+  const size_t t = n / ((size_t)d * 8), u = n % ((size_t)d * 8);
+  float acc = residual_grad ? residual_grad[n] : 0.f;
+  for (int s = 0; s < k; ++s) acc += dxs[(size_t)slot_pos[t * k + s] * d * 8 + u];
+  dx[n] = acc;
+}
+
+// ---- weight gradient: dW[e, j, i] = sum_r dy[r, j] ~a[src(r), i] --------------------
+// Workgroup: a 32 (j) x 32 (i) tile of one expert; thread (tj, ti) accumulates
+// the 2 x 2 pairs (tj + 16 p, ti + 16 q) as 2x2 complex matrices.  The expert's
+// rows are staged 8 at a time in LDS in Pauli coordinates.
+constexpr int kWgRows = 8;
+constexpr int kWgT = 32;
+
+__global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restrict__ dy, const float* __restrict__ a,
+                                                          const int32_t* __restrict__ gather,
+                                                          const int32_t* __restrict__ offsets, int d_in, int d_out,
+                                                          float* __restrict__ dW) {
+  __shared__ float4 sdy[kWgRows][kWgT][2];  // M(dy) as (M00, M10), (M01, M11): re, im each
+  __shared__ float4 sa[kWgRows][kWgT][2];
+  const int e = blockIdx.z;
+  const int j0 = blockIdx.x * kWgT, i0 = blockIdx.y * kWgT;
+  const int tid = threadIdx.x, tj = tid & 15, ti = tid >> 4;
+  const int row_beg = offsets[e], row_end = offsets[e + 1];
+  // C[p][q] = sum M(dy_j) M(a_i)^H, entries (re, im) of C00, C01, C10, C11
+  float acc[2][2][8];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[p][q][c] = 0.f;
+
+  // staging: thread tid loads multivector (row tid / 32, column tid % 32) of each operand
+  const int sr = tid >> 5, sc = tid & 31;
+  for (int r0 = row_beg; r0 < row_end; r0 += kWgRows) {
+    {
+      const int r = r0 + sr;
+      float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (r < row_end && j0 + sc < d_out) {
+        const float4* p = reinterpret_cast<const float4*>(dy + ((size_t)r * d_out + j0 + sc) * 8);
+        const float4 u = p[0], v = p[1];
+        x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w; x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+      }
+      if (r < row_end && i0 + sc < d_in) {
+        const size_t src = gather ? (size_t)gather[r] : (size_t)r;
+        const float4* p = reinterpret_cast<const float4*>(a + (src * d_in + i0 + sc) * 8);
+        const float4 u = p[0], v = p[1];
+        z[0] = u.x; z[1] = u.y; z[2] = u.z; z[3] = u.w; z[4] = v.x; z[5] = v.y; z[6] = v.z; z[7] = v.w;
+      }
+      float c0[4], c1[4];
+      blade_to_pauli(x, c0, c1);
+      sdy[sr][sc][0] = make_float4(c0[0], c0[1], c0[2], c0[3]);
+      sdy[sr][sc][1] = make_float4(c1[0], c1[1], c1[2], c1[3]);
+      blade_to_pauli(z, c0, c1);
+      sa[sr][sc][0] = make_float4(c0[0], c0[1], c0[2], c0[3]);
+      sa[sr][sc][1] = make_float4(c1[0], c1[1], c1[2], c1[3]);
+    }
+    __syncthreads();
+    const int nr = min(kWgRows, row_end - r0);
+    for (int rr = 0; rr < nr; ++rr) {
+      float4 D[2][2], A[2][2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        D[p][0] = sdy[rr][tj + 16 * p][0];
+        D[p][1] = sdy[rr][tj + 16 * p][1];
+        A[p][0] = sa[rr][ti + 16 * p][0];
+        A[p][1] = sa[rr][ti + 16 * p][1];
+      }
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          // column c of M: D[p][c] = (M0c re, M0c im, M1c re, M1c im)
+          // C[a][b] += sum_c D[a][c] conj(A[b][c])
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            const float4 dd = D[p][cc], aa = A[q][cc];
+            // rows a = 0, 1 of D column cc: (dd.x, dd.y), (dd.z, dd.w); rows b of A: (aa.x, aa.y), (aa.z, aa.w)
+            // C00 += D0c conj(A0c), C01 += D0c conj(A1c), C10 += D1c conj(A0c), C11 += D1c conj(A1c)
+            acc[p][q][0] += dd.x * aa.x + dd.y * aa.y;
+            acc[p][q][1] += dd.y * aa.x - dd.x * aa.y;
+            acc[p][q][2] += dd.x * aa.z + dd.y * aa.w;
+            acc[p][q][3] += dd.y * aa.z - dd.x * aa.w;
+            acc[p][q][4] += dd.z * aa.x + dd.w * aa.y;
+            acc[p][q][5] += dd.w * aa.x - dd.z * aa.y;
+            acc[p][q][6] += dd.z * aa.z + dd.w * aa.w;
+            acc[p][q][7] += dd.w * aa.z - dd.z * aa.w;
+          }
+        }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int j = j0 + tj + 16 * p, i = i0 + ti + 16 * q;
+      if (j >= d_out || i >= d_in) continue;
+      const float* C = acc[p][q];
+      float o[8];
+      pauli_to_blade(C[0], C[1], C[2], C[3], C[4], C[5], C[6], C[7], o);
+      float4* dst = reinterpret_cast<float4*>(dW + (((size_t)e * d_out + j) * d_in + i) * 8);
+      dst[0] = make_float4(0.5f * o[0], 0.5f * o[1], 0.5f * o[2], 0.5f * o[3]);
+      dst[1] = make_float4(0.5f * o[4], 0.5f * o[5], 0.5f * o[6], 0.5f * o[7]);
+    }
+}
+
+// db[e, j] = sum over the expert's rows of dy[r, j]; one thread per (expert, component).
+__global__ __launch_bounds__(256) void bias_grad_kernel(const float* __restrict__ dy,
+                                                        const int32_t* __restrict__ offsets, int d_out,
+                                                        float* __restrict__ db) {
+  const int e = blockIdx.y;
+  const int u = blockIdx.x * 256 + threadIdx.x;
+  if (u >= d_out * 8) return;
+  float acc = 0.f;
+  for (int r = offsets[e]; r < offsets[e + 1]; ++r) acc += dy[(size_t)r * d_out * 8 + u];
+  db[(size_t)e * d_out * 8 + u] = acc;
+}
+
+}  // namespace
+
+int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
+                        int d_in, int d_out, float* dW, float* db, hipStream_t stream) {
+  if (E == 0) return 0;
+  hipLaunchKernelGGL(weight_grad_kernel, dim3((d_out + kWgT - 1) / kWgT, (d_in + kWgT - 1) / kWgT, E), dim3(256), 0,
+                     stream, dy, a, gather, offsets, d_in, d_out, dW);
+  if (check_launch("weight gradient")) return -1;
+  if (db) {
+    hipLaunchKernelGGL(bias_grad_kernel, dim3((d_out * 8 + 255) / 256, E), dim3(256), 0, stream, dy, offsets, d_out,
+                       db);
+    if (check_launch("bias gradient")) return -1;
+  }
+  return 0;
+}
+
+int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream) {
+  if (n_mv == 0) return 0;
+  const dim3 grid((unsigned)((n_mv + 255) / 256));
+  switch (act) {
+    case kActNone: hipLaunchKernelGGL(act_backward_kernel<kActNone>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
+    case kActGelu: hipLaunchKernelGGL(act_backward_kernel<kActGelu>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
+    case kActRelu: hipLaunchKernelGGL(act_backward_kernel<kActRelu>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
+    default: hipLaunchKernelGGL(act_backward_kernel<kActSigmoid>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
+  }
+  return check_launch("activation backward");
+}
+
+int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
+                     const int32_t* slot_pos, float* dy_sorted, float* dtopk_w, hipStream_t stream) {
+  if (N == 0) return 0;
+  hipLaunchKernelGGL(combine_backward_kernel, dim3((N + 3) / 4), dim3(256), 0, stream, dout, y_sorted, N, k, d, topk_w,
+                     slot_pos, dy_sorted, dtopk_w);
+  return check_launch("combine backward");
+}
+
+int dispatch_backward(const float* dxs, int N, int k, int d, const int32_t* slot_pos, const float* residual_grad,
+                      float* dx, hipStream_t stream) {
+  const size_t n = (size_t)N * d * 8;
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(dispatch_backward_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dxs, N, k, d,
+                     slot_pos, residual_grad, dx);
+  return check_launch("dispatch backward");
+}
+
+}  // namespace ygg
+
+using namespace ygg;
+
+YGG_API int ygg_adjoint_weights_f32(const float* W, int E, int d_out, int d_in, float* W_adj, hipStream_t stream) {
+  YGG_CHECK_ARG(E >= 0 && d_out >= 0 && d_in >= 0, "ygg_adjoint_weights_f32: bad sizes");
+  const size_t n = (size_t)E * d_out * d_in;
+  if (n == 0) return 0;
+  YGG_CHECK_ARG(W && W_adj && W != W_adj, "ygg_adjoint_weights_f32: null or aliased pointers");
+  hipLaunchKernelGGL(adjoint_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, W, E, d_out, d_in,
+                     W_adj);
+  return check_launch("ygg_adjoint_weights_f32");
+}
+
+YGG_API int ygg_grouped_weight_grad_f32(const float* dy, const float* a, const int32_t* gather,
+                                        const int32_t* offsets, int E, int d_in, int d_out, float* dW, float* db,
+                                        hipStream_t stream) {
+  YGG_CHECK_ARG(E >= 0 && E <= 65535 && d_in >= 1 && d_out >= 1,
+                "ygg_grouped_weight_grad_f32: bad sizes E=%d d_in=%d d_out=%d", E, d_in, d_out);
+  YGG_CHECK_ARG(E == 0 || (dy && a && offsets && dW), "ygg_grouped_weight_grad_f32: null pointer argument");
+  return grouped_weight_grad(dy, a, gather, offsets, E, d_in, d_out, dW, db, stream);
+}
+
+YGG_API int ygg_activation_backward(const float* h, const float* grad_out, size_t n_mv, int act, float* grad_in,
+                                    hipStream_t stream) {
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_activation_backward: activation %d", act);
+  YGG_CHECK_ARG(n_mv == 0 || (h && grad_out && grad_in), "ygg_activation_backward: null pointer argument");
+  return activation_backward(h, grad_out, n_mv, act, grad_in, stream);
+}

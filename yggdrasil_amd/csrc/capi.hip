@@ -201,3 +201,106 @@ YGG_API int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int
                          b_down, w_format, /*residual=*/x, out, topk_idx, topk_w, counts, offsets,
                          static_cast<char*>(workspace) + xn_bytes, workspace_bytes - xn_bytes, stream);
 }
+
+// ---- backward of the layer (fp32, fp32 Pauli weights) -----------------------------
+// The routing is recomputed exactly as the forward computed it (same kernels,
+// same inputs), so perm, slot_pos and offsets match the forward's; so are the
+// activations the backward needs (h before and after the activation, y).
+// The regions of its workspace, in order (each 256-byte aligned).
+static int bw_regions(int N, int d, int F, int E, int k, size_t* r) {
+  const size_t P = (size_t)N * k;
+  int n = 0;
+  r[n++] = (size_t)N * k * 4;  // topk_idx
+  r[n++] = (size_t)N * k * 4;  // topk_w
+  r[n++] = (size_t)E * 4;      // counts
+  r[n++] = (size_t)(E + 1) * 4;  // offsets
+  r[n++] = P * 4;              // perm
+  r[n++] = P * 4;              // slot_pos
+  r[n++] = (size_t)N * E * 4;  // logits scratch
+  r[n++] = ygg_route_workspace_bytes(N, E, k);
+  r[n++] = (size_t)N * d * 32;  // x in Pauli rows
+  for (int q = 0; q < 4; ++q) r[n++] = P * F * 32;  // h_pre, h, Pauli rows of h / dh_pre, dh / dh_pre
+  for (int q = 0; q < 3; ++q) r[n++] = P * d * 32;  // y / dx rows, dy, Pauli rows of dy
+  return n;
+}
+
+YGG_API size_t ygg_moe_backward_workspace_bytes(int N, int d, int F, int E, int k) {
+  size_t r[24], b = 0;
+  const int n = bw_regions(N, d, F, E, k, r);
+  for (int q = 0; q < n; ++q) b += align256(r[q]);
+  return b;
+}
+
+YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
+                             const float* router_w, const float* router_b, const float* w_up, const float* w_up_adj,
+                             const float* b_up, const float* w_down, const float* w_down_adj, const float* b_down,
+                             int residual, const float* dout, float* dx, float* dw_up, float* db_up, float* dw_down,
+                             float* db_down, float* dtopk_w, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  YGG_CHECK_ARG(N >= 0 && d >= 1 && F >= 1 && E >= 1 && k >= 1 && k <= E, "ygg_moe_backward: bad sizes");
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_moe_backward: activation %d", act);
+  YGG_CHECK_ARG(workspace_bytes >= ygg_moe_backward_workspace_bytes(N, d, F, E, k),
+                "ygg_moe_backward: workspace of %zu bytes, need %zu", workspace_bytes,
+                ygg_moe_backward_workspace_bytes(N, d, F, E, k));
+  YGG_CHECK_ARG(logits || (router_w && router_b), "ygg_moe_backward: need logits or router parameters");
+  YGG_CHECK_ARG(w_up && w_up_adj && w_down && w_down_adj && dw_up && dw_down, "ygg_moe_backward: null weights");
+  if (N == 0) return 0;
+  YGG_CHECK_ARG(x && dout && dx, "ygg_moe_backward: null x, dout or dx");
+  const size_t P = (size_t)N * k;
+  size_t sz[24];
+  bw_regions(N, d, F, E, k, sz);
+  char* base = static_cast<char*>(workspace);
+  int next = 0;
+  auto take = [&]() {
+    void* r = base;
+    base += align256(sz[next++]);
+    return r;
+  };
+  int32_t* idx = static_cast<int32_t*>(take());
+  float* tw = static_cast<float*>(take());
+  int32_t* counts = static_cast<int32_t*>(take());
+  int32_t* offsets = static_cast<int32_t*>(take());
+  int32_t* perm = static_cast<int32_t*>(take());
+  int32_t* slot_pos = static_cast<int32_t*>(take());
+  float* lg = static_cast<float*>(take());
+  const size_t rws_bytes = align256(sz[next]);
+  void* rws = take();
+  float* xp = static_cast<float*>(take());
+  float* h_pre = static_cast<float*>(take());
+  float* h = static_cast<float*>(take());
+  float* fp = static_cast<float*>(take());  // Pauli rows of h, then of dh_pre
+  float* dh = static_cast<float*>(take());  // dh, then dh_pre in place
+  float* y = static_cast<float*>(take());   // y, then dx rows
+  float* dy = static_cast<float*>(take());
+  float* dp = static_cast<float*>(take());  // Pauli rows of dy
+
+  if (logits) {
+    if (ygg_route(logits, N, E, k, idx, tw, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
+  } else if (ygg_route_energy(x, kF32, N, d, router_w, router_b, E, k, idx, tw, counts, offsets, perm, slot_pos, lg,
+                              rws, rws_bytes, stream)) {
+    return -1;
+  }
+  // forward recompute: h_pre, h (blade), y (blade)
+  if (ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
+  if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
+    return -1;
+  if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h, 1, stream)) return -1;
+  if (ygg_pauli_rows_from_blade_f32(h, (int)P, F, fp, stream)) return -1;
+  if (dtopk_w &&
+      ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, y, 1, stream))
+    return -1;
+  // combine backward -> dy; down backward -> dh, dW_down, db_down
+  if (combine_backward(dout, dtopk_w ? y : nullptr, N, k, d, tw, slot_pos, dy, dtopk_w, stream)) return -1;
+  if (ygg_pauli_rows_from_blade_f32(dy, (int)P, d, dp, stream)) return -1;
+  if (ygg_pauli_grouped_linear_f32(dp, nullptr, (int)P, w_down_adj, nullptr, offsets, E, d, F, kActNone, dh, 1, stream))
+    return -1;
+  if (grouped_weight_grad(dy, h, nullptr, offsets, E, F, d, dw_down, db_down, stream)) return -1;
+  // activation backward (in place), up backward -> dx rows, dW_up, db_up
+  if (activation_backward(h_pre, dh, P * F, act, dh, stream)) return -1;
+  if (ygg_pauli_rows_from_blade_f32(dh, (int)P, F, fp, stream)) return -1;
+  if (ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_up_adj, nullptr, offsets, E, F, d, kActNone, y, 1, stream))
+    return -1;
+  if (grouped_weight_grad(dh, x, perm, offsets, E, d, F, dw_up, db_up, stream)) return -1;
+  // dispatch backward: each token's rows summed, plus dout when the forward added x
+  return dispatch_backward(y, N, k, d, slot_pos, residual ? dout : nullptr, dx, stream);
+}

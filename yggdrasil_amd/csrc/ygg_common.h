@@ -138,6 +138,19 @@ int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, i
                    const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
                    hipStream_t stream);
 
+// backward pieces (backward.hip), all fp32 blade order: the grouped weight
+// gradient dW[e, j, i] = sum_rows dy[r, j] ~a[src(r), i] (src through gather
+// when not NULL) and db (when not NULL); the activations' backward; the
+// combine's (dy[slot] = w dout_t, dtopk_w = <dout_t, y[slot]> when y_sorted
+// is not NULL) and the dispatch's (dx_t = residual_grad_t + sum_s dxs[slot]).
+int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
+                        int d_in, int d_out, float* dW, float* db, hipStream_t stream);
+int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream);
+int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
+                     const int32_t* slot_pos, float* dy_sorted, float* dtopk_w, hipStream_t stream);
+int dispatch_backward(const float* dxs, int N, int k, int d, const int32_t* slot_pos, const float* residual_grad,
+                      float* dx, hipStream_t stream);
+
 inline int dtype_size(int dt) { return dt == kF32 ? 4 : dt == kBF16 ? 2 : dt == kI8 ? 1 : 0; }
 
 }  // namespace ygg

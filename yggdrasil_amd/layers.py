@@ -194,13 +194,41 @@ class CliffordMoELayer(nn.Module):
                                            cfg.weight_format)
         if self._workspace is None or self._workspace.numel() < ws_bytes or self._workspace.device != x.device:
             self._workspace = torch.empty((max(ws_bytes, 1),), device=x.device, dtype=torch.uint8)
+        if self._needs_grad(x, residual):
+            out = _MoEFunction.apply(flat, res, self.w_up, self.b_up, self.w_down, self.b_down, self, logits)
+        else:
+            out = self._forward_flat(flat, logits, res)
+        return out.reshape(B, T, cfg.d_model, 8)
+
+    def _forward_flat(self, flat, logits, res):
+        cfg, prep = self.cfg, self._get_prepared()
         out, routing = ops.moe_forward(flat, cfg.top_k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"],
                                        cfg.activation, logits=logits,
                                        router_weight=self.router_weight.detach() if logits is None else None,
                                        router_bias=self.router_bias.detach() if logits is None else None,
                                        residual=res, workspace=self._workspace)
         self.last_routing = routing
-        return out.reshape(B, T, cfg.d_model, 8)
+        return out
+
+    def _needs_grad(self, x, residual) -> bool:
+        """Autograd runs for fp32 layers with 'pauli_f32' weights (the backward's format);
+        other formats compute the forward only and their output carries no graph."""
+        if not torch.is_grad_enabled() or self.cfg.weight_format != "pauli_f32":
+            return False
+        return x.requires_grad or (residual is not None and residual.requires_grad) or any(
+            p.requires_grad for p in (self.w_up, self.b_up, self.w_down, self.b_down))
+
+    @torch.no_grad()
+    def _get_adjoint(self):
+        """Adjoint expert weights (reverse, channel axes exchanged) in the 'pauli_f32' layout."""
+        key = self._param_versions()
+        if getattr(self, "_adjoint", None) is None or self._adjoint["key"] != key:
+            self._adjoint = dict(key=key,
+                                 w_up=ops.prepare_weights(ops.adjoint_weights(self.w_up.detach().contiguous()),
+                                                          "pauli_f32"),
+                                 w_down=ops.prepare_weights(ops.adjoint_weights(self.w_down.detach().contiguous()),
+                                                            "pauli_f32"))
+        return self._adjoint
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor | None = None):
         """geoformer interface: (B, T, 8 d) or (B, T, d, 8) -> (same shape, aux_loss)."""
@@ -227,6 +255,36 @@ class CliffordMoELayer(nn.Module):
         c = self.last_routing["counts"].float()
         f = c / (c.sum() + 1e-12)
         return ((f - 1.0 / self.cfg.n_experts) ** 2).sum()
+
+
+class _MoEFunction(torch.autograd.Function):
+    """The layer as one autograd node: forward ``ygg_moe_forward``, backward ``ygg_moe_backward``.
+
+    Gradients reach x, the residual and the expert weights and biases.  The
+    routing is a constant of the backward, as in the reference, whose router
+    has no backward (``hlm_block.py:202-206``).
+    """
+
+    @staticmethod
+    def forward(ctx, flat, res, w_up, b_up, w_down, b_down, layer, logits):
+        ctx.layer, ctx.has_res = layer, res is not None
+        ctx.save_for_backward(flat, logits if logits is not None else flat.new_empty(0))
+        ctx.has_logits = logits is not None
+        return layer._forward_flat(flat, logits, res)
+
+    @staticmethod
+    def backward(ctx, dout):
+        flat, logits = ctx.saved_tensors
+        layer = ctx.layer
+        cfg = layer.cfg
+        prep, adj = layer._get_prepared(), layer._get_adjoint()
+        use_logits = ctx.has_logits
+        dx, dWu, dbu, dWd, dbd, _ = ops.moe_backward(
+            flat, cfg.top_k, prep["w_up"], adj["w_up"], prep["w_down"], adj["w_down"], dout.contiguous(),
+            prep["b_up"], prep["b_down"], cfg.activation, logits=logits if use_logits else None,
+            router_weight=None if use_logits else layer.router_weight.detach(),
+            router_bias=None if use_logits else layer.router_bias.detach())
+        return dx, (dout if ctx.has_res else None), dWu, dbu, dWd, dbd, None, None
 
 
 class CliffordLinear(nn.Module):

@@ -446,6 +446,80 @@ def moe_block_ffn(x: torch.Tensor, k: int, norm_gamma: torch.Tensor, norm_beta: 
     return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets)
 
 
+# ---------------------------------------------------------------------------
+# backward (fp32)
+# ---------------------------------------------------------------------------
+
+
+def adjoint_weights(w: torch.Tensor) -> torch.Tensor:
+    """(E, d_out, d_in, 8) -> (E, d_in, d_out, 8): reverse of each weight, channel axes exchanged."""
+    dev = _dev(w)
+    if w.dtype != torch.float32 or w.dim() != 4 or w.shape[-1] != 8:
+        raise ValueError("adjoint_weights: w must be fp32 (E, d_out, d_in, 8)")
+    E, d_out, d_in = w.shape[:3]
+    out = torch.empty((E, d_in, d_out, 8), device=dev, dtype=torch.float32)
+    check(lib().ygg_adjoint_weights_f32(ptr(w), E, d_out, d_in, ptr(out), stream_handle(dev)), "adjoint_weights")
+    return out
+
+
+def grouped_weight_grad(dy: torch.Tensor, a: torch.Tensor, offsets: torch.Tensor, E: int,
+                        gather: torch.Tensor | None = None, with_bias: bool = True):
+    """dW[e, j, i] = sum over expert e's rows of dy[r, j] ~a[src(r), i]; (dW, db or None). fp32 blade order."""
+    dev = _dev(dy, a, offsets, gather)
+    d_out, d_in = dy.shape[1], a.shape[1]
+    dW = torch.empty((E, d_out, d_in, 8), device=dev, dtype=torch.float32)
+    db = torch.empty((E, d_out, 8), device=dev, dtype=torch.float32) if with_bias else None
+    check(lib().ygg_grouped_weight_grad_f32(ptr(dy), ptr(a), ptr(gather), ptr(offsets), E, d_in, d_out, ptr(dW),
+                                            ptr(db), stream_handle(dev)), "grouped_weight_grad")
+    return dW, db
+
+
+def activation_backward(h: torch.Tensor, grad_out: torch.Tensor, act: str) -> torch.Tensor:
+    """Gradient w.r.t. the input of a grade-wise activation; h, grad_out (..., 8) fp32."""
+    dev = _dev(h, grad_out)
+    if h.shape != grad_out.shape or h.dtype != torch.float32 or grad_out.dtype != torch.float32:
+        raise ValueError("activation_backward: h and grad_out must be fp32 tensors of one shape")
+    out = torch.empty_like(h)
+    check(lib().ygg_activation_backward(ptr(h), ptr(grad_out), h.numel() // 8, ACT_CODE[act], ptr(out),
+                                        stream_handle(dev)), "activation_backward")
+    return out
+
+
+def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: PreparedWeights, w_down: PreparedWeights,
+                 w_down_adj: PreparedWeights, dout: torch.Tensor, b_up: torch.Tensor | None = None,
+                 b_down: torch.Tensor | None = None, act: str = "gelu", logits: torch.Tensor | None = None,
+                 router_weight: torch.Tensor | None = None, router_bias: torch.Tensor | None = None,
+                 residual: bool = False, workspace: torch.Tensor | None = None):
+    """Backward of ``moe_forward`` (fp32, ``pauli_f32`` weights). Returns dx, dW_up, db_up, dW_down, db_down, dtopk_w."""
+    dev = _dev(x, dout, logits)
+    for pw in (w_up, w_up_adj, w_down, w_down_adj):
+        if pw.fmt != "pauli_f32":
+            raise ValueError("moe_backward: weights must be prepared as 'pauli_f32'")
+    if x.dtype != torch.float32 or dout.dtype != torch.float32 or dout.shape != x.shape:
+        raise ValueError("moe_backward: x and dout must be fp32 (N, d, 8) of one shape")
+    Nt, d = x.shape[0], x.shape[1]
+    E, F = w_up.E, w_up.d_out
+    if (w_up_adj.d_out, w_up_adj.d_in, w_down.d_out, w_down.d_in, w_down_adj.d_out, w_down_adj.d_in) != \
+            (d, F, d, F, F, d):
+        raise ValueError("moe_backward: weight shapes do not chain d -> F -> d")
+    ws_bytes = lib().ygg_moe_backward_workspace_bytes(Nt, d, F, E, k)
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dx = torch.empty_like(x)
+    dWu, dbu = torch.empty((E, F, d, 8), **f32), torch.empty((E, F, 8), **f32)
+    dWd, dbd = torch.empty((E, d, F, 8), **f32), torch.empty((E, d, 8), **f32)
+    dtw = torch.empty((Nt, k), **f32)
+    rw = router_weight.float().contiguous() if router_weight is not None else None
+    rb = router_bias.float().contiguous() if router_bias is not None else None
+    check(lib().ygg_moe_backward(ptr(x), Nt, d, F, E, k, ACT_CODE[act], ptr(logits), ptr(rw), ptr(rb),
+                                 ptr(w_up.data), ptr(w_up_adj.data), ptr(b_up), ptr(w_down.data),
+                                 ptr(w_down_adj.data), ptr(b_down), int(residual), ptr(dout), ptr(dx), ptr(dWu),
+                                 ptr(dbu), ptr(dWd), ptr(dbd), ptr(dtw), ptr(workspace), ws_bytes,
+                                 stream_handle(dev)), "moe_backward")
+    return dx, dWu, dbu, dWd, dbd, dtw
+
+
 def grade_quantize(w: torch.Tensor, grade_bits=(8, 6, 6, 4), symmetric: bool = True, codes: bool = True):
     """Grade-aware quantization per leading index (``grade_quantize.py:153-238``).
 
