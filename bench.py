@@ -1,6 +1,6 @@
 """Benchmark of the MoE-HLM expert layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5,c3b] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5,c3b,c1t,c3t] [--no-cpu-baseline]
 
 A step is one forward pass of the layer over one batch of synthetic input
 (inputs resident in HBM before timing starts).  The headline workload is
@@ -9,7 +9,8 @@ multivectors, E=32 experts, top-4, expert FFN 128 -> 512 -> 128 with the
 grade-wise GELU, Zipf(1.2) expert load.  Configs 1, 2, 4 and 5 are timed in
 the same run and reported under "configs", with "c3b": config 3 inside the
 FFN half of the block, x + moe(ffn_norm(x)) (CliffordLayerNorm in front, the
-residual added in the combine).
+residual added in the combine), and "c1t" / "c3t": a training step (forward and
+backward, fp32) at the config 1 and 3 shapes.
 
 One JSON line is printed.  ``roofline`` covers the dominant kernel, the
 grouped CliffordLinear MFMA kernel (both expert products), from HIP events
@@ -36,7 +37,7 @@ PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
 # measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
 PAULI_C3_TRAFFIC_BYTES = 410.9e6
-SEEDS = {"c1": 1, "c1l": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3t": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
@@ -49,6 +50,9 @@ CONFIGS = {
     "c3l": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="bf16", logits="zipf", layers=1),
     "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1),
     "c5": dict(N=4096, d=256, E=64, k=2, F=1024, dtype="bf16", fmt="pauli", logits="normal_bias", layers=12),
+    # training step (forward + backward, fp32 Pauli weights) at the config 1 and config 3 shapes
+    "c1t": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1, train=True),
+    "c3t": dict(N=8192, d=128, E=32, k=4, F=512, dtype="f32", fmt="pauli_f32", logits="zipf", layers=1, train=True),
     # the FFN half of the block around config 3: x + moe(ffn_norm(x)) (pre-norm, residual)
     "c3b": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, block=True),
 }
@@ -59,7 +63,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b")
+    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b,c1t,c3t")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=256)
     # a plain device copy of this many MiB, run (3 times) before the configs: the reference
@@ -290,6 +294,48 @@ def run_block_config(torch, ops, name, c, steps, warmup):
                 grade_quantize_bytes=gq_bytes, grade_quantize_hbm_frac=gq_bytes / (ms_gq * 1e-3) / PEAK_HBM)
 
 
+def run_train_config(torch, ops, name, c, steps, warmup):
+    """Forward + backward of the layer (fp32 Pauli weights); the weight-gradient kernel timed alone."""
+    x, layers = make_inputs(torch, c, seed=SEEDS[name])
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    L0 = layers[0]
+    w_up, w_down = L0.pop("w_up"), L0.pop("w_down")
+    pu, pd = ops.prepare_weights(w_up, c["fmt"]), ops.prepare_weights(w_down, c["fmt"])
+    au = ops.prepare_weights(ops.adjoint_weights(w_up), c["fmt"])
+    ad = ops.prepare_weights(ops.adjoint_weights(w_down), c["fmt"])
+    del w_up, w_down
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEEDS[name] + 200)
+    dout = torch.randn(x.shape, generator=g, device="cuda")
+    logits, rw, rb = L0.get("logits"), L0.get("router_w"), L0.get("router_b")
+    ws_f = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype, c["fmt"]), device="cuda", dtype=torch.uint8)
+    ws_b = torch.empty(ops.lib().ygg_moe_backward_workspace_bytes(N, d, F, E, k), device="cuda", dtype=torch.uint8)
+    out = torch.empty_like(x)
+
+    def step():
+        ops.moe_forward(x, k, pu, pd, None, None, "gelu", logits=logits, router_weight=rw, router_bias=rb,
+                        workspace=ws_f, out=out)
+        ops.moe_backward(x, k, pu, au, pd, ad, dout, None, None, "gelu", logits=logits, router_weight=rw,
+                         router_bias=rb, workspace=ws_b)
+
+    ms = time_fn(torch, step, steps, warmup)
+    # the weight gradients alone: up (rows of x through perm, F outputs) and down (h rows, d outputs)
+    r = ops.route(logits if logits is not None else ops.router_energy_logits(x, rw, rb), k)
+    P = N * k
+    dh = torch.randn(P, F, 8, generator=g, device="cuda")
+    dy = torch.randn(P, d, 8, generator=g, device="cuda")
+    h = torch.randn(P, F, 8, generator=g, device="cuda")
+    ms_wg_up = time_fn(torch, lambda: ops.grouped_weight_grad(dh, x, r.offsets, E, gather=r.perm), steps, warmup)
+    ms_wg_down = time_fn(torch, lambda: ops.grouped_weight_grad(dy, h, r.offsets, E), steps, warmup)
+    flops_proj = 128.0 * d * F * P
+    return dict(workload=name, N=N, d=d, E=E, k=k, F=F, dtype="f32", weights=c["fmt"],
+                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3),
+                kernels_ms=dict(weight_grad_up=ms_wg_up, weight_grad_down=ms_wg_down),
+                step_tflops=6 * flops_proj / (ms * 1e-3) / 1e12,
+                weight_grad_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,
+                weight_grad_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32)
+
+
 def calibrate_gemm(torch):
     """hipBLASLt (torch.matmul) bf16 GEMM rates on N(0,1) operands, two timed passes per shape."""
     out = []
@@ -436,6 +482,8 @@ def main():
         print(f"[bench] {name} {config_label(c)}", file=sys.stderr, flush=True)
         if name == "c2":
             results[name] = run_c2(torch, ops, c, args.steps, args.warmup)
+        elif c.get("train"):
+            results[name] = run_train_config(torch, ops, name, c, args.steps, args.warmup)
         elif c.get("block"):
             results[name] = run_block_config(torch, ops, name, c, args.steps, args.warmup)
         else:
