@@ -102,7 +102,7 @@ def _run_layer_case(name, fmt_override=None):
         assert np.array_equal(rt["counts"].cpu().numpy(), ref[pre + "counts"]), "expert counts"
         assert np.allclose(rt["topk_w"].cpu().numpy(), ref[pre + "w"][:, ::-1], rtol=1e-5, atol=1e-6)
         x = y
-    got = x.float().cpu().numpy()
+    got = x.detach().float().cpu().numpy()
     err = normwise_err(got, ref["out"])
     tol = TOL_BF16 if bf16 else TOL_F32
     assert err < tol, f"{name}: normwise error {err:.3e} >= {tol}"
@@ -132,7 +132,8 @@ def test_geoformer_interface_flat_input():
     say("geoformer flat interface c1")
     out, aux = layer(xf)
     assert out.shape == xf.shape and aux.dim() == 0
-    assert normwise_err(out.cpu().numpy().reshape(ref["out"].shape), ref["out"]) < TOL_F32
+    assert out.requires_grad  # fp32 Pauli layers are autograd nodes
+    assert normwise_err(out.detach().cpu().numpy().reshape(ref["out"].shape), ref["out"]) < TOL_F32
     c = ref["counts"].astype(np.float64)
     f = c / c.sum()
     assert abs(aux.item() - ((f - 1 / p["E"]) ** 2).sum()) < 1e-6
@@ -229,3 +230,36 @@ def test_module_rejects_cpu_tensors():
     layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
     with pytest.raises(ValueError):
         layer.moe_forward(torch.zeros(1, 4, 8, 8))
+
+
+@pytest.mark.parametrize("N,d,F,E,k,act", [(64, 128, 512, 32, 2, "gelu"), (1, 16, 32, 4, 1, "relu"),
+                                           (128, 64, 96, 64, 2, "sigmoid"), (37, 40, 72, 9, 3, "gelu"),
+                                           (100, 32, 64, 16, 2, "relu")])
+def test_decode_routing_inside_up_product(N, d, F, E, k, act):
+    """Decode layers given logits route inside the up product: the routing arrays equal
+    ygg_route's bit for bit (ties included), the output is the oracle's at the int8 bound."""
+    yggdrasil_amd, ops = _mods()
+    g = np.random.default_rng(N * 3 + E)
+    x = _inputs.bf16_round(g.standard_normal((N, d, 8), dtype=np.float32))
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F, bias_std=0.2)
+    logits = np.round(g.standard_normal((N, E)), 1).astype(np.float32)  # many exact ties
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, activation=act,
+                                     dtype=torch.bfloat16, weight_format="int8", router="logits")
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    lt = torch.from_numpy(logits).cuda()
+    say(f"decode routed up N={N} d={d} F={F} E={E} k={k} {act}")
+    y = layer.moe_forward(torch.from_numpy(x).cuda().bfloat16().reshape(1, N, d, 8), logits=lt)
+    y = y.float().cpu().numpy().reshape(N, d, 8)
+    r = ops.route(lt, k)
+    for key in ("topk_idx", "topk_w", "counts", "offsets"):
+        assert torch.equal(layer.last_routing[key], getattr(r, key)), key
+    idx, w = r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy()
+    wu_q = moe.dequantize_int8(*moe.quantize_int8(wu))
+    wd_q = moe.dequantize_int8(*moe.quantize_int8(wd))
+    ref = np.zeros((N, d, 8), np.float32)
+    for t in range(N):
+        for s in np.argsort(idx[t]):
+            e = idx[t, s]
+            ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu_q[e], bu[e], wd_q[e], bd[e], act)[0]
+    assert normwise_err(y, ref) < TOL_BF16

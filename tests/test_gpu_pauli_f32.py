@@ -142,7 +142,7 @@ def test_layer_pauli_f32_large_down_splits():
     say(f"layer pauli_f32 N={N} d={d} F={F} E={E} k={k}")
     xt = torch.from_numpy(x).cuda()
     out = layer.moe_forward(xt, logits=torch.from_numpy(logits_np).cuda(), residual=xt)
-    out = out.cpu().numpy().reshape(N, d, 8)
+    out = out.detach().cpu().numpy().reshape(N, d, 8)
     idx = layer.last_routing["topk_idx"].cpu().numpy()
     idx_o, w = moe.route_topk(moe.softmax(logits_np), k)
     assert np.array_equal(idx, idx_o)

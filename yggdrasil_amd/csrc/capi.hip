@@ -119,7 +119,12 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
   p += align256(P * F * 8 * es);
   void* ys = p;
 
-  if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
+  // decode layers given logits route inside their up product (no routing launch)
+  const bool decode = decode_shape((int)P, E, w_format);
+  const bool fused_route = decode && logits && decode_route_fusable(N, E, k, d);
+  if (fused_route) {
+    // routed below
+  } else if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
     if (ygg_route_energy(x, dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos,
                          lg, rws, rws_bytes, stream))
       return -1;
@@ -153,13 +158,19 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
       return -1;
     return ygg_combine(ys, kBF16, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
   }
-  if (decode_shape((int)P, E, w_format)) {
+  if (decode) {
     // decode: weight-streaming products; the up product reads x through perm (no
-    // dispatch copy), the down product runs in K splits whose fp32 partial planes
-    // the combine adds in split order
-    if (decode_linear_gather(static_cast<const uint16_t*>(x), perm, (int)P, static_cast<const int8_t*>(w_up), s_up,
-                             b_up, offsets, E, d, F, act, static_cast<uint16_t*>(h), stream))
+    // dispatch copy) -- or routes itself --, the down product runs in K splits whose
+    // fp32 partial planes the combine adds in split order
+    if (fused_route) {
+      if (decode_linear_gather_routed(static_cast<const uint16_t*>(x), logits, N, E, k, topk_idx, topk_w, counts,
+                                      offsets, perm, slot_pos, static_cast<const int8_t*>(w_up), s_up, b_up, d, F,
+                                      act, static_cast<uint16_t*>(h), stream))
+        return -1;
+    } else if (decode_linear_gather(static_cast<const uint16_t*>(x), perm, (int)P, static_cast<const int8_t*>(w_up),
+                                    s_up, b_up, offsets, E, d, F, act, static_cast<uint16_t*>(h), stream)) {
       return -1;
+    }
     if (decode_linear_partial(static_cast<const uint16_t*>(h), (int)P, static_cast<const int8_t*>(w_down), s_down,
                               b_down, offsets, E, F, d, static_cast<float*>(ys), stream))
       return -1;

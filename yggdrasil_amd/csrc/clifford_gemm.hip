@@ -29,6 +29,7 @@
 // first row) by walking the device-side offsets, so the grid is sized from
 // host-known bounds (ceil(P/BM) + E tiles) with no host synchronisation.
 
+#include "route_select.h"
 #include "ygg_common.h"
 
 namespace ygg {
@@ -410,15 +411,42 @@ __device__ inline void decode_step(f32x4_t (&acc)[kDecCB][8], const uint4 a, con
 #undef YGG_STEP
 }
 
-template <int ACT, bool GATHER, bool OUT_BLADE, int OUT_DT, bool PARTIAL, bool MULTI>
+// Routing inside the up product (decode layers given logits, N <= kFuseMaxTokens):
+// every workgroup selects the experts of all N tokens itself (the same
+// select_from_logits as the routing kernels), so the layer needs no routing
+// launch.  Its logits loads go out before the weight stream, which therefore
+// stays in flight while it selects.  The workgroups of column block 0 also
+// write the routing arrays of their expert's slots (every slot belongs to one
+// expert), which the down product and the combine read.
+struct DecodeRoute {
+  const float* logits;
+  int N, E, k;
+  int32_t* topk_idx;
+  float* topk_w;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* perm;
+  int32_t* slot_pos;
+};
+constexpr int kFuseMaxTokens = 128;                    // 4 passes of 32 tokens
+constexpr int kFuseMaxSlots = kFuseMaxTokens * kMaxTopK;
+constexpr int kFusePasses = kFuseMaxTokens / (64 * kDecWaves / kSelLanes);
+
+template <int ACT, bool GATHER, bool OUT_BLADE, int OUT_DT, bool PARTIAL, bool MULTI, int RQ = 0>
 __global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(
     const uint16_t* __restrict__ A, const int32_t* __restrict__ gather, const int8_t* __restrict__ Wq,
     const float* __restrict__ wscale, const float* __restrict__ bias, const int32_t* __restrict__ offsets, int d_in,
-    int d_out, int k_split, int P_max, void* __restrict__ Y) {
+    int d_out, int k_split, int P_max, void* __restrict__ Y, DecodeRoute rt = DecodeRoute{}) {
+  static_assert(RQ == 0 || (GATHER && !MULTI && !PARTIAL), "routing is fused into the one-chunk up product only");
   __shared__ float part[kDecWaves][kDecRows][kDecJ][9];  // +1 float of padding per multivector
+  __shared__ int32_t rows_tok[RQ > 0 ? kFuseMaxTokens : 1];  // fused routing: this expert's tokens in order
   const int e = blockIdx.x, split = blockIdx.z;
-  const int row_beg = offsets[e], row_end = offsets[e + 1];
-  if (row_beg >= row_end) return;
+  int row_beg = 0, row_end = 0;
+  if constexpr (RQ == 0) {
+    row_beg = offsets[e];
+    row_end = offsets[e + 1];
+    if (row_beg >= row_end) return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int jl = lane & 15, g = lane >> 4;  // output column (B) / row (A) within a block; K group
   const int col0 = blockIdx.y * kDecJ;
@@ -543,11 +571,109 @@ __global__ __launch_bounds__(64 * kDecWaves) void grouped_cl_decode_i8(
   // row and are not stored); its byte offset into x is src * d_in * 16
   auto row_src = [&](int r0) {
     int src = min(r0 + jl, row_end - 1);
-    if constexpr (GATHER) src = gather[src];
+    if constexpr (RQ > 0) src = rows_tok[src - row_beg];
+    else if constexpr (GATHER) src = gather[src];
     return src;
   };
 
-  if constexpr (!MULTI) {
+  if constexpr (RQ > 0) {
+    // ---- fused routing: logits, then the weight stream, then the selection
+    const int N = rt.N, E = rt.E, k = rt.k;
+    const int j = tid & (kSelLanes - 1);
+    float lg[kFusePasses][RQ];
+#pragma unroll
+    for (int ps = 0; ps < kFusePasses; ++ps) {
+      const int t = ps * (64 * kDecWaves / kSelLanes) + (tid >> 3);
+#pragma unroll
+      for (int q = 0; q < RQ; ++q) {
+        const int x = j + kSelLanes * q;
+        lg[ps][q] = (t < N && x < E) ? rt.logits[(size_t)t * E + x] : -INFINITY;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(k_lo);
+    load_epilogue();
+    __builtin_amdgcn_sched_barrier(0);
+    // LDS scratch on top of part (free until the first finish())
+    int32_t* s_sel = reinterpret_cast<int32_t*>(&part[0][0][0][0]);
+    float* s_w = reinterpret_cast<float*>(s_sel + kFuseMaxTokens * kMaxTopK);
+    int32_t* s_cnt = reinterpret_cast<int32_t*>(s_w + kFuseMaxTokens * kMaxTopK);
+    int32_t* s_off = s_cnt + kMaxExperts;
+    int32_t* s_wv = s_off + kMaxExperts + 1;
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
+#pragma unroll
+    for (int ps = 0; ps < kFusePasses; ++ps) {
+      if (ps * (64 * kDecWaves / kSelLanes) < N) {
+        const int t = ps * (64 * kDecWaves / kSelLanes) + (tid >> 3);
+        int se;
+        float sw;
+        select_from_logits<RQ>(lg[ps], E, k, t < N, j, lane, se, sw);
+        if (se >= 0) {
+          s_sel[t * k + j] = se;
+          s_w[t * k + j] = sw;
+        }
+      }
+    }
+    __syncthreads();
+    for (int f = tid; f < N * k; f += 64 * kDecWaves) atomicAdd(&s_cnt[s_sel[f]], 1);
+    // this expert's tokens in ascending order: a ballot per wave, then wave bases
+    bool mine = false;
+    if (tid < N)
+      for (int s = 0; s < k; ++s) mine |= s_sel[tid * k + s] == e;
+    const uint64_t bal = __ballot(mine);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    if (lane == 0) s_wv[wave] = __popcll(bal);
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the counts over experts
+      const int c = lane < E ? s_cnt[lane] : 0;
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      if (lane < E) s_off[lane] = incl - c;
+      if (lane == E - 1) s_off[E] = incl;
+    }
+    if (mine) {
+      int base = 0;
+      for (int w = 0; w < wave; ++w) base += s_wv[w];
+      rows_tok[base + __popcll(bal & lt_mask)] = tid;
+    }
+    __syncthreads();
+    row_beg = s_off[e];
+    row_end = s_off[e + 1];
+    if (blockIdx.y == 0) {  // the routing arrays of this expert's slots, for the later launches
+      for (int r = tid; r < row_end - row_beg; r += 64 * kDecWaves) {
+        const int t = rows_tok[r];
+        int s = 0;
+        while (s_sel[t * k + s] != e) ++s;
+        rt.topk_idx[t * k + s] = e;
+        rt.topk_w[t * k + s] = s_w[t * k + s];
+        rt.slot_pos[t * k + s] = row_beg + r;
+        rt.perm[row_beg + r] = t;
+      }
+      if (tid == 0) {
+        rt.counts[e] = row_end - row_beg;
+        rt.offsets[e] = row_beg;
+        if (e == E - 1) rt.offsets[E] = row_end;
+      }
+    }
+    __syncthreads();  // part is overwritten from here on
+    if (row_beg >= row_end) return;
+    {
+      f32x4_t acc[kDecCB][8];
+      zero(acc);
+      chunk(acc, k_lo, (uint32_t)row_src(row_beg) * d_in * 16);
+      finish(acc, row_beg);
+    }
+    for (int r0 = row_beg + kDecRows; r0 < row_end; r0 += kDecRows) {
+      f32x4_t acc[kDecCB][8];
+      zero(acc);
+      chunk(acc, k_lo, (uint32_t)row_src(r0) * d_in * 16);
+      finish(acc, r0);
+    }
+  } else if constexpr (!MULTI) {
     // one chunk (the decode case): the weights stay in registers for every row
     // block, and the first block's row index is loaded ahead of them (vmcnt
     // retires in order, so its wait does not wait for the weight stream)
@@ -862,6 +988,42 @@ int ygg::decode_linear_gather(const uint16_t* x, const int32_t* perm, int P_max,
   YGG_CHECK_ARG(decode_offsets_fit(P_max, d_in), "decode up product: %d rows x %d inputs too large", P_max, d_in);
   return decode_dispatch(act, dim3(E, (d_out + kDecJ - 1) / kDecJ, 1), stream, false, kBF16, x, perm, Wq, scales,
                          bias, offsets, d_in, d_out, decode_splits(d_in) * kDecChunk, P_max, h);
+}
+
+bool ygg::decode_route_fusable(int N, int E, int k, int d_in) {
+  return N >= 1 && N <= kFuseMaxTokens && N * k <= kFuseMaxSlots && E <= kMaxExperts && k <= kMaxTopK &&
+         d_in <= kDecChunk;
+}
+
+template <int ACT>
+static void launch_routed(dim3 grid, hipStream_t st, int Q, const uint16_t* x, const int8_t* W, const float* sc,
+                          const float* bias, int d_in, int d_out, int P_max, uint16_t* h, const DecodeRoute& rt) {
+  if (Q <= 4)
+    grouped_cl_decode_i8<ACT, true, false, kBF16, false, false, 4><<<grid, 64 * kDecWaves, 0, st>>>(
+        x, nullptr, W, sc, bias, nullptr, d_in, d_out, kDecChunk, P_max, h, rt);
+  else
+    grouped_cl_decode_i8<ACT, true, false, kBF16, false, false, 8><<<grid, 64 * kDecWaves, 0, st>>>(
+        x, nullptr, W, sc, bias, nullptr, d_in, d_out, kDecChunk, P_max, h, rt);
+}
+
+int ygg::decode_linear_gather_routed(const uint16_t* x, const float* logits, int N, int E, int k, int32_t* topk_idx,
+                                     float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                                     int32_t* slot_pos, const int8_t* Wq, const float* scales, const float* bias,
+                                     int d_in, int d_out, int act, uint16_t* h, hipStream_t stream) {
+  YGG_CHECK_ARG(decode_route_fusable(N, E, k, d_in), "decode routed up product: N=%d E=%d k=%d d_in=%d", N, E, k,
+                d_in);
+  const int P_max = N * k;
+  YGG_CHECK_ARG(decode_offsets_fit(P_max, d_in), "decode up product: %d rows x %d inputs too large", P_max, d_in);
+  const DecodeRoute rt{logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos};
+  const dim3 grid(E, (d_out + kDecJ - 1) / kDecJ, 1);
+  const int Q = (E + kSelLanes - 1) / kSelLanes;
+  switch (act) {
+    case kActNone: launch_routed<kActNone>(grid, stream, Q, x, Wq, scales, bias, d_in, d_out, P_max, h, rt); break;
+    case kActGelu: launch_routed<kActGelu>(grid, stream, Q, x, Wq, scales, bias, d_in, d_out, P_max, h, rt); break;
+    case kActRelu: launch_routed<kActRelu>(grid, stream, Q, x, Wq, scales, bias, d_in, d_out, P_max, h, rt); break;
+    default: launch_routed<kActSigmoid>(grid, stream, Q, x, Wq, scales, bias, d_in, d_out, P_max, h, rt); break;
+  }
+  return check_launch("grouped_cl_decode_i8 (routed)");
 }
 
 int ygg::decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,

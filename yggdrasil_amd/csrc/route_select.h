@@ -1,0 +1,183 @@
+// route_select.h -- the per-token routing selection (CliffordRouter's softmax,
+// top-k and renormalisation, clifford_router.py:18-21,54-104), eight lanes per
+// token, shared by the routing kernels (route.hip) and the decode up product
+// that routes inside its own workgroups (clifford_gemm.hip).
+#pragma once
+
+#include "ygg_common.h"
+
+namespace ygg {
+
+constexpr int kMaxExperts = 64;
+constexpr int kMaxTopK = 8;
+constexpr int kSelLanes = 8;                          // lanes per token
+
+// The logits of one token straight from its activation row (the reference's
+// CliffordRouter energy signature, clifford_router.py:54-90): per-grade sums of
+// squares over the row (lane j takes multivectors j, j + 8, ...; the eight lanes
+// of the token are combined by a shuffle tree), normalised by their sum + 1e-12,
+// then the (E, 4) map and bias.  Lane j returns the logits of experts j + 8 q.
+template <int Q>
+__device__ inline void energy_logits(const void* __restrict__ x, int x_dtype, int d, const float* __restrict__ rw,
+                                     const float* __restrict__ rb, int E, int t, bool active, int j, float (&p)[Q]) {
+  float gs[4] = {0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    for (int i = j; i < d; i += kSelLanes) {
+      float v[8];
+      if (x_dtype == kF32) {
+        const float4* q4 = reinterpret_cast<const float4*>(static_cast<const float*>(x) + ((size_t)t * d + i) * 8);
+        const float4 a = q4[0], b = q4[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + ((size_t)t * d + i) * 8);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[2 * c] = bf16_bits_to_f32((uint16_t)(w[c] & 0xffff));
+          v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(w[c] >> 16));
+        }
+      }
+      gs[0] += v[0] * v[0];
+      gs[1] += v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      gs[2] += v[4] * v[4] + v[5] * v[5] + v[6] * v[6];
+      gs[3] += v[7] * v[7];
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < kSelLanes; o <<= 1)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) gs[c] += __shfl_xor(gs[c], o);
+  const float tot = gs[0] + gs[1] + gs[2] + gs[3] + 1e-12f;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    float l = -INFINITY;
+    if (active && e < E) {
+      l = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) l += (gs[c] / tot) * rw[e * 4 + c];
+      l += rb[e];
+    }
+    p[q] = l;
+  }
+}
+
+// The selection of one token, eight lanes per token (lane j = tid % 8), from
+// its logits p (lane j: experts j + 8 q, -inf past E or for an inactive token):
+// probabilities, top-k and renormalised weights; lane j returns slot j
+// (expert, weight), or expert -1 for j >= k or an inactive token.
+template <int Q>  // Q >= ceil(E / 8) logits per lane (-inf past E)
+__device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool active, int j, int lane, int& out_e,
+                                          float& out_w) {
+  // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
+  float m = -INFINITY;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) m = fmaxf(m, p[q]);
+#pragma unroll
+  for (int o = 1; o < kSelLanes; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    p[q] = (e < E) ? expf(__fsub_rn(p[q], m)) : 0.f;
+  }
+  // NumPy pairwise sum of the row: rows of fewer than 8 values are summed in
+  // order; otherwise accumulator j sums the elements j, j+8, ... below
+  // E8 = E - E % 8, the eight accumulators are combined as a tree and the
+  // remaining E % 8 values are added in order.
+  const int E8 = E - (E & 7);
+  float sum;
+  if (E < 8) {
+    sum = 0.f;
+    for (int e = 0; e < E; ++e) sum = __fadd_rn(sum, __shfl(p[0], (lane & ~7) + e));
+  } else {
+    float r = p[0];
+#pragma unroll
+    for (int q = 1; q < Q; ++q)
+      if (j + kSelLanes * q < E8) r = __fadd_rn(r, p[q]);
+    r = __fadd_rn(r, __shfl_xor(r, 1));
+    r = __fadd_rn(r, __shfl_xor(r, 2));
+    r = __fadd_rn(r, __shfl_xor(r, 4));
+    sum = r;
+    // the remaining E % 8 values are element E / 8 of lanes 0 .. E % 8 - 1 (any Q >= ceil(E / 8))
+    float prem = p[0];
+#pragma unroll
+    for (int q = 1; q < Q; ++q)
+      if (q == (E >> 3)) prem = p[q];
+    for (int e = E8; e < E; ++e) sum = __fadd_rn(sum, __shfl(prem, (lane & ~7) + (e & 7)));
+  }
+  const float denom = __fadd_rn(sum, 1e-12f);
+#pragma unroll
+  for (int q = 0; q < Q; ++q) p[q] = __fdiv_rn(p[q], denom);
+
+  // ---- top-k: k rounds of (max probability, then min index) over the 8 lanes.
+  // The selection key orders NaN probabilities below every real one, so the
+  // order is total, all 8 lanes agree on each winner and every slot gets a
+  // valid expert (with NaN logits the weights are unspecified).
+  float key[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) key[q] = (p[q] == p[q]) ? p[q] : -1.0f;
+  int sel[kMaxTopK];
+  float wsel[kMaxTopK];
+  uint32_t taken = 0;  // bit q: this lane's element q is selected
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    sel[s] = 0;
+    wsel[s] = 0.f;
+    if (s < k) {
+      float bv = -2.0f;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const int e = j + kSelLanes * q;
+        if (e < E && !((taken >> q) & 1u) && (key[q] > bv || (key[q] == bv && e < bi))) {
+          bv = key[q];
+          bi = e;
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < kSelLanes; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      // k <= E: at least one candidate remains, so bi is a valid expert
+      sel[s] = bi;
+      wsel[s] = bv;
+      if ((bi & (kSelLanes - 1)) == j) taken |= 1u << ((bi / kSelLanes) & 31);
+    }
+  }
+  // renormalise; the sum runs from the least to the most probable slot
+  float ssum = 0.f;
+#pragma unroll
+  for (int s = kMaxTopK - 1; s >= 0; --s)
+    if (s < k) ssum = __fadd_rn(ssum, wsel[s]);
+  ssum = __fadd_rn(ssum, 1e-12f);
+  int my_e = -1;  // lane j holds slot j
+  float my_w = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s)
+    if (s == j && s < k) {
+      my_e = sel[s];
+      my_w = __fdiv_rn(wsel[s], ssum);
+    }
+  out_e = active ? my_e : -1;
+  out_w = my_w;
+}
+
+template <int Q>
+__device__ inline void select_token(const float* __restrict__ logits, int E, int k, int t, bool active, int j,
+                                    int lane, int& out_e, float& out_w) {
+  float p[Q];
+  const float* row = logits + (size_t)(active ? t : 0) * E;
+#pragma unroll
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    p[q] = (active && e < E) ? row[e] : -INFINITY;
+  }
+  select_from_logits<Q>(p, E, k, active, j, lane, out_e, out_w);
+}
+
+}  // namespace ygg

@@ -129,6 +129,14 @@ int decode_splits(int d_in);
 int decode_linear_gather(const uint16_t* x, const int32_t* perm, int P_max, const int8_t* Wq, const float* scales,
                          const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act, uint16_t* h,
                          hipStream_t stream);
+// The up product with the routing inside it (decode layers given logits):
+// whether (N, E, k, d_in) qualifies, and the launch, which also writes the
+// routing arrays (as ygg_route) for the down product and the combine.
+bool decode_route_fusable(int N, int E, int k, int d_in);
+int decode_linear_gather_routed(const uint16_t* x, const float* logits, int N, int E, int k, int32_t* topk_idx,
+                                float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_pos,
+                                const int8_t* Wq, const float* scales, const float* bias, int d_in, int d_out, int act,
+                                uint16_t* h, hipStream_t stream);
 int decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
                           const int32_t* offsets, int E, int d_in, int d_out, float* y_planes, hipStream_t stream);
 
