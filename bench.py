@@ -295,7 +295,8 @@ def run_block_config(torch, ops, name, c, steps, warmup):
 
 
 def run_train_config(torch, ops, name, c, steps, warmup):
-    """Forward + backward of the layer (fp32 Pauli weights); the weight-gradient kernel timed alone."""
+    """Forward + backward of the layer (fp32 Pauli weights), as autograd runs it (no routing-weight
+    gradient); the weight-gradient kernel timed alone."""
     x, layers = make_inputs(torch, c, seed=SEEDS[name])
     N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
     L0 = layers[0]
@@ -316,7 +317,7 @@ def run_train_config(torch, ops, name, c, steps, warmup):
         ops.moe_forward(x, k, pu, pd, None, None, "gelu", logits=logits, router_weight=rw, router_bias=rb,
                         workspace=ws_f, out=out)
         ops.moe_backward(x, k, pu, au, pd, ad, dout, None, None, "gelu", logits=logits, router_weight=rw,
-                         router_bias=rb, workspace=ws_b)
+                         router_bias=rb, workspace=ws_b, routing_grad=False)
 
     ms = time_fn(torch, step, steps, warmup)
     # the weight gradients alone: up (rows of x through perm, F outputs) and down (h rows, d outputs)

@@ -106,6 +106,22 @@ __global__ __launch_bounds__(256) void act_backward_kernel(const float* __restri
   op[1] = make_float4(o[4], o[5], o[6], o[7]);
 }
 
+// The forward activation of blade-order rows (the same activate_blade the fused
+// epilogues apply), for the backward's recompute of h from h before the activation.
+template <int ACT>
+__global__ __launch_bounds__(256) void act_forward_kernel(const float* __restrict__ h, size_t n_mv,
+                                                          float* __restrict__ out) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= n_mv) return;
+  const float4* hp = reinterpret_cast<const float4*>(h + n * 8);
+  const float4 h0 = hp[0], h1 = hp[1];
+  float y[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+  activate_blade<ACT>(y);
+  float4* op = reinterpret_cast<float4*>(out + n * 8);
+  op[0] = make_float4(y[0], y[1], y[2], y[3]);
+  op[1] = make_float4(y[4], y[5], y[6], y[7]);
+}
+
 // ---- combine backward: dy[slot] = w dout_t; dw[t, s] = <dout_t, y[slot]> ----------
 // One wave per token.
 __global__ __launch_bounds__(256) void combine_backward_kernel(const float* __restrict__ dout,
@@ -158,7 +174,7 @@ constexpr int kWgT = 32;
 __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restrict__ dy, const float* __restrict__ a,
                                                           const int32_t* __restrict__ gather,
                                                           const int32_t* __restrict__ offsets, int d_in, int d_out,
-                                                          float* __restrict__ dW) {
+                                                          float* __restrict__ dW, float* __restrict__ db) {
   __shared__ float4 sdy[kWgRows][kWgT][2];  // M(dy) as (M00, M10), (M01, M11): re, im each
   __shared__ float4 sa[kWgRows][kWgT][2];
   const int e = blockIdx.z;
@@ -174,8 +190,11 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
 #pragma unroll
       for (int c = 0; c < 8; ++c) acc[p][q][c] = 0.f;
 
-  // staging: thread tid loads multivector (row tid / 32, column tid % 32) of each operand
+  // staging: thread tid loads multivector (row tid / 32, column tid % 32) of each operand;
+  // the workgroups of i-tile 0 also sum the staged dy rows for db (blade order)
   const int sr = tid >> 5, sc = tid & 31;
+  const bool bias_tile = db != nullptr && blockIdx.y == 0;
+  float bsum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int r0 = row_beg; r0 < row_end; r0 += kWgRows) {
     {
       const int r = r0 + sr;
@@ -191,6 +210,9 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
         const float4 u = p[0], v = p[1];
         z[0] = u.x; z[1] = u.y; z[2] = u.z; z[3] = u.w; z[4] = v.x; z[5] = v.y; z[6] = v.z; z[7] = v.w;
       }
+      if (bias_tile)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) bsum[c] += x[c];
       float c0[4], c1[4];
       blade_to_pauli(x, c0, c1);
       sdy[sr][sc][0] = make_float4(c0[0], c0[1], c0[2], c0[3]);
@@ -234,6 +256,24 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
     }
     __syncthreads();
   }
+  if (bias_tile) {  // the 8 staging rows' partial sums, added in row order
+    float* red = reinterpret_cast<float*>(&sdy[0][0][0]);  // free after the last chunk's barrier
+#pragma unroll
+    for (int c = 0; c < 8; ++c) red[(sr * kWgT + sc) * 8 + c] = bsum[c];
+    __syncthreads();
+    if (sr == 0 && j0 + sc < d_out) {
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float v = 0.f;
+        for (int q = 0; q < kWgRows; ++q) v += red[(q * kWgT + sc) * 8 + c];
+        o[c] = v;
+      }
+      float4* dst = reinterpret_cast<float4*>(db + ((size_t)e * d_out + j0 + sc) * 8);
+      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+  }
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -249,32 +289,14 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
     }
 }
 
-// db[e, j] = sum over the expert's rows of dy[r, j]; one thread per (expert, component).
-__global__ __launch_bounds__(256) void bias_grad_kernel(const float* __restrict__ dy,
-                                                        const int32_t* __restrict__ offsets, int d_out,
-                                                        float* __restrict__ db) {
-  const int e = blockIdx.y;
-  const int u = blockIdx.x * 256 + threadIdx.x;
-  if (u >= d_out * 8) return;
-  float acc = 0.f;
-  for (int r = offsets[e]; r < offsets[e + 1]; ++r) acc += dy[(size_t)r * d_out * 8 + u];
-  db[(size_t)e * d_out * 8 + u] = acc;
-}
-
 }  // namespace
 
 int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
                         int d_in, int d_out, float* dW, float* db, hipStream_t stream) {
   if (E == 0) return 0;
   hipLaunchKernelGGL(weight_grad_kernel, dim3((d_out + kWgT - 1) / kWgT, (d_in + kWgT - 1) / kWgT, E), dim3(256), 0,
-                     stream, dy, a, gather, offsets, d_in, d_out, dW);
-  if (check_launch("weight gradient")) return -1;
-  if (db) {
-    hipLaunchKernelGGL(bias_grad_kernel, dim3((d_out * 8 + 255) / 256, E), dim3(256), 0, stream, dy, offsets, d_out,
-                       db);
-    if (check_launch("bias gradient")) return -1;
-  }
-  return 0;
+                     stream, dy, a, gather, offsets, d_in, d_out, dW, db);
+  return check_launch("weight gradient");
 }
 
 int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream) {
@@ -287,6 +309,18 @@ int activation_backward(const float* h, const float* g, size_t n_mv, int act, fl
     default: hipLaunchKernelGGL(act_backward_kernel<kActSigmoid>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
   }
   return check_launch("activation backward");
+}
+
+int activation_forward(const float* h, size_t n_mv, int act, float* out, hipStream_t stream) {
+  if (n_mv == 0) return 0;
+  const dim3 grid((unsigned)((n_mv + 255) / 256));
+  switch (act) {
+    case kActNone: hipLaunchKernelGGL(act_forward_kernel<kActNone>, grid, dim3(256), 0, stream, h, n_mv, out); break;
+    case kActGelu: hipLaunchKernelGGL(act_forward_kernel<kActGelu>, grid, dim3(256), 0, stream, h, n_mv, out); break;
+    case kActRelu: hipLaunchKernelGGL(act_forward_kernel<kActRelu>, grid, dim3(256), 0, stream, h, n_mv, out); break;
+    default: hipLaunchKernelGGL(act_forward_kernel<kActSigmoid>, grid, dim3(256), 0, stream, h, n_mv, out); break;
+  }
+  return check_launch("activation forward");
 }
 
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,

@@ -295,7 +295,7 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   if (ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
   if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
     return -1;
-  if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h, 1, stream)) return -1;
+  if (activation_forward(h_pre, P * F, act, h, stream)) return -1;
   if (ygg_pauli_rows_from_blade_f32(h, (int)P, F, fp, stream)) return -1;
   if (dtopk_w &&
       ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, y, 1, stream))

@@ -154,6 +154,7 @@ int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, i
 int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
                         int d_in, int d_out, float* dW, float* db, hipStream_t stream);
 int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream);
+int activation_forward(const float* h, size_t n_mv, int act, float* out, hipStream_t stream);
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
                      const int32_t* slot_pos, float* dy_sorted, float* dtopk_w, hipStream_t stream);
 int dispatch_backward(const float* dxs, int N, int k, int d, const int32_t* slot_pos, const float* residual_grad,

@@ -283,7 +283,7 @@ class _MoEFunction(torch.autograd.Function):
             flat, cfg.top_k, prep["w_up"], adj["w_up"], prep["w_down"], adj["w_down"], dout.contiguous(),
             prep["b_up"], prep["b_down"], cfg.activation, logits=logits if use_logits else None,
             router_weight=None if use_logits else layer.router_weight.detach(),
-            router_bias=None if use_logits else layer.router_bias.detach())
+            router_bias=None if use_logits else layer.router_bias.detach(), routing_grad=False)
         return dx, (dout if ctx.has_res else None), dWu, dbu, dWd, dbd, None, None
 
 

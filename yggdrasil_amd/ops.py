@@ -489,8 +489,12 @@ def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: Prepa
                  w_down_adj: PreparedWeights, dout: torch.Tensor, b_up: torch.Tensor | None = None,
                  b_down: torch.Tensor | None = None, act: str = "gelu", logits: torch.Tensor | None = None,
                  router_weight: torch.Tensor | None = None, router_bias: torch.Tensor | None = None,
-                 residual: bool = False, workspace: torch.Tensor | None = None):
-    """Backward of ``moe_forward`` (fp32, ``pauli_f32`` weights). Returns dx, dW_up, db_up, dW_down, db_down, dtopk_w."""
+                 residual: bool = False, workspace: torch.Tensor | None = None, routing_grad: bool = True):
+    """Backward of ``moe_forward`` (fp32, ``pauli_f32`` weights). Returns dx, dW_up, db_up, dW_down, db_down, dtopk_w.
+
+    ``routing_grad=False`` skips the routing-weight gradient (dtopk_w is None), and with it
+    the recompute of the expert outputs it needs.
+    """
     dev = _dev(x, dout, logits)
     for pw in (w_up, w_up_adj, w_down, w_down_adj):
         if pw.fmt != "pauli_f32":
@@ -509,7 +513,7 @@ def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: Prepa
     dx = torch.empty_like(x)
     dWu, dbu = torch.empty((E, F, d, 8), **f32), torch.empty((E, F, 8), **f32)
     dWd, dbd = torch.empty((E, d, F, 8), **f32), torch.empty((E, d, 8), **f32)
-    dtw = torch.empty((Nt, k), **f32)
+    dtw = torch.empty((Nt, k), **f32) if routing_grad else None
     rw = router_weight.float().contiguous() if router_weight is not None else None
     rb = router_bias.float().contiguous() if router_bias is not None else None
     check(lib().ygg_moe_backward(ptr(x), Nt, d, F, E, k, ACT_CODE[act], ptr(logits), ptr(rw), ptr(rb),
