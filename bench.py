@@ -37,12 +37,15 @@ PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
 # measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
 PAULI_C3_TRAFFIC_BYTES = 410.9e6
-SEEDS = {"c1": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3t": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3t": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
-    "c1": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1),
-    # config 1 again with the fp32 8x8 L(w)-block products on the vector units (comparison)
+    # config 1: the router is CliffordLinear(d -> E) then the scalar part (the step computes it)
+    "c1": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="head", layers=1),
+    # config 1 with CliffordRouter's grade-energy router, and with the fp32 8x8 L(w)-block products
+    # on the vector units (comparisons)
+    "c1e": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1),
     "c1l": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="f32", logits="energy", layers=1),
     "c2": dict(N=16384, d=128, E=16, k=2, F=0, dtype="f32", fmt=None, logits="normal", layers=1),
     "c3": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1),
@@ -109,6 +112,8 @@ def make_inputs(torch, c, seed=0):
             bonus = (k - torch.arange(k, device=dev, dtype=torch.float32)).expand(N, k)
             lg.scatter_add_(1, ranking[chosen], bonus)
             L["logits"] = lg.contiguous()
+        elif c["logits"] == "head":  # CliffordLinear(d -> E) weights; logits = scalar part of its output
+            L["head_w"] = rn(1, E, d, 8) / (8.0 * d) ** 0.5
         else:  # energy router
             L["router_w"] = 0.1 * rn(E, 4)
             L["router_b"] = torch.zeros(E, device=dev)
@@ -142,8 +147,13 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     for L in layers:
         prepared.append(dict(
             w_up=ops.prepare_weights(L["w_up"], c["fmt"]), w_down=ops.prepare_weights(L["w_down"], c["fmt"]),
-            logits=L.get("logits"), router_w=L.get("router_w"), router_b=L.get("router_b")))
+            logits=L.get("logits"), router_w=L.get("router_w"), router_b=L.get("router_b"),
+            head=L["head_w"][0].contiguous() if "head_w" in L else None))
         del L["w_up"], L["w_down"]
+
+    def head_logits(cur, P):
+        # the layer's CliffordLinear head (CliffordMoELayer._head_logits): scalar part of W_h x
+        return ops.router_head_logits(cur, P["head"])
     torch.cuda.synchronize()
     ws = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype, c["fmt"]), device="cuda", dtype=torch.uint8)
     bufs = [torch.empty_like(x), torch.empty_like(x)]
@@ -154,7 +164,8 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         cur = x
         for li, P in enumerate(prepared):
             out = bufs[li % 2]
-            _, rt = ops.moe_forward(cur, k, P["w_up"], P["w_down"], None, None, "gelu", logits=P["logits"],
+            lg = head_logits(cur, P) if P["head"] is not None else P["logits"]
+            _, rt = ops.moe_forward(cur, k, P["w_up"], P["w_down"], None, None, "gelu", logits=lg,
                                     router_weight=P["router_w"], router_bias=P["router_b"],
                                     residual=cur if resid else None, workspace=ws, out=out)
             cur = out
@@ -164,7 +175,11 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     counts = info["rt"]["counts"].cpu()
     # the dominant kernel: both grouped expert products of layer 0, timed alone
     P0 = prepared[0]
-    logits = P0["logits"] if P0["logits"] is not None else ops.router_energy_logits(x, P0["router_w"], P0["router_b"])
+    if P0["head"] is not None:
+        logits = head_logits(x, P0)
+    else:
+        logits = P0["logits"] if P0["logits"] is not None else ops.router_energy_logits(x, P0["router_w"],
+                                                                                         P0["router_b"])
     r = ops.route(logits, k)
     fmt_code = ops.WFORMAT_CODE[c["fmt"]]
     L = ops.lib()

@@ -57,6 +57,13 @@ int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K
  * logits[t, e] = sum_g energy[t, g] / (sum energy + 1e-12) * W_r[e, g] + b_r[e].
  * x: (N, d, 8) of x_dtype; router_w (E, 4), router_b (E); logits (N, E);
  * energy (N, 4) or NULL. */
+/* Router of the CliffordLinear-head kind (hlm.py:109,141-145; the TinyHLMMoE
+ * layer of the reference's config 1): logits (N, E) = scalar part of
+ * CliffordLinear(d -> E) with weights head_w (E, d, 8) fp32 blade order and no
+ * bias, in the fp32 order of clifford_linear.py:101-123 (bit-exact). */
+int ygg_router_head_logits(const void* x, int x_dtype, int N, int d, const float* head_w, int E, float* logits,
+                           ygg_stream_t stream);
+
 int ygg_router_energy_logits(const void* x, int x_dtype, int N, int d, const float* router_w,
                              const float* router_b, int E, float* logits, float* energy, ygg_stream_t stream);
 

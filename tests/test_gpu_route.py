@@ -220,3 +220,20 @@ def test_route_energy_fused_against_oracle(N, d, E, k, dtype):
     for a, b in [(got.perm, ref.perm), (got.slot_pos, ref.slot_pos), (got.counts, ref.counts),
                  (got.offsets, ref.offsets)]:
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("N,d,E,dtype", [(256, 64, 8, "f32"), (33, 7, 5, "f32"), (100, 16, 64, "bf16"),
+                                         (3000, 32, 16, "f32")])
+def test_router_head_logits_bit_exact(N, d, E, dtype):
+    """The CliffordLinear(d -> E) head's scalar part in the reference's fp32 order, bit for bit."""
+    ops = _ops()
+    g = np.random.default_rng(N + d + E)
+    x = g.standard_normal((N, d, 8), dtype=np.float32)
+    W = (g.standard_normal((E, d, 8)) / np.sqrt(8 * d)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    if dtype == "bf16":
+        xt = xt.bfloat16()
+        x = xt.float().cpu().numpy()
+    say(f"router head logits N={N} d={d} E={E} {dtype}")
+    got = ops.router_head_logits(xt, torch.from_numpy(W).cuda()).cpu().numpy()
+    assert np.array_equal(got, moe.clifford_linear(x, W, None)[..., 0])

@@ -361,6 +361,65 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   return 0;
 }
 
+// The CliffordLinear(d -> E) head's scalar part (the router of the TinyHLMMoE-style
+// layer, hlm.py:109,141-145): logits[t, e] = <sum_i W[e, i] x[t, i]>_0, in the fp32
+// order of CliffordLinear.forward's geom_matmul (clifford_linear.py:101-123 over
+// rune/ops/batched.py:72-82): for each i in turn, the eight diagonal terms
+// (s_c W_c) x_c of the product's scalar part are added to zero in component order
+// (s = -1 on grades 2 and 3), and that product is added to the running sum.  No
+// multiply-add contraction, so the logits are the reference's bit for bit.  One
+// thread per (token, expert); the expert's weights are read by 64 neighbouring
+// threads at once (L1/L2 broadcast), x rows by the E threads of a token.
+template <typename XT>
+__global__ __launch_bounds__(256) void router_head_logits_kernel(const XT* __restrict__ x, int N, int d,
+                                                                 const float* __restrict__ head_w, int E,
+                                                                 float* __restrict__ logits) {
+#pragma clang fp contract(off)
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)N * E) return;
+  const int t = (int)(n / E), e = (int)(n % E);
+  const XT* xr = x + (size_t)t * d * 8;
+  const float* wr = head_w + (size_t)e * d * 8;
+  float acc = 0.f;
+  for (int i = 0; i < d; ++i) {
+    float xv[8];
+    if constexpr (sizeof(XT) == 4) {
+      const float4 a = reinterpret_cast<const float4*>(xr + i * 8)[0], b = reinterpret_cast<const float4*>(xr + i * 8)[1];
+      xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    } else {
+      const uint4 q = *reinterpret_cast<const uint4*>(xr + i * 8);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        xv[2 * c] = __builtin_bit_cast(float, w[c] << 16);
+        xv[2 * c + 1] = __builtin_bit_cast(float, w[c] & 0xffff0000u);
+      }
+    }
+    const float4 a = reinterpret_cast<const float4*>(wr + i * 8)[0], b = reinterpret_cast<const float4*>(wr + i * 8)[1];
+    const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float p = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) p = p + (c < 4 ? wv[c] : -wv[c]) * xv[c];
+    acc = acc + p;
+  }
+  logits[n] = acc;
+}
+
+YGG_API int ygg_router_head_logits(const void* x, int x_dtype, int N, int d, const float* head_w, int E,
+                                   float* logits, hipStream_t stream) {
+  YGG_CHECK_ARG(x_dtype == kF32 || x_dtype == kBF16, "ygg_router_head_logits: x dtype %d unsupported", x_dtype);
+  YGG_CHECK_ARG(N >= 0 && d >= 1 && E >= 1, "ygg_router_head_logits: bad sizes N=%d d=%d E=%d", N, d, E);
+  YGG_CHECK_ARG(N == 0 || (x && head_w && logits), "ygg_router_head_logits: null pointer");
+  if (N == 0) return 0;
+  const unsigned blocks = (unsigned)(((size_t)N * E + 255) / 256);
+  if (x_dtype == kF32)
+    router_head_logits_kernel<float><<<blocks, 256, 0, stream>>>(static_cast<const float*>(x), N, d, head_w, E, logits);
+  else
+    router_head_logits_kernel<uint16_t><<<blocks, 256, 0, stream>>>(static_cast<const uint16_t*>(x), N, d, head_w, E,
+                                                                    logits);
+  return check_launch("router_head_logits");
+}
+
 YGG_API int ygg_router_energy_logits(const void* x, int x_dtype, int N, int d, const float* router_w,
                                      const float* router_b, int E, float* logits, float* energy,
                                      hipStream_t stream) {

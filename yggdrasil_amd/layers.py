@@ -145,8 +145,7 @@ class CliffordMoELayer(nn.Module):
         fmt = self.cfg.weight_format
         head = None
         if self.head_weight is not None:
-            head = ops.prepare_weights(self.head_weight.detach().unsqueeze(0),
-                                       "f32" if self.cfg.dtype == torch.float32 else "bf16")
+            head = self.head_weight.detach().float().contiguous()
         self._prepared = dict(
             key=self._param_versions(),
             w_up=ops.prepare_weights(self.w_up.detach(), fmt),
@@ -164,12 +163,8 @@ class CliffordMoELayer(nn.Module):
 
     # -- forward ---------------------------------------------------------------
     def _head_logits(self, flat_x: torch.Tensor, prep) -> torch.Tensor:
-        """CliffordLinear(d -> E) then grade 0 (hlm.py:109,141-145 pattern)."""
-        Nt = flat_x.shape[0]
-        xs = ops.to_mask_order(flat_x)
-        offsets = torch.tensor([0, Nt], device=flat_x.device, dtype=torch.int32)
-        y = ops.grouped_clifford_linear(xs, prep["head"], offsets, None, "none", out_dtype=torch.float32)
-        return y[..., 0].contiguous()
+        """CliffordLinear(d -> E) then grade 0 (hlm.py:109,141-145), bit-exact with the reference."""
+        return ops.router_head_logits(flat_x, prep["head"])
 
     def moe_forward(self, x: torch.Tensor, logits: torch.Tensor | None = None,
                     residual: torch.Tensor | None = None) -> torch.Tensor:
@@ -343,7 +338,8 @@ class CliffordMoEBlockFFN(nn.Module):
 
     With the energy router or caller logits the whole sub-layer is one library
     call (``ygg_moe_block_ffn``): the norm, then the MoE layer on the normed
-    tokens with x added back in its combine.
+    tokens with x added back in its combine.  Inference only: its output
+    carries no autograd graph.
     """
 
     def __init__(self, cfg: MoEHLMConfig, device=None, generator: torch.Generator | None = None,
@@ -383,9 +379,10 @@ class CliffordMoEBlockFFN(nn.Module):
         if x.dtype != cfg.dtype:
             raise ValueError(f"layer dtype is {cfg.dtype}, input is {x.dtype}")
         if cfg.router == "clifford_head" and logits is None:
-            x_norm = self.ffn_norm(x)
-            return moe.moe_forward(x_norm, logits=moe._head_logits(
-                x_norm.reshape(-1, cfg.d_model, 8), moe._get_prepared()), residual=x)
+            with torch.no_grad():  # the block is inference-only (the norm has no backward here)
+                x_norm = self.ffn_norm(x)
+                return moe.moe_forward(x_norm, logits=moe._head_logits(
+                    x_norm.reshape(-1, cfg.d_model, 8), moe._get_prepared()), residual=x)
         if cfg.router == "logits" and logits is None:
             raise ValueError("router='logits' needs logits")
         B, T = x.shape[:2]

@@ -98,6 +98,22 @@ def router_energy_logits(x: torch.Tensor, router_weight: torch.Tensor, router_bi
     return (logits, energy) if return_energy else logits
 
 
+def router_head_logits(x: torch.Tensor, head_weight: torch.Tensor) -> torch.Tensor:
+    """Scalar part of CliffordLinear(d -> E) (``hlm.py:109,141-145``). x: (N, d, 8); head_weight (E, d, 8)."""
+    dev = _dev(x)
+    if x.dim() != 3 or x.shape[2] != 8 or not x.is_contiguous():
+        raise ValueError(f"router_head_logits: x must be contiguous (N, d, 8), got {tuple(x.shape)}")
+    Nt, d = x.shape[0], x.shape[1]
+    E = head_weight.shape[0]
+    if tuple(head_weight.shape) != (E, d, 8):
+        raise ValueError(f"router_head_logits: head_weight must be (E, {d}, 8)")
+    hw = head_weight.float().contiguous()
+    logits = torch.empty((Nt, E), device=dev, dtype=torch.float32)
+    check(lib().ygg_router_head_logits(ptr(x), _dtype_code(x), Nt, d, ptr(hw), E, ptr(logits), stream_handle(dev)),
+          "router_head_logits")
+    return logits
+
+
 def route(logits: torch.Tensor, k: int, out: Routing | None = None, workspace: torch.Tensor | None = None) -> Routing:
     """Softmax, top-k (lowest index wins ties) and the expert counting sort.
 
