@@ -1,6 +1,6 @@
 """Benchmark of the MoE-HLM expert layer on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5,c3b,c1t,c3t] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c3,c1,c2,c4,c5,c3b,c3ep,c1t,c3t] [--no-cpu-baseline]
 
 A step is one forward pass of the layer over one batch of synthetic input
 (inputs resident in HBM before timing starts).  The headline workload is
@@ -37,7 +37,7 @@ PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
 # measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
 PAULI_C3_TRAFFIC_BYTES = 410.9e6
-SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3t": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
@@ -56,6 +56,9 @@ CONFIGS = {
     # training step (forward + backward, fp32 Pauli weights) at the config 1 and config 3 shapes
     "c1t": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1, train=True),
     "c3t": dict(N=8192, d=128, E=32, k=4, F=512, dtype="f32", fmt="pauli_f32", logits="zipf", layers=1, train=True),
+    # config 3 at one GPU's expert-parallel share (8 GPUs x 4 experts): the GPU holding the most
+    # rows under the Zipf load, its rows delivered contiguously (the all-to-all is not on one GPU)
+    "c3ep": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, ep=8),
     # the FFN half of the block around config 3: x + moe(ffn_norm(x)) (pre-norm, residual)
     "c3b": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, block=True),
 }
@@ -66,7 +69,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b,c1t,c3t")
+    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b,c3ep,c1t,c3t")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=256)
     # a plain device copy of this many MiB, run (3 times) before the configs: the reference
@@ -269,6 +272,44 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     return res
 
 
+def run_ep_config(torch, ops, name, c, steps, warmup):
+    """One GPU's share of config 3 under expert parallelism: its experts' rows, Pauli products."""
+    x, layers = make_inputs(torch, c, seed=SEEDS[name])
+    N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    G = c["ep"]
+    L0 = layers[0]
+    r = ops.route(L0["logits"], k)
+    off = r.offsets.cpu()
+    per = E // G
+    rows = [int(off[(g + 1) * per] - off[g * per]) for g in range(G)]
+    g = max(range(G), key=lambda i: rows[i])
+    e0, beg, end = g * per, int(off[g * per]), int(off[(g + 1) * per])
+    x_local = x[r.perm[beg:end].long()].contiguous()  # the rows the all-to-all delivers, expert-grouped
+    offs = (r.offsets[e0:e0 + per + 1] - r.offsets[e0]).contiguous()
+    pu = ops.prepare_weights(L0["w_up"][e0:e0 + per].contiguous(), c["fmt"])
+    pd = ops.prepare_weights(L0["w_down"][e0:e0 + per].contiguous(), c["fmt"])
+    del L0["w_up"], L0["w_down"]
+    P = end - beg
+    Lb, st, dt = ops.lib(), ops.stream_handle(), ops.DTYPE_CODE[x.dtype]
+    xp = torch.empty((P, 2, d, 4), device="cuda", dtype=x.dtype)
+    h = torch.empty((P, 2, F, 4), device="cuda", dtype=x.dtype)
+    y = torch.empty((P, d, 8), device="cuda", dtype=x.dtype)
+
+    def step():
+        ops.check(Lb.ygg_pauli_rows_from_blade(x_local.data_ptr(), P, d, xp.data_ptr(), st))
+        ops.check(Lb.ygg_pauli_grouped_linear(xp.data_ptr(), 1, None, P, pu.data.data_ptr(), None, offs.data_ptr(),
+                                              per, d, F, 1, h.data_ptr(), 0, dt, st))
+        ops.check(Lb.ygg_pauli_grouped_linear(h.data_ptr(), 1, None, P, pd.data.data_ptr(), None, offs.data_ptr(),
+                                              per, F, d, 0, y.data_ptr(), 1, dt, st))
+
+    ms = time_fn(torch, step, steps, warmup)
+    flops = 2 * 128.0 * d * F * P
+    return dict(workload=name, gpus_modelled=G, experts_here=list(range(e0, e0 + per)), rows_here=P,
+                rows_per_gpu=rows, straggler_ratio=P / (N * k / G), ms_per_step=ms,
+                rows_per_s=P / (ms * 1e-3), expert_tflops=flops / (ms * 1e-3) / 1e12,
+                expert_mfma_frac=flops / (ms * 1e-3) / PEAK_BF16)
+
+
 def run_block_config(torch, ops, name, c, steps, warmup):
     """x + moe(ffn_norm(x)) through ygg_moe_block_ffn; the norm kernel also timed alone."""
     x, layers = make_inputs(torch, c, seed=SEEDS[name])
@@ -457,10 +498,37 @@ def cpu_baseline(c, sample_rows):
     del y
     per_row = t_ffn / sample_rows
     t_layer = t_rdc + per_row * N * k
+    # the C restatement with OpenMP on every host core this process may use, on 8x the rows
+    threads = len(os.sched_getaffinity(0))
+    rows_p = min(8 * sample_rows, N * k)
+    xs_p = np.ascontiguousarray(np.transpose(np.resize(x, (rows_p, d, 8)), (1, 0, 2)))
+    t0 = time.perf_counter()
+    hp = np.transpose(native.c_geom_matmul(wu, xs_p, threads=threads), (1, 0, 2))
+    hp = moe.gelu(hp)
+    native.c_geom_matmul(wd, np.ascontiguousarray(np.transpose(hp, (1, 0, 2))), threads=threads)
+    t_par = time.perf_counter() - t0
+    host = dict(nproc=os.cpu_count(), affinity=threads, cpu=_cpu_model(),
+                env={k_: os.environ[k_] for k_ in ("OMP_NUM_THREADS", "MKL_NUM_THREADS", "OPENBLAS_NUM_THREADS")
+                     if k_ in os.environ})
     return dict(value=N / t_layer, unit="tokens/s", cores=1, kind=kind,
                 sample=(f"{config_label(c)}: expert FFN on {sample_rows} of {N * k} token-expert rows via {what}, "
                         f"extrapolated linearly in FLOPs; NumPy routing/dispatch/combine over all {N} tokens "
-                        f"({t_rdc:.2f} s); measured {t_ffn:.1f} s"))
+                        f"({t_rdc:.2f} s); measured {t_ffn:.1f} s"),
+                parallel=dict(value=N / (t_rdc + t_par / rows_p * N * k), unit="tokens/s", cores=threads, kind="port",
+                              sample=(f"oracle C restatement of cl3_batch_geom_matmul with OpenMP on {threads} "
+                                      f"threads, {rows_p} rows, measured {t_par:.2f} s, same extrapolation")),
+                host=host)
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def config_label(c):
@@ -498,6 +566,8 @@ def main():
         print(f"[bench] {name} {config_label(c)}", file=sys.stderr, flush=True)
         if name == "c2":
             results[name] = run_c2(torch, ops, c, args.steps, args.warmup)
+        elif c.get("ep"):
+            results[name] = run_ep_config(torch, ops, name, c, args.steps, args.warmup)
         elif c.get("train"):
             results[name] = run_train_config(torch, ops, name, c, args.steps, args.warmup)
         elif c.get("block"):
