@@ -116,53 +116,43 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
   float key[Q];
 #pragma unroll
   for (int q = 0; q < Q; ++q) key[q] = (p[q] == p[q]) ? p[q] : -1.0f;
-  int sel[kMaxTopK];
-  float wsel[kMaxTopK];
+  // a rolled loop: lane j keeps round j's winner (its slot), so no per-slot arrays
   uint32_t taken = 0;  // bit q: this lane's element q is selected
+  int my_e = -1;       // lane j holds slot j
+  float my_raw = 0.f;
+#pragma unroll 1
+  for (int s = 0; s < k; ++s) {
+    float bv = -2.0f;
+    int bi = 0x7fffffff;
 #pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s) {
-    sel[s] = 0;
-    wsel[s] = 0.f;
-    if (s < k) {
-      float bv = -2.0f;
-      int bi = 0x7fffffff;
-#pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        const int e = j + kSelLanes * q;
-        if (e < E && !((taken >> q) & 1u) && (key[q] > bv || (key[q] == bv && e < bi))) {
-          bv = key[q];
-          bi = e;
-        }
+    for (int q = 0; q < Q; ++q) {
+      const int e = j + kSelLanes * q;
+      if (e < E && !((taken >> q) & 1u) && (key[q] > bv || (key[q] == bv && e < bi))) {
+        bv = key[q];
+        bi = e;
       }
-#pragma unroll
-      for (int o = 1; o < kSelLanes; o <<= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      // k <= E: at least one candidate remains, so bi is a valid expert
-      sel[s] = bi;
-      wsel[s] = bv;
-      if ((bi & (kSelLanes - 1)) == j) taken |= 1u << ((bi / kSelLanes) & 31);
     }
+#pragma unroll
+    for (int o = 1; o < kSelLanes; o <<= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    // k <= E: at least one candidate remains, so bi is a valid expert
+    if (s == j) {
+      my_e = bi;
+      my_raw = bv;
+    }
+    if ((bi & (kSelLanes - 1)) == j) taken |= 1u << ((bi / kSelLanes) & 31);
   }
-  // renormalise; the sum runs from the least to the most probable slot
+  // renormalise; the sum runs from the least to the most probable slot (lane k-1 down to 0)
   float ssum = 0.f;
-#pragma unroll
-  for (int s = kMaxTopK - 1; s >= 0; --s)
-    if (s < k) ssum = __fadd_rn(ssum, wsel[s]);
+  for (int s = k - 1; s >= 0; --s) ssum = __fadd_rn(ssum, __shfl(my_raw, (lane & ~(kSelLanes - 1)) + s));
   ssum = __fadd_rn(ssum, 1e-12f);
-  int my_e = -1;  // lane j holds slot j
-  float my_w = 0.f;
-#pragma unroll
-  for (int s = 0; s < kMaxTopK; ++s)
-    if (s == j && s < k) {
-      my_e = sel[s];
-      my_w = __fdiv_rn(wsel[s], ssum);
-    }
+  const float my_w = (j < k) ? __fdiv_rn(my_raw, ssum) : 0.f;
   out_e = active ? my_e : -1;
   out_w = my_w;
 }
