@@ -8,6 +8,22 @@
 
 namespace ygg {
 
+// Exchange within the 8-lane token groups by DPP (a register move, no LDS round
+// trip): step 0 pairs lanes i and i^1, step 1 lanes i and i^2 (quad permutes),
+// step 2 lanes i and 7-i of each half row (row_half_mirror), which joins the two
+// quads of a group as i^4 would.  After the three steps of a reduction every
+// lane holds the same result; for sums that is the tree ((r0+r1)+(r2+r3)) +
+// ((r4+r5)+(r6+r7)) exactly, as each addition only sees its operands swapped.
+template <int STEP>
+__device__ inline int grp_xchg(int v) {
+  constexpr int ctrl = STEP == 0 ? 0xB1 : STEP == 1 ? 0x4E : 0x141;
+  return __builtin_amdgcn_update_dpp(0, v, ctrl, 0xF, 0xF, false);
+}
+template <int STEP>
+__device__ inline float grp_xchg(float v) {
+  return __builtin_bit_cast(float, grp_xchg<STEP>(__builtin_bit_cast(int, v)));
+}
+
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
 constexpr int kSelLanes = 8;                          // lanes per token
@@ -15,7 +31,7 @@ constexpr int kSelLanes = 8;                          // lanes per token
 // The logits of one token straight from its activation row (the reference's
 // CliffordRouter energy signature, clifford_router.py:54-90): per-grade sums of
 // squares over the row (lane j takes multivectors j, j + 8, ...; the eight lanes
-// of the token are combined by a shuffle tree), normalised by their sum + 1e-12,
+// of the token are combined by a DPP tree), normalised by their sum + 1e-12,
 // then the (E, 4) map and bias.  Lane j returns the logits of experts j + 8 q.
 template <int Q>
 __device__ inline void energy_logits(const void* __restrict__ x, int x_dtype, int d, const float* __restrict__ rw,
@@ -44,9 +60,11 @@ __device__ inline void energy_logits(const void* __restrict__ x, int x_dtype, in
     }
   }
 #pragma unroll
-  for (int o = 1; o < kSelLanes; o <<= 1)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) gs[c] += __shfl_xor(gs[c], o);
+  for (int c = 0; c < 4; ++c) {
+    gs[c] += grp_xchg<0>(gs[c]);
+    gs[c] += grp_xchg<1>(gs[c]);
+    gs[c] += grp_xchg<2>(gs[c]);
+  }
   const float tot = gs[0] + gs[1] + gs[2] + gs[3] + 1e-12f;
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
@@ -73,8 +91,9 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
   float m = -INFINITY;
 #pragma unroll
   for (int q = 0; q < Q; ++q) m = fmaxf(m, p[q]);
-#pragma unroll
-  for (int o = 1; o < kSelLanes; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = fmaxf(m, grp_xchg<0>(m));
+  m = fmaxf(m, grp_xchg<1>(m));
+  m = fmaxf(m, grp_xchg<2>(m));
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     const int e = j + kSelLanes * q;
@@ -94,9 +113,9 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
 #pragma unroll
     for (int q = 1; q < Q; ++q)
       if (j + kSelLanes * q < E8) r = __fadd_rn(r, p[q]);
-    r = __fadd_rn(r, __shfl_xor(r, 1));
-    r = __fadd_rn(r, __shfl_xor(r, 2));
-    r = __fadd_rn(r, __shfl_xor(r, 4));
+    r = __fadd_rn(r, grp_xchg<0>(r));
+    r = __fadd_rn(r, grp_xchg<1>(r));
+    r = __fadd_rn(r, grp_xchg<2>(r));
     sum = r;
     // the remaining E % 8 values are element E / 8 of lanes 0 .. E % 8 - 1 (any Q >= ceil(E / 8))
     float prem = p[0];
@@ -132,15 +151,15 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
         bi = e;
       }
     }
-#pragma unroll
-    for (int o = 1; o < kSelLanes; o <<= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
+    auto take_better = [&](float ov, int oi) {
       if (ov > bv || (ov == bv && oi < bi)) {
         bv = ov;
         bi = oi;
       }
-    }
+    };
+    take_better(grp_xchg<0>(bv), grp_xchg<0>(bi));
+    take_better(grp_xchg<1>(bv), grp_xchg<1>(bi));
+    take_better(grp_xchg<2>(bv), grp_xchg<2>(bi));
     // k <= E: at least one candidate remains, so bi is a valid expert
     if (s == j) {
       my_e = bi;
