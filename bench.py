@@ -367,13 +367,12 @@ def run_train_config(torch, ops, name, c, steps, warmup):
     logits, rw, rb = L0.get("logits"), L0.get("router_w"), L0.get("router_b")
     ws_f = torch.empty(ops.moe_workspace_bytes(N, d, F, E, k, x.dtype, c["fmt"]), device="cuda", dtype=torch.uint8)
     ws_b = torch.empty(ops.lib().ygg_moe_backward_workspace_bytes(N, d, F, E, k), device="cuda", dtype=torch.uint8)
-    out = torch.empty_like(x)
 
-    def step():
-        ops.moe_forward(x, k, pu, pd, None, None, "gelu", logits=logits, router_weight=rw, router_bias=rb,
-                        workspace=ws_f, out=out)
+    def step():  # as the autograd node runs it: the forward keeps h before the activation
+        _, _, h_pre = ops.moe_forward_train(x, k, pu, pd, None, None, "gelu", logits=logits, router_weight=rw,
+                                            router_bias=rb, workspace=ws_f)
         ops.moe_backward(x, k, pu, au, pd, ad, dout, None, None, "gelu", logits=logits, router_weight=rw,
-                         router_bias=rb, workspace=ws_b, routing_grad=False)
+                         router_bias=rb, workspace=ws_b, routing_grad=False, h_pre=h_pre)
 
     ms = time_fn(torch, step, steps, warmup)
     # the weight gradients alone: up (rows of x through perm, F outputs) and down (h rows, d outputs)

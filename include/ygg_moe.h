@@ -224,13 +224,26 @@ size_t ygg_moe_backward_workspace_bytes(int N, int d, int F, int E, int k);
  * biases or NULL; residual: the forward added x to its output.  Writes dx
  * (N, d, 8), dw_up (E, F, d, 8), dw_down (E, d, F, 8) (blade order), db_up
  * (E, F, 8), db_down (E, d, 8) and dtopk_w (N, k, the gradient of the routing
- * weights, slots as ygg_route) when not NULL.  No gradient flows into the
- * router. */
+ * weights, slots as ygg_route) when not NULL.  h_pre_saved: the rows
+ * ygg_moe_forward_train kept, or NULL to recompute them.  No gradient flows into
+ * the router. */
 int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
                      const float* router_w, const float* router_b, const float* w_up, const float* w_up_adj,
                      const float* b_up, const float* w_down, const float* w_down_adj, const float* b_down,
-                     int residual, const float* dout, float* dx, float* dw_up, float* db_up, float* dw_down,
-                     float* db_down, float* dtopk_w, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
+                     int residual, const float* dout, const float* h_pre_saved, float* dx, float* dw_up,
+                     float* db_up, float* dw_down, float* db_down, float* dtopk_w, void* workspace,
+                     size_t workspace_bytes, ygg_stream_t stream);
+
+/* The forward of a training step: ygg_moe_forward for fp32 layers with fp32
+ * Pauli weights (format 4), which also writes h_pre (N k, F, 8) fp32 blade
+ * order, the up product's expert-grouped rows before the activation.  Passed
+ * to ygg_moe_backward as h_pre_saved (with the same x and routing inputs), it
+ * spares the backward the recompute of that product. */
+int ygg_moe_forward_train(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
+                          const float* router_w, const float* router_b, const float* w_up, const float* b_up,
+                          const float* w_down, const float* b_down, const float* residual, float* out,
+                          int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, float* h_pre,
+                          void* workspace, size_t workspace_bytes, ygg_stream_t stream);
 
 /* ---- weight import: grade-aware quantization -----------------------------------
  * quantize_multivector / dequantize_multivector

@@ -147,3 +147,26 @@ def test_moe_backward_routing_weight_gradient():
     # the forward it differentiates: out = sum_s w y, so <dout, out> = sum dw * w
     out, _ = ops.moe_forward(xt, k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"], "gelu", logits=lt)
     assert abs(float((out * ct).sum()) - float((dtw * r.topk_w).sum())) < 1e-3 * float((out * ct).abs().sum())
+
+
+def test_forward_train_keeps_what_the_backward_would_recompute():
+    """moe_forward_train's output is moe_forward's, and a backward given its h_pre equals the
+    recomputing backward bit for bit."""
+    ops = _ops()
+    g = np.random.default_rng(10)
+    N, d, F, E, k = 300, 16, 40, 6, 2
+    layer, _ = _layer_case(g, N, d, F, E, k, "gelu", "logits")
+    prep, adj = layer._get_prepared(), layer._get_adjoint()
+    xt = torch.from_numpy(g.standard_normal((N, d, 8)).astype(np.float32)).cuda()
+    ct = torch.from_numpy(g.standard_normal((N, d, 8)).astype(np.float32)).cuda()
+    lt = torch.from_numpy(g.standard_normal((N, E)).astype(np.float32)).cuda()
+    say("forward_train h_pre")
+    args = (xt, k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"], "gelu")
+    out, rt, h_pre = ops.moe_forward_train(*args, logits=lt)
+    ref, rt2 = ops.moe_forward(*args, logits=lt)
+    assert torch.equal(out, ref) and torch.equal(rt["topk_idx"], rt2["topk_idx"])
+    bargs = (xt, k, prep["w_up"], adj["w_up"], prep["w_down"], adj["w_down"], ct, prep["b_up"], prep["b_down"], "gelu")
+    g1 = ops.moe_backward(*bargs, logits=lt, h_pre=h_pre)
+    g2 = ops.moe_backward(*bargs, logits=lt)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)

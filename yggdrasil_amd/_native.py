@@ -50,7 +50,9 @@ SIGNATURES = {
     "ygg_activation_backward": (_c_int, [_vp, _vp, _c_size, _c_int, _vp, _vp]),
     "ygg_moe_backward_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ygg_moe_backward": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
-                                  _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+                                  _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "ygg_moe_forward_train": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "ygg_grade_quantize": (_c_int, [_vp, _c_int, _c_size, _vp, _c_int, _vp, _vp, _vp, _vp, _vp]),
     "ygg_clifford_layer_norm": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_double, _vp, _c_int, _vp]),
     "ygg_moe_block_ffn_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),

@@ -84,12 +84,13 @@ YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dt
   return b;
 }
 
-YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
+static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
                             const float* logits, const float* router_w, const float* router_b, const void* w_up,
                             const float* s_up, const float* b_up, const void* w_down, const float* s_down,
                             const float* b_down, int w_format, const void* residual, void* out, int32_t* topk_idx,
                             float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
-                            size_t workspace_bytes, hipStream_t stream) {
+                            size_t workspace_bytes, hipStream_t stream,
+                            float* h_pre_out) {
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
   YGG_CHECK_ARG(dtype == kF32 ? (w_format == kWF32 || w_format == kWPauliF32)
                              : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
@@ -136,8 +137,8 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
     // perm, down in K splits whose partial planes the combine adds in split order
     const int splits = pauli_f32_splits((int)P, E, F, d);
     if (ygg_pauli_rows_from_blade_f32(static_cast<const float*>(x), N, d, static_cast<float*>(xs), stream)) return -1;
-    if (ygg_pauli_grouped_linear_f32(static_cast<const float*>(xs), perm, (int)P, static_cast<const float*>(w_up), b_up,
-                                     offsets, E, d, F, act, static_cast<float*>(h), /*Pauli rows*/ 0, stream))
+    if (pauli_f32_linear_save_pre(static_cast<const float*>(xs), perm, (int)P, static_cast<const float*>(w_up), b_up,
+                                  offsets, E, d, F, act, static_cast<float*>(h), h_pre_out, stream))
       return -1;
     if (pauli_f32_linear_partial(static_cast<const float*>(h), (int)P, static_cast<const float*>(w_down), b_down,
                                  offsets, E, F, d, splits, static_cast<float*>(ys), stream))
@@ -185,6 +186,30 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
                                   /*blade=*/1, stream))
     return -1;
   return ygg_combine(ys, dtype, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
+}
+
+YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
+                            const float* logits, const float* router_w, const float* router_b, const void* w_up,
+                            const float* s_up, const float* b_up, const void* w_down, const float* s_down,
+                            const float* b_down, int w_format, const void* residual, void* out, int32_t* topk_idx,
+                            float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream) {
+  return moe_forward_impl(x, dtype, N, d, F, E, k, act, logits, router_w, router_b, w_up, s_up, b_up, w_down, s_down,
+                          b_down, w_format, residual, out, topk_idx, topk_w, counts, offsets, workspace,
+                          workspace_bytes, stream, nullptr);
+}
+
+// The forward of a training step (fp32 Pauli weights): ygg_moe_forward, and the
+// up product's rows before the activation, kept for ygg_moe_backward.
+YGG_API int ygg_moe_forward_train(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
+                                  const float* router_w, const float* router_b, const float* w_up, const float* b_up,
+                                  const float* w_down, const float* b_down, const float* residual, float* out,
+                                  int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, float* h_pre,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  YGG_CHECK_ARG(N == 0 || h_pre, "ygg_moe_forward_train: null h_pre");
+  return moe_forward_impl(x, kF32, N, d, F, E, k, act, logits, router_w, router_b, w_up, nullptr, b_up, w_down,
+                          nullptr, b_down, kWPauliF32, residual, out, topk_idx, topk_w, counts, offsets, workspace,
+                          workspace_bytes, stream, h_pre);
 }
 
 YGG_API size_t ygg_moe_block_ffn_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int w_format) {
@@ -245,9 +270,9 @@ YGG_API size_t ygg_moe_backward_workspace_bytes(int N, int d, int F, int E, int 
 YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, int act, const float* logits,
                              const float* router_w, const float* router_b, const float* w_up, const float* w_up_adj,
                              const float* b_up, const float* w_down, const float* w_down_adj, const float* b_down,
-                             int residual, const float* dout, float* dx, float* dw_up, float* db_up, float* dw_down,
-                             float* db_down, float* dtopk_w, void* workspace, size_t workspace_bytes,
-                             hipStream_t stream) {
+                             int residual, const float* dout, const float* h_pre_saved, float* dx, float* dw_up,
+                             float* db_up, float* dw_down, float* db_down, float* dtopk_w, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream) {
   YGG_CHECK_ARG(N >= 0 && d >= 1 && F >= 1 && E >= 1 && k >= 1 && k <= E, "ygg_moe_backward: bad sizes");
   YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_moe_backward: activation %d", act);
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_backward_workspace_bytes(N, d, F, E, k),
@@ -291,11 +316,15 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
                               rws, rws_bytes, stream)) {
     return -1;
   }
-  // forward recompute: h_pre, h (blade), y (blade)
-  if (ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
-  if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
-    return -1;
-  if (activation_forward(h_pre, P * F, act, h, stream)) return -1;
+  // forward recompute: h_pre (unless the forward kept it), h (blade), y (blade)
+  const float* hp_in = h_pre_saved;
+  if (!hp_in) {
+    if (ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
+    if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
+      return -1;
+    hp_in = h_pre;
+  }
+  if (activation_forward(hp_in, P * F, act, h, stream)) return -1;
   if (ygg_pauli_rows_from_blade_f32(h, (int)P, F, fp, stream)) return -1;
   if (dtopk_w &&
       ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, y, 1, stream))
@@ -307,7 +336,7 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
     return -1;
   if (grouped_weight_grad(dy, h, nullptr, offsets, E, F, d, dw_down, db_down, stream)) return -1;
   // activation backward (in place), up backward -> dx rows, dW_up, db_up
-  if (activation_backward(h_pre, dh, P * F, act, dh, stream)) return -1;
+  if (activation_backward(hp_in, dh, P * F, act, dh, stream)) return -1;
   if (ygg_pauli_rows_from_blade_f32(dh, (int)P, F, fp, stream)) return -1;
   if (ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_up_adj, nullptr, offsets, E, F, d, kActNone, y, 1, stream))
     return -1;

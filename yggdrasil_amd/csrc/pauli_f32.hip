@@ -65,7 +65,7 @@ template <int ACT, int OUT>
 __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
     const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
-    float* __restrict__ Y) {
+    float* __restrict__ Y, float* __restrict__ Ypre) {
   __shared__ float4 part[kF32Waves][2 * kF32Tok][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
   int e, row0, row_end;
   if (!f32_find_tile(offsets, E, blockIdx.x, e, row0, row_end)) return;
@@ -137,6 +137,11 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
       for (int c = 0; c < 8; ++c) y[c] += bias[((size_t)e * d_out + j) * 8 + blade_to_mask(c)];
     }
     if constexpr (OUT == kF32OutPauliRows) {
+      if (Ypre != nullptr) {  // the pre-activation rows, blade order (kept for the backward)
+        float4* q = reinterpret_cast<float4*>(Ypre + ((size_t)row * d_out + j) * 8);
+        q[0] = make_float4(y[0], y[1], y[2], y[3]);
+        q[1] = make_float4(y[4], y[5], y[6], y[7]);
+      }
       activate_blade<ACT>(y);
       float c0[4], c1[4];
       blade_to_pauli(y, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
@@ -210,8 +215,9 @@ using namespace ygg;
 namespace {
 template <int OUT>
 int launch_f32_act(int act, dim3 grid, hipStream_t st, const float* X, const int32_t* gather, const float* W,
-                   const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y) {
-#define YGG_F(A) pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y)
+                   const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
+                   float* Ypre = nullptr) {
+#define YGG_F(A) pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y, Ypre)
   switch (act) {
     case kActNone: YGG_F(kActNone); break;
     case kActGelu: YGG_F(kActGelu); break;
@@ -247,6 +253,14 @@ int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, con
   if (P_max == 0) return 0;
   return launch_f32_act<kF32OutPartial>(kActNone, f32_grid(P_max, E, d_out, splits), stream, x, nullptr, w, bias,
                                         offsets, E, d_in, d_out, P_max, y_planes);
+}
+
+int ygg::pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, const float* w,
+                                   const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act,
+                                   float* y_pauli, float* y_pre, hipStream_t stream) {
+  if (P_max == 0) return 0;
+  return launch_f32_act<kF32OutPauliRows>(act, f32_grid(P_max, E, d_out, 1), stream, x, gather, w, bias, offsets, E,
+                                          d_in, d_out, P_max, y_pauli, y_pre);
 }
 
 YGG_API int ygg_pauli_rows_from_blade_f32(const float* x, int rows, int d, float* out, hipStream_t stream) {

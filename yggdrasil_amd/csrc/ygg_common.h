@@ -115,6 +115,11 @@ int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out,
 // bias in split 0, no activation.
 int pauli_f32_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
 int pauli_f32_splits(int P_max, int E, int d_in, int d_out);
+// The fp32 Pauli product writing Pauli rows (activation applied) and, when
+// y_pre is not NULL, the blade-order rows before the activation.
+int pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, const float* w, const float* bias,
+                              const int32_t* offsets, int E, int d_in, int d_out, int act, float* y_pauli,
+                              float* y_pre, hipStream_t stream);
 int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias, const int32_t* offsets,
                              int E, int d_in, int d_out, int splits, float* y_planes, hipStream_t stream);
 

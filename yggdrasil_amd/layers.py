@@ -263,13 +263,20 @@ class _MoEFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, flat, res, w_up, b_up, w_down, b_down, layer, logits):
         ctx.layer, ctx.has_res = layer, res is not None
-        ctx.save_for_backward(flat, logits if logits is not None else flat.new_empty(0))
+        cfg, prep = layer.cfg, layer._get_prepared()
+        out, routing, h_pre = ops.moe_forward_train(
+            flat, cfg.top_k, prep["w_up"], prep["w_down"], prep["b_up"], prep["b_down"], cfg.activation,
+            logits=logits, router_weight=layer.router_weight.detach() if logits is None else None,
+            router_bias=layer.router_bias.detach() if logits is None else None, residual=res,
+            workspace=layer._workspace)
+        layer.last_routing = routing
+        ctx.save_for_backward(flat, logits if logits is not None else flat.new_empty(0), h_pre)
         ctx.has_logits = logits is not None
-        return layer._forward_flat(flat, logits, res)
+        return out
 
     @staticmethod
     def backward(ctx, dout):
-        flat, logits = ctx.saved_tensors
+        flat, logits, h_pre = ctx.saved_tensors
         layer = ctx.layer
         cfg = layer.cfg
         prep, adj = layer._get_prepared(), layer._get_adjoint()
@@ -278,7 +285,7 @@ class _MoEFunction(torch.autograd.Function):
             flat, cfg.top_k, prep["w_up"], adj["w_up"], prep["w_down"], adj["w_down"], dout.contiguous(),
             prep["b_up"], prep["b_down"], cfg.activation, logits=logits if use_logits else None,
             router_weight=None if use_logits else layer.router_weight.detach(),
-            router_bias=None if use_logits else layer.router_bias.detach(), routing_grad=False)
+            router_bias=None if use_logits else layer.router_bias.detach(), routing_grad=False, h_pre=h_pre)
         return dx, (dout if ctx.has_res else None), dWu, dbu, dWd, dbd, None, None
 
 

@@ -505,11 +505,13 @@ def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: Prepa
                  w_down_adj: PreparedWeights, dout: torch.Tensor, b_up: torch.Tensor | None = None,
                  b_down: torch.Tensor | None = None, act: str = "gelu", logits: torch.Tensor | None = None,
                  router_weight: torch.Tensor | None = None, router_bias: torch.Tensor | None = None,
-                 residual: bool = False, workspace: torch.Tensor | None = None, routing_grad: bool = True):
+                 residual: bool = False, workspace: torch.Tensor | None = None, routing_grad: bool = True,
+                 h_pre: torch.Tensor | None = None):
     """Backward of ``moe_forward`` (fp32, ``pauli_f32`` weights). Returns dx, dW_up, db_up, dW_down, db_down, dtopk_w.
 
     ``routing_grad=False`` skips the routing-weight gradient (dtopk_w is None), and with it
-    the recompute of the expert outputs it needs.
+    the recompute of the expert outputs it needs.  ``h_pre``: the rows ``moe_forward_train``
+    kept (then the up product is not recomputed).
     """
     dev = _dev(x, dout, logits)
     for pw in (w_up, w_up_adj, w_down, w_down_adj):
@@ -534,10 +536,40 @@ def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: Prepa
     rb = router_bias.float().contiguous() if router_bias is not None else None
     check(lib().ygg_moe_backward(ptr(x), Nt, d, F, E, k, ACT_CODE[act], ptr(logits), ptr(rw), ptr(rb),
                                  ptr(w_up.data), ptr(w_up_adj.data), ptr(b_up), ptr(w_down.data),
-                                 ptr(w_down_adj.data), ptr(b_down), int(residual), ptr(dout), ptr(dx), ptr(dWu),
+                                 ptr(w_down_adj.data), ptr(b_down), int(residual), ptr(dout), ptr(h_pre), ptr(dx),
+                                 ptr(dWu),
                                  ptr(dbu), ptr(dWd), ptr(dbd), ptr(dtw), ptr(workspace), ws_bytes,
                                  stream_handle(dev)), "moe_backward")
     return dx, dWu, dbu, dWd, dbd, dtw
+
+
+def moe_forward_train(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: PreparedWeights,
+                      b_up: torch.Tensor | None = None, b_down: torch.Tensor | None = None, act: str = "gelu",
+                      logits: torch.Tensor | None = None, router_weight: torch.Tensor | None = None,
+                      router_bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+                      workspace: torch.Tensor | None = None):
+    """``moe_forward`` for a training step (fp32, ``pauli_f32``): also returns the up product's
+    pre-activation rows ``h_pre`` (N k, F, 8) for ``moe_backward``."""
+    dev = _dev(x, logits, residual)
+    if w_up.fmt != "pauli_f32" or w_down.fmt != "pauli_f32" or x.dtype != torch.float32:
+        raise ValueError("moe_forward_train: fp32 layers with 'pauli_f32' weights")
+    Nt, d = x.shape[0], x.shape[1]
+    E, F = w_up.E, w_up.d_out
+    ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    out = torch.empty_like(x)
+    i32 = dict(device=dev, dtype=torch.int32)
+    topk_idx, counts, offsets = torch.empty((Nt, k), **i32), torch.empty((E,), **i32), torch.empty((E + 1,), **i32)
+    topk_w = torch.empty((Nt, k), device=dev, dtype=torch.float32)
+    h_pre = torch.empty((Nt * k, F, 8), device=dev, dtype=torch.float32)
+    rw = router_weight.float().contiguous() if router_weight is not None else None
+    rb = router_bias.float().contiguous() if router_bias is not None else None
+    check(lib().ygg_moe_forward_train(ptr(x), Nt, d, F, E, k, ACT_CODE[act], ptr(logits), ptr(rw), ptr(rb),
+                                      ptr(w_up.data), ptr(b_up), ptr(w_down.data), ptr(b_down), ptr(residual),
+                                      ptr(out), ptr(topk_idx), ptr(topk_w), ptr(counts), ptr(offsets), ptr(h_pre),
+                                      ptr(workspace), ws_bytes, stream_handle(dev)), "moe_forward_train")
+    return out, dict(topk_idx=topk_idx, topk_w=topk_w, counts=counts, offsets=offsets), h_pre
 
 
 def grade_quantize(w: torch.Tensor, grade_bits=(8, 6, 6, 4), symmetric: bool = True, codes: bool = True):
