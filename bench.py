@@ -207,7 +207,7 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         # as above in fp32 split rows; the layer's down product splits its contraction
         # into partial planes, the exported entry timed here writes blade rows directly
         xp = ops.pauli_rows_from_blade_f32(x)
-        h = torch.empty((N * k, 2, 2, F, 2), device="cuda", dtype=x.dtype)
+        h = torch.empty((N * k, F, 2, 2, 2), device="cuda", dtype=x.dtype)
 
         def up():
             ops.check(L.ygg_pauli_grouped_linear_f32(xp.data_ptr(), r.perm.data_ptr(), N * k,

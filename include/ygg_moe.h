@@ -162,10 +162,10 @@ int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather,
 int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out, ygg_stream_t stream);
 
 /* fp32 products with weights in format 4 (v_mfma_f32_32x32x2_f32):
- * x holds fp32 "Pauli split rows" (rows, 2, 2, d_in, 2) -- see
+ * x holds fp32 "Pauli rows" (rows, d_in, 2, 2, 2) -- see
  * ygg_pauli_rows_from_blade_f32 -- and row r of the product reads
- * x[gather[r]] (gather NULL: x[r]).  y_layout 0: Pauli split rows
- * (P, 2, 2, d_out, 2) fp32; 1: blade-order fp32 rows (P, d_out, 8).
+ * x[gather[r]] (gather NULL: x[r]).  y_layout 0: Pauli rows
+ * (P, d_out, 2, 2, 2) fp32; 1: blade-order fp32 rows (P, d_out, 8).
  * bias prepared (mask order) or NULL; act as above.  Replaces
  * CliffordLinear.forward (clifford_linear.py:101-123) of every expert, with
  * the activation (activations.py:15-128) fused, for fp32 layers. */
@@ -173,7 +173,9 @@ int ygg_pauli_grouped_linear_f32(const float* x, const int32_t* gather, int P_ma
                                  const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out,
                                  int act, float* y, int y_layout, ygg_stream_t stream);
 
-/* Blade-order fp32 rows (rows, d, 8) -> fp32 Pauli split rows (rows, 2, 2, d, 2). */
+/* Blade-order fp32 rows (rows, d, 8) -> fp32 Pauli rows (rows, d, 2, 2, 2): element
+ * [m][i][b][k][c] is the real (k = 0) or imaginary (k = 1) part of entry (c, b) of
+ * multivector x[m][i] as a 2x2 complex matrix. */
 int ygg_pauli_rows_from_blade_f32(const float* x, int rows, int d, float* out, ygg_stream_t stream);
 
 /* ---- the whole layer ---------------------------------------------------------

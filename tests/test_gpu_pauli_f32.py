@@ -33,15 +33,15 @@ def _offsets(g, E, P):
 
 
 def pauli_split_rows(x):
-    """(rows, d, 8) blade order -> (rows, 2, 2, d, 2): [b][re / im][i][c] of the 2x2 matrix X[c][b]."""
+    """(rows, d, 8) blade order -> (rows, d, 2, 2, 2): [b][re / im][c] of the 2x2 matrix X[c][b]."""
     s, v1, v2, v3, b12, b13, b23, t = [x[..., i] for i in range(8)]
     m00 = (s + v3, t + b12)
     m10 = (v1 + b13, b23 + v2)
     m01 = (v1 - b13, b23 - v2)
     m11 = (s - v3, t - b12)
-    col0 = [np.stack([m00[k], m10[k]], -1) for k in range(2)]
-    col1 = [np.stack([m01[k], m11[k]], -1) for k in range(2)]
-    return np.stack([np.stack(col0, 1), np.stack(col1, 1)], 1)
+    col0 = np.stack([np.stack([m00[k], m10[k]], -1) for k in range(2)], -2)  # [k][c]
+    col1 = np.stack([np.stack([m01[k], m11[k]], -1) for k in range(2)], -2)
+    return np.stack([col0, col1], -3)
 
 
 def test_pauli_rows_from_blade_f32_bit_exact():
@@ -50,7 +50,7 @@ def test_pauli_rows_from_blade_f32_bit_exact():
     x = g.standard_normal((45, 7, 8), dtype=np.float32)
     say("pauli f32 rows from blade")
     got = ops.pauli_rows_from_blade_f32(torch.from_numpy(x).cuda()).cpu().numpy()
-    assert got.shape == (45, 2, 2, 7, 2)
+    assert got.shape == (45, 7, 2, 2, 2)
     assert np.array_equal(got, pauli_split_rows(x))
 
 
@@ -108,7 +108,7 @@ def test_pauli_f32_rejects_bad_arguments():
     assert L.ygg_pauli_grouped_linear_f32(None, None, 4, None, None, None, 2, 4, 4, 0, None, 2, None) == -1
     assert L.ygg_pauli_rows_from_blade_f32(None, 3, 0, None, None) == -1
     with pytest.raises(ValueError):
-        ops.pauli_grouped_linear_f32(torch.zeros(4, 2, 2, 3, 2, device="cuda"),
+        ops.pauli_grouped_linear_f32(torch.zeros(4, 3, 2, 2, 2, device="cuda"),
                                      ops.prepare_weights(torch.zeros(1, 4, 3, 8, device="cuda"), "f32"),
                                      torch.tensor([0, 4], device="cuda", dtype=torch.int32))
 

@@ -223,7 +223,7 @@ def test_route_energy_fused_against_oracle(N, d, E, k, dtype):
 
 
 @pytest.mark.parametrize("N,d,E,dtype", [(256, 64, 8, "f32"), (33, 7, 5, "f32"), (100, 16, 64, "bf16"),
-                                         (3000, 32, 16, "f32")])
+                                         (3000, 32, 16, "f32"), (5, 130, 70, "f32"), (61, 128, 32, "bf16")])
 def test_router_head_logits_bit_exact(N, d, E, dtype):
     """The CliffordLinear(d -> E) head's scalar part in the reference's fp32 order, bit for bit."""
     ops = _ops()

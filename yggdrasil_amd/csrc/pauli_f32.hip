@@ -9,15 +9,17 @@
 //
 // Layouts
 // -------
-// * Pauli split rows ("PS", fp32): GEMM row (m, b) -- column b of every
-//   multivector of token row m -- is stored as two runs, real parts then
-//   imaginary parts, each d x (c0, c1):
-//   X[(((m * 2 + b) * 2 + k) * d + i) * 2 + c],  k = 0 real, 1 imaginary.
-// * Prepared weights (format 4): per (e, j, k, i) eight floats [c][a][q]:
-//   k = 0: (u, v), k = 1: (-v, u), where u + iv = W_ji[a, c] / 2.  With
-//   v_mfma_f32_32x32x2_f32 (K = 2: lane l holds k = l / 32) the real part
-//   takes q = 0 and the imaginary part q = 1, so both B operands come from
-//   memory as they are.
+// * Pauli rows (fp32): the four complex entries of every multivector, grouped
+//   by matrix column b and real / imaginary part k:
+//   X[((m * d + i) * 2 + b) * 2 + k) * 2 + c] = (re if k = 0, im if k = 1) of X_i[c][b]
+//   for token row m; 8 floats per multivector, as in blade order.  The wave's 64
+//   MFMA rows (16 tokens x (b, k)) read 32 contiguous bytes per token and input.
+// * Prepared weights (format 4): per (e, i, k, j) eight floats [c][a][q]:
+//   k = 0: (u, v), k = 1: (-v, u), where u + iv = W_ji[a, c] / 2, at
+//   ((e * d_in + i) * 2 + k) * d_out + j.  With v_mfma_f32_32x32x2_f32 (K = 2:
+//   lane l holds k = l / 32) the real part takes q = 0 and the imaginary part
+//   q = 1, so both B operands come from memory as they are, and the 32 columns
+//   of a wave are 1 KiB runs per (i, k).
 //
 // Work decomposition
 // ------------------
@@ -39,6 +41,7 @@ typedef float f32x16v_t __attribute__((ext_vector_type(16)));
 constexpr int kF32Waves = 4;
 constexpr int kF32Tok = 16;  // tokens per tile (32 GEMM rows)
 constexpr int kF32Cols = 32;  // output multivectors per tile
+constexpr int kF32U = 4;      // input multivectors per register-buffered block of the K loop
 
 enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2 };
 
@@ -71,17 +74,19 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
   if (!f32_find_tile(offsets, E, blockIdx.x, e, row0, row_end)) return;
   const int col0 = blockIdx.y * kF32Cols;
   const int split = blockIdx.z, splits = gridDim.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the K loop runs on scalars
   const int l32 = lane & 31, k = lane >> 5;
 
   // A operand: GEMM row (t, b) = l32, real (k = 0) or imaginary (k = 1) run
   int m = row0 + (l32 >> 1);
   m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
   const int src = gather ? gather[m] : m;
-  const float* arow = X + ((size_t)(src * 2 + (l32 & 1)) * 2 + k) * d_in * 2;
+  const float* arow = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
   // B operand: output column j (clamped: columns past d_out are not stored)
   const int jc = min(col0 + l32, d_out - 1);
-  const float* wrow = Wp + ((size_t)(e * d_out + jc) * 2 + k) * d_in * 8;
+  const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
+  const size_t w_step = (size_t)2 * d_out * 8;  // floats from input i to i + 1
   // contraction range of this (split, wave)
   const int per_split = (d_in + splits - 1) / splits;
   const int is0 = split * per_split, is1 = min(d_in, is0 + per_split);
@@ -95,11 +100,15 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[a][q][v] = 0.f;
-#pragma unroll 4
-  for (int i = i0; i < i1; ++i) {
-    const float2 xa = *reinterpret_cast<const float2*>(arow + (size_t)i * 2);
-    const float4 w0 = *reinterpret_cast<const float4*>(wrow + (size_t)i * 8);      // c = 0
-    const float4 w1 = *reinterpret_cast<const float4*>(wrow + (size_t)i * 8 + 4);  // c = 1
+  // Operands of input multivector i: x (re, im) of the lane's GEMM row and the eight
+  // weight floats of its column.  Blocks of kF32U multivectors are double buffered in
+  // registers, so one block's loads are in flight while the previous block's MFMAs run.
+  auto load_op = [&](int i, float2& xa, float4& w0, float4& w1) {
+    xa = *reinterpret_cast<const float2*>(arow + (size_t)i * 8);
+    w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
+    w1 = *reinterpret_cast<const float4*>(wrow + i * w_step + 4);  // c = 1
+  };
+  auto mma = [&](const float2& xa, const float4& w0, const float4& w1) {
     acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.x, acc[0][0], 0, 0, 0);
     acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.y, acc[0][1], 0, 0, 0);
     acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.z, acc[1][0], 0, 0, 0);
@@ -108,6 +117,35 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
     acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.y, acc[0][1], 0, 0, 0);
     acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.z, acc[1][0], 0, 0, 0);
     acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.w, acc[1][1], 0, 0, 0);
+  };
+  const int nblk = max(i1 - i0, 0) / kF32U;
+  float2 xa0[kF32U], xa1[kF32U];
+  float4 wa0[kF32U], wb0[kF32U], wa1[kF32U], wb1[kF32U];
+  if (nblk > 0) {
+#pragma unroll
+    for (int u = 0; u < kF32U; ++u) load_op(i0 + u, xa0[u], wa0[u], wb0[u]);
+  }
+  for (int b = 0; b < nblk; b += 2) {  // buffer 0 holds block b, buffer 1 block b + 1
+    if (b + 1 < nblk) {
+#pragma unroll
+      for (int u = 0; u < kF32U; ++u) load_op(i0 + (b + 1) * kF32U + u, xa1[u], wa1[u], wb1[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kF32U; ++u) mma(xa0[u], wa0[u], wb0[u]);
+    if (b + 1 < nblk) {
+      if (b + 2 < nblk) {
+#pragma unroll
+        for (int u = 0; u < kF32U; ++u) load_op(i0 + (b + 2) * kF32U + u, xa0[u], wa0[u], wb0[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kF32U; ++u) mma(xa1[u], wa1[u], wb1[u]);
+    }
+  }
+  for (int i = i0 + nblk * kF32U; i < i1; ++i) {
+    float2 xa;
+    float4 w0, w1;
+    load_op(i, xa, w0, w1);
+    mma(xa, w0, w1);
   }
   // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4
 #pragma unroll
@@ -145,11 +183,9 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
       activate_blade<ACT>(y);
       float c0[4], c1[4];
       blade_to_pauli(y, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
-      const size_t base = (size_t)row * 4;  // (row, b, k) runs
-      *reinterpret_cast<float2*>(Y + ((base + 0) * d_out + j) * 2) = make_float2(c0[0], c0[2]);
-      *reinterpret_cast<float2*>(Y + ((base + 1) * d_out + j) * 2) = make_float2(c0[1], c0[3]);
-      *reinterpret_cast<float2*>(Y + ((base + 2) * d_out + j) * 2) = make_float2(c1[0], c1[2]);
-      *reinterpret_cast<float2*>(Y + ((base + 3) * d_out + j) * 2) = make_float2(c1[1], c1[3]);
+      float4* q = reinterpret_cast<float4*>(Y + ((size_t)row * d_out + j) * 8);  // [b][k][c]
+      q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+      q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
     } else {
       size_t mv = (size_t)row * d_out + j;
       if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
@@ -176,8 +212,9 @@ __global__ __launch_bounds__(256) void pauli_f32_prep_kernel(const float* __rest
   // W[a][c]: (a, c) = (0, 0) M00, (0, 1) M01, (1, 0) M10, (1, 1) M11 as (u, v)
   const float u[2][2] = {{c0[0], c1[0]}, {c0[2], c1[2]}};  // [a][c]
   const float v[2][2] = {{c0[1], c1[1]}, {c0[3], c1[3]}};
-  float* r0 = out + ((ej * 2 + 0) * d_in + i) * 8;  // k = 0: (u, v)
-  float* r1 = out + ((ej * 2 + 1) * d_in + i) * 8;  // k = 1: (-v, u)
+  const size_t e = ej / d_out, j = ej % d_out;
+  float* r0 = out + (((e * d_in + i) * 2 + 0) * d_out + j) * 8;  // k = 0: (u, v)
+  float* r1 = out + (((e * d_in + i) * 2 + 1) * d_out + j) * 8;  // k = 1: (-v, u)
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -189,23 +226,19 @@ __global__ __launch_bounds__(256) void pauli_f32_prep_kernel(const float* __rest
     }
 }
 
-// blade fp32 rows (rows, d, 8) -> Pauli split rows; one thread per multivector
+// blade fp32 rows (rows, d, 8) -> Pauli rows; one thread per multivector
 __global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const float* __restrict__ x, int rows, int d,
                                                                       float* __restrict__ out) {
   const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= (size_t)rows * d) return;
-  const size_t m = n / d;
-  const int i = (int)(n % d);
   const float4 p0 = reinterpret_cast<const float4*>(x + n * 8)[0];
   const float4 p1 = reinterpret_cast<const float4*>(x + n * 8)[1];
   const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
   float c0[4], c1[4];
   blade_to_pauli(v, c0, c1);
-  const size_t base = m * 4;
-  *reinterpret_cast<float2*>(out + ((base + 0) * d + i) * 2) = make_float2(c0[0], c0[2]);
-  *reinterpret_cast<float2*>(out + ((base + 1) * d + i) * 2) = make_float2(c0[1], c0[3]);
-  *reinterpret_cast<float2*>(out + ((base + 2) * d + i) * 2) = make_float2(c1[0], c1[2]);
-  *reinterpret_cast<float2*>(out + ((base + 3) * d + i) * 2) = make_float2(c1[1], c1[3]);
+  float4* q = reinterpret_cast<float4*>(out + n * 8);  // [b][k][c]
+  q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+  q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
 }
 
 }  // namespace ygg

@@ -367,42 +367,66 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
 // rune/ops/batched.py:72-82): for each i in turn, the eight diagonal terms
 // (s_c W_c) x_c of the product's scalar part are added to zero in component order
 // (s = -1 on grades 2 and 3), and that product is added to the running sum.  No
-// multiply-add contraction, so the logits are the reference's bit for bit.  One
-// thread per (token, expert); the expert's weights are read by 64 neighbouring
-// threads at once (L1/L2 broadcast), x rows by the E threads of a token.
+// multiply-add contraction, so the logits are the reference's bit for bit.
+//
+// One wave per token.  The per-i products are independent: lane i computes them
+// for 64 input multivectors at a time (x and W rows read as contiguous 2 KiB runs
+// across the wave) into LDS, then lane e adds its expert's 64 products in i order
+// to its running sum.  Experts beyond 64 take further passes.
+constexpr int kHeadWaves = 4;
+
 template <typename XT>
-__global__ __launch_bounds__(256) void router_head_logits_kernel(const XT* __restrict__ x, int N, int d,
-                                                                 const float* __restrict__ head_w, int E,
-                                                                 float* __restrict__ logits) {
+__global__ __launch_bounds__(64 * kHeadWaves) void router_head_logits_kernel(const XT* __restrict__ x, int N, int d,
+                                                                            const float* __restrict__ head_w, int E,
+                                                                            float* __restrict__ logits) {
 #pragma clang fp contract(off)
-  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (n >= (size_t)N * E) return;
-  const int t = (int)(n / E), e = (int)(n % E);
-  const XT* xr = x + (size_t)t * d * 8;
-  const float* wr = head_w + (size_t)e * d * 8;
-  float acc = 0.f;
-  for (int i = 0; i < d; ++i) {
-    float xv[8];
-    if constexpr (sizeof(XT) == 4) {
-      const float4 a = reinterpret_cast<const float4*>(xr + i * 8)[0], b = reinterpret_cast<const float4*>(xr + i * 8)[1];
-      xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-    } else {
-      const uint4 q = *reinterpret_cast<const uint4*>(xr + i * 8);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  // kHeadWaves x min(E, 64) x 64 floats; product (e, i) sits at column i ^ e of row e, so the
+  // lanes adding along a row hit distinct banks
+  extern __shared__ float head_buf[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int EB = E < 64 ? E : 64;
+  float* pb = head_buf + (size_t)wave * EB * 64;
+  const int t = blockIdx.x * kHeadWaves + wave;
+  const bool active = t < N;  // every wave takes part in the barriers below
+  const XT* xr = x + (size_t)(active ? t : 0) * d * 8;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int ne = (E - e0) < 64 ? (E - e0) : 64;
+    float acc = 0.f;
+    for (int i0 = 0; i0 < d; i0 += 64) {
+      const int i = i0 + lane, ni = (d - i0) < 64 ? (d - i0) : 64;
+      if (active && i < d) {
+        float xv[8];
+        if constexpr (sizeof(XT) == 4) {
+          const float4 a = reinterpret_cast<const float4*>(xr + (size_t)i * 8)[0];
+          const float4 b = reinterpret_cast<const float4*>(xr + (size_t)i * 8)[1];
+          xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+        } else {
+          const uint4 q = *reinterpret_cast<const uint4*>(xr + (size_t)i * 8);
+          const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        xv[2 * c] = __builtin_bit_cast(float, w[c] << 16);
-        xv[2 * c + 1] = __builtin_bit_cast(float, w[c] & 0xffff0000u);
+          for (int c = 0; c < 4; ++c) {
+            xv[2 * c] = __builtin_bit_cast(float, w[c] << 16);
+            xv[2 * c + 1] = __builtin_bit_cast(float, w[c] & 0xffff0000u);
+          }
+        }
+#pragma unroll 4
+        for (int el = 0; el < ne; ++el) {
+          const float4* wr = reinterpret_cast<const float4*>(head_w + ((size_t)(e0 + el) * d + i) * 8);
+          const float4 a = wr[0], b = wr[1];
+          const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+          float p = 0.f;
+#pragma unroll
+          for (int c = 0; c < 8; ++c) p = p + (c < 4 ? wv[c] : -wv[c]) * xv[c];
+          pb[el * 64 + (lane ^ el)] = p;
+        }
       }
+      __syncthreads();
+      if (active && lane < ne)
+        for (int il = 0; il < ni; ++il) acc = acc + pb[lane * 64 + (il ^ lane)];
+      __syncthreads();
     }
-    const float4 a = reinterpret_cast<const float4*>(wr + i * 8)[0], b = reinterpret_cast<const float4*>(wr + i * 8)[1];
-    const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float p = 0.f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) p = p + (c < 4 ? wv[c] : -wv[c]) * xv[c];
-    acc = acc + p;
+    if (active && lane < ne) logits[(size_t)t * E + e0 + lane] = acc;
   }
-  logits[n] = acc;
 }
 
 YGG_API int ygg_router_head_logits(const void* x, int x_dtype, int N, int d, const float* head_w, int E,
@@ -411,12 +435,14 @@ YGG_API int ygg_router_head_logits(const void* x, int x_dtype, int N, int d, con
   YGG_CHECK_ARG(N >= 0 && d >= 1 && E >= 1, "ygg_router_head_logits: bad sizes N=%d d=%d E=%d", N, d, E);
   YGG_CHECK_ARG(N == 0 || (x && head_w && logits), "ygg_router_head_logits: null pointer");
   if (N == 0) return 0;
-  const unsigned blocks = (unsigned)(((size_t)N * E + 255) / 256);
+  const unsigned blocks = (unsigned)((N + kHeadWaves - 1) / kHeadWaves);
+  const size_t lds = (size_t)kHeadWaves * (E < 64 ? E : 64) * 64 * sizeof(float);
   if (x_dtype == kF32)
-    router_head_logits_kernel<float><<<blocks, 256, 0, stream>>>(static_cast<const float*>(x), N, d, head_w, E, logits);
+    router_head_logits_kernel<float><<<blocks, 64 * kHeadWaves, lds, stream>>>(static_cast<const float*>(x), N, d,
+                                                                               head_w, E, logits);
   else
-    router_head_logits_kernel<uint16_t><<<blocks, 256, 0, stream>>>(static_cast<const uint16_t*>(x), N, d, head_w, E,
-                                                                    logits);
+    router_head_logits_kernel<uint16_t><<<blocks, 64 * kHeadWaves, lds, stream>>>(static_cast<const uint16_t*>(x), N,
+                                                                                  d, head_w, E, logits);
   return check_launch("router_head_logits");
 }
 

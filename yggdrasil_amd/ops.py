@@ -321,18 +321,18 @@ def pauli_grouped_linear_f32(x: torch.Tensor, pw: PreparedWeights, offsets: torc
                              y_layout: str = "blade") -> torch.Tensor:
     """fp32 per-expert CliffordLinear with Pauli weights (``fmt='pauli_f32'``).
 
-    x: (rows, 2, 2, d_in, 2) fp32 Pauli split rows (see :func:`pauli_rows_from_blade_f32`);
+    x: (rows, d_in, 2, 2, 2) fp32 Pauli rows (see :func:`pauli_rows_from_blade_f32`);
     output row r reads x[gather[r]] (or x[r]).  y_layout 'blade' -> (P, d_out, 8),
-    'pauli' -> (P, 2, 2, d_out, 2).
+    'pauli' -> (P, d_out, 2, 2, 2).
     """
     if pw.fmt != "pauli_f32":
         raise ValueError("pauli_grouped_linear_f32 needs weights prepared with fmt='pauli_f32'")
     dev = _dev(x, offsets, bias_prepared, gather)
-    if x.dtype != torch.float32 or x.dim() != 5 or x.shape[3] != pw.d_in:
-        raise ValueError(f"x must be fp32 Pauli split rows (rows, 2, 2, {pw.d_in}, 2)")
+    if x.dtype != torch.float32 or x.dim() != 5 or tuple(x.shape[1:]) != (pw.d_in, 2, 2, 2):
+        raise ValueError(f"x must be fp32 Pauli rows (rows, {pw.d_in}, 2, 2, 2)")
     if rows is None:
         rows = gather.shape[0] if gather is not None else x.shape[0]
-    shape = (rows, 2, 2, pw.d_out, 2) if y_layout == "pauli" else (rows, pw.d_out, 8)
+    shape = (rows, pw.d_out, 2, 2, 2) if y_layout == "pauli" else (rows, pw.d_out, 8)
     y = torch.empty(shape, device=dev, dtype=torch.float32)
     check(lib().ygg_pauli_grouped_linear_f32(ptr(x), ptr(gather), rows, ptr(pw.data), ptr(bias_prepared),
                                              ptr(offsets), pw.E, pw.d_in, pw.d_out, ACT_CODE[act], ptr(y),
@@ -341,12 +341,16 @@ def pauli_grouped_linear_f32(x: torch.Tensor, pw: PreparedWeights, offsets: torc
 
 
 def pauli_rows_from_blade_f32(x: torch.Tensor) -> torch.Tensor:
-    """(rows, d, 8) fp32 blade order -> (rows, 2, 2, d, 2) fp32 Pauli split rows."""
+    """(rows, d, 8) fp32 blade order -> (rows, d, 2, 2, 2) fp32 Pauli rows.
+
+    Element [m, i, b, k, c] is the real (k = 0) or imaginary (k = 1) part of entry
+    (c, b) of multivector x[m, i] as a 2x2 complex matrix.
+    """
     dev = _dev(x)
     if x.dtype != torch.float32:
         raise ValueError("fp32 rows only")
     rows, d = x.shape[0], x.shape[1]
-    out = torch.empty((rows, 2, 2, d, 2), device=dev, dtype=torch.float32)
+    out = torch.empty((rows, d, 2, 2, 2), device=dev, dtype=torch.float32)
     check(lib().ygg_pauli_rows_from_blade_f32(ptr(x), rows, d, ptr(out), stream_handle(dev)),
           "pauli_rows_from_blade_f32")
     return out
