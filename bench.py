@@ -37,6 +37,7 @@ PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
 # measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
 PAULI_C3_TRAFFIC_BYTES = 410.9e6
+WGRAD_MFMA_ROWS_PER_EXPERT = 256  # as ygg_moe_backward: mean rows per expert from which it uses the MFMA kernel
 SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5}
 
 CONFIGS = {
@@ -381,11 +382,23 @@ def run_train_config(torch, ops, name, c, steps, warmup):
     dh = torch.randn(P, F, 8, generator=g, device="cuda")
     dy = torch.randn(P, d, 8, generator=g, device="cuda")
     h = torch.randn(P, F, 8, generator=g, device="cuda")
-    ms_wg_up = time_fn(torch, lambda: ops.grouped_weight_grad(dh, x, r.offsets, E, gather=r.perm), steps, warmup)
-    ms_wg_down = time_fn(torch, lambda: ops.grouped_weight_grad(dy, h, r.offsets, E), steps, warmup)
+    if P >= WGRAD_MFMA_ROWS_PER_EXPERT * E:  # the backward's choice: MFMA on Pauli rows
+        wg_kind = "mfma"
+        dhp, xp = ops.pauli_rows_from_blade_f32(dh), ops.pauli_rows_from_blade_f32(x.reshape(N, d, 8))
+        dyp, hp = ops.pauli_rows_from_blade_f32(dy), ops.pauli_rows_from_blade_f32(h)
+        ws_w = torch.empty(ops.lib().ygg_grouped_weight_grad_pauli_f32_workspace_bytes(P, E, d, F), device="cuda",
+                           dtype=torch.uint8)
+        ms_wg_up = time_fn(torch, lambda: ops.grouped_weight_grad_pauli(dhp, xp, r.offsets, E, gather=r.perm,
+                                                                        workspace=ws_w), steps, warmup)
+        ms_wg_down = time_fn(torch, lambda: ops.grouped_weight_grad_pauli(dyp, hp, r.offsets, E, workspace=ws_w),
+                             steps, warmup)
+    else:  # vector ALUs on blade rows
+        wg_kind = "valu"
+        ms_wg_up = time_fn(torch, lambda: ops.grouped_weight_grad(dh, x, r.offsets, E, gather=r.perm), steps, warmup)
+        ms_wg_down = time_fn(torch, lambda: ops.grouped_weight_grad(dy, h, r.offsets, E), steps, warmup)
     flops_proj = 128.0 * d * F * P
     return dict(workload=name, N=N, d=d, E=E, k=k, F=F, dtype="f32", weights=c["fmt"],
-                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3),
+                ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), weight_grad_kernel=wg_kind,
                 kernels_ms=dict(weight_grad_up=ms_wg_up, weight_grad_down=ms_wg_down),
                 step_tflops=6 * flops_proj / (ms * 1e-3) / 1e12,
                 weight_grad_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,

@@ -210,6 +210,18 @@ int ygg_adjoint_weights_f32(const float* W, int E, int d_out, int d_in, float* W
 int ygg_grouped_weight_grad_f32(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
                                 int d_in, int d_out, float* dW, float* db, ygg_stream_t stream);
 
+/* The same gradients on the fp32 MFMA units, from fp32 Pauli rows (the layout of
+ * ygg_pauli_rows_from_blade_f32) of dy (P_max rows, d_out) and a (d_in): each
+ * expert's rows are cut into chunks whose partial sums go to `workspace`
+ * (ygg_grouped_weight_grad_pauli_f32_workspace_bytes) and are added in chunk
+ * order, so results do not depend on scheduling.  dW and db as above, blade
+ * order.  CliffordLinear.backward's weight and bias gradients
+ * (clifford_linear.py:125-163) for every expert at once. */
+size_t ygg_grouped_weight_grad_pauli_f32_workspace_bytes(int P_max, int E, int d_in, int d_out);
+int ygg_grouped_weight_grad_pauli_f32(const float* dy_pauli, const float* a_pauli, const int32_t* gather,
+                                      const int32_t* offsets, int P_max, int E, int d_in, int d_out, float* dW,
+                                      float* db, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
+
 /* Gradient w.r.t. the input h of a grade-wise activation (act as in
  * ygg_grouped_clifford_linear) given grad_out; n_mv multivectors, fp32 blade
  * order; grad_in may alias grad_out. */

@@ -174,3 +174,23 @@ def test_grade_quantize_argument_checks():
     assert b"bit width" in L.ygg_last_error()
     assert L.ygg_grade_quantize(None, 2, 4, ctypes.addressof(bits), 1, None, None, None, None, None) == -1
     assert L.ygg_grade_quantize(None, 2, 4, None, 1, None, None, None, None, None) == -1
+
+
+def test_weight_grad_pauli_argument_checks():
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    need = L.ygg_grouped_weight_grad_pauli_f32_workspace_bytes(3000, 4, 16, 32)
+    # chunks of 1024 rows: ceil(3000 / 1024) + E partial planes of (d_out d_in + d_out) multivectors
+    assert need == (3 + 4) * (32 * 16 * 8 + 32 * 8) * 4
+    assert L.ygg_grouped_weight_grad_pauli_f32_workspace_bytes(-1, 4, 16, 32) == 0
+    assert L.ygg_grouped_weight_grad_pauli_f32(None, None, None, None, 10, 2, 0, 4, None, None, None, 0, None) == -1
+    assert b"bad sizes" in L.ygg_last_error()
+    fake = 4096  # never dereferenced: the checks reject before any launch
+    assert L.ygg_grouped_weight_grad_pauli_f32(fake, fake, None, fake, 3000, 4, 16, 32, fake, None, fake, need - 1,
+                                               None) == -1
+    assert b"workspace" in L.ygg_last_error()
+    assert L.ygg_grouped_weight_grad_pauli_f32(None, None, None, fake, 10, 2, 4, 4, fake, None, fake, 1 << 20,
+                                               None) == -1

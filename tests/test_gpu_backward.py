@@ -81,6 +81,35 @@ def test_grouped_weight_grad(E, d_in, d_out, P, gathered):
         assert normwise_err(db[e], db_o) < TOL_F32, e
 
 
+@pytest.mark.parametrize("E,d_in,d_out,P,gathered", [(3, 8, 16, 50, False), (2, 40, 70, 2300, True),
+                                                     (4, 64, 128, 700, True), (1, 7, 33, 1029, False),
+                                                     (5, 16, 9, 3000, True)])
+def test_grouped_weight_grad_pauli(E, d_in, d_out, P, gathered):
+    """The MFMA weight gradient from Pauli rows: per-chunk partial sums (1024 rows) added in order."""
+    ops = _ops()
+    g = np.random.default_rng(E * 7 + d_in + P)
+    dy = g.standard_normal((P, d_out, 8)).astype(np.float32)
+    nsrc = P + 17
+    a = g.standard_normal((nsrc if gathered else P, d_in, 8)).astype(np.float32)
+    gather = g.integers(0, nsrc, P).astype(np.int32) if gathered else None
+    offsets = _offsets(g, E, P)
+    say(f"weight grad (MFMA) E={E} d_in={d_in} d_out={d_out} P={P} gathered={gathered}")
+    dyp = ops.pauli_rows_from_blade_f32(torch.from_numpy(dy).cuda())
+    ap = ops.pauli_rows_from_blade_f32(torch.from_numpy(a).cuda())
+    dW, db = ops.grouped_weight_grad_pauli(dyp, ap, torch.from_numpy(offsets).cuda(), E,
+                                           gather=torch.from_numpy(gather).cuda() if gathered else None)
+    dW, db = dW.cpu().numpy(), db.cpu().numpy()
+    rows_a = a[gather] if gathered else a
+    for e in range(E):
+        sl = slice(offsets[e], offsets[e + 1])
+        if offsets[e] == offsets[e + 1]:
+            assert not dW[e].any() and not db[e].any()
+            continue
+        _, dW_o, db_o = bw.clifford_linear_backward(rows_a[sl], np.zeros((d_out, d_in, 8), np.float32), dy[sl])
+        assert normwise_err(dW[e], dW_o) < TOL_F32, e
+        assert normwise_err(db[e], db_o) < TOL_F32, e
+
+
 def _layer_case(g, N, d, F, E, k, act, router):
     import yggdrasil_amd
 
@@ -101,6 +130,7 @@ def _layer_case(g, N, d, F, E, k, act, router):
     (300, 32, 64, 8, 2, "sigmoid", "energy", True),
     (130, 8, 24, 5, 3, "relu", "logits", True),
     (1200, 16, 32, 8, 2, "gelu", "energy", False),
+    (2600, 8, 24, 2, 2, "gelu", "logits", True),  # 2600 rows per expert: the weight gradient's row chunks
 ])
 def test_layer_autograd_against_oracle(N, d, F, E, k, act, router, residual):
     g = np.random.default_rng(N + d + F)

@@ -47,6 +47,9 @@ SIGNATURES = {
                                  _c_size, _vp]),
     "ygg_adjoint_weights_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "ygg_grouped_weight_grad_f32": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "ygg_grouped_weight_grad_pauli_f32_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "ygg_grouped_weight_grad_pauli_f32": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+                                                   _c_size, _vp]),
     "ygg_activation_backward": (_c_int, [_vp, _vp, _c_size, _c_int, _vp, _vp]),
     "ygg_moe_backward_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "ygg_moe_backward": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,

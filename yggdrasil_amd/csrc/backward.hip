@@ -289,6 +289,212 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same weight gradient on the fp32 MFMA units, from Pauli rows (the fp32
+// Pauli-row layout of pauli_f32.hip: [b][re, im][c] per multivector).
+//
+// C_ji[a][c] = sum_{r, b} D_rj[a][b] conj(A_ri[c][b]) with D = M(dy), A = M(x).
+// v_mfma_f32_32x32x2_f32 contracts K = 2 lanes, taken as (re, im) of one
+// (row, b) term: with the D entry's (re, im) as the A operand and the x entry's
+// (re, im) as the B operand the sum is Re(D conj(A)); with (-im, re) as the B
+// operand it is Im(D conj(A)).  A wave owns 32 j x 32 i, eight 32 x 32
+// accumulators ((a, c) x (re, im)), 16 MFMAs per row.
+//
+// The rows of one expert are cut into chunks of kWgmChunk rows; every
+// (chunk, 64 x 64 tile) is one workgroup, which writes its Pauli sums to a
+// partial plane of its chunk.  The reduction adds an expert's chunks in chunk
+// order, so the result does not depend on scheduling.  The workgroups of the
+// first i tile also sum the D rows of their chunk for the bias gradient.
+constexpr int kWgmChunk = 1024;  // rows per chunk
+constexpr int kWgmTile = 64;     // j and i per workgroup (2 x 2 waves of 32)
+constexpr int kWgmU = 2;         // rows per register-buffered block
+
+__device__ inline bool wgm_find_chunk(const int32_t* __restrict__ offsets, int E, int chunk, int& e, int& r0,
+                                      int& r1) {
+  int acc = 0, beg = offsets[0];
+  for (int x = 0; x < E; ++x) {
+    const int end = offsets[x + 1];
+    const int n = (end - beg + kWgmChunk - 1) / kWgmChunk;
+    if (chunk < acc + n) {
+      e = x;
+      r0 = beg + (chunk - acc) * kWgmChunk;
+      r1 = min(end, r0 + kWgmChunk);
+      return true;
+    }
+    acc += n;
+    beg = end;
+  }
+  return false;
+}
+
+// grid (chunks bound, ceil(d_out / 64), ceil(d_in / 64)), 256 threads.
+// part: (chunks, d_out, d_in, 8) Pauli sums [a][c][re, im]; dbpart: (chunks, d_out, 8)
+// Pauli-row sums [b][re, im][a] of D, or NULL.
+__global__ __launch_bounds__(256) void weight_grad_mfma_kernel(const float* __restrict__ Dp,
+                                                               const float* __restrict__ Ap,
+                                                               const int32_t* __restrict__ gather,
+                                                               const int32_t* __restrict__ offsets, int E, int d_in,
+                                                               int d_out, float* __restrict__ part,
+                                                               float* __restrict__ dbpart) {
+  int e, r0, r1;
+  if (!wgm_find_chunk(offsets, E, blockIdx.x, e, r0, r1)) return;
+  (void)e;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  r0 = __builtin_amdgcn_readfirstlane(r0);
+  r1 = __builtin_amdgcn_readfirstlane(r1);
+  const int l32 = lane & 31, kk = lane >> 5;
+  const int j0 = blockIdx.y * kWgmTile + (wave & 1) * 32, i0 = blockIdx.z * kWgmTile + (wave >> 1) * 32;
+  const int jc = min(j0 + l32, d_out - 1), ic = min(i0 + l32, d_in - 1);  // clamped loads, not stored
+  const float* dcol = Dp + (size_t)jc * 8 + kk * 2;  // + row * d_out * 8; b = 0 at +0, b = 1 at +4
+  const float* acol = Ap + (size_t)ic * 8;           // + src * d_in * 8
+  const bool bias_wave = dbpart != nullptr && blockIdx.z == 0 && (wave >> 1) == 0;
+
+  pf32x16_t acc[2][2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[a][c][q][v] = 0.f;
+  float bs[4] = {0.f, 0.f, 0.f, 0.f};
+
+  struct RowOps {
+    float2 d0, d1;  // component kk of D[0][b], D[1][b] for b = 0, 1
+    float4 x0, x1;  // A[c][b], b = 0, 1: (re c0, re c1, im c0, im c1)
+  };
+  auto load_row = [&](int r, RowOps& o) {
+    const size_t src = gather ? (size_t)gather[r] : (size_t)r;
+    const float* dr = dcol + (size_t)r * d_out * 8;
+    o.d0 = *reinterpret_cast<const float2*>(dr);
+    o.d1 = *reinterpret_cast<const float2*>(dr + 4);
+    const float4* ar = reinterpret_cast<const float4*>(acol + src * d_in * 8);
+    o.x0 = ar[0];
+    o.x1 = ar[1];
+  };
+  auto mma_row = [&](const RowOps& o) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const float2 dv = b ? o.d1 : o.d0;
+      const float4 xv = b ? o.x1 : o.x0;
+      const float dd[2] = {dv.x, dv.y};
+      const float re[2] = {xv.x, xv.y}, im[2] = {xv.z, xv.w};
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float bre = kk ? im[c] : re[c];   // (re, im)[kk]
+        const float bim = kk ? re[c] : -im[c];  // (-im, re)[kk]
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          acc[a][c][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(dd[a], bre, acc[a][c][0], 0, 0, 0);
+          acc[a][c][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(dd[a], bim, acc[a][c][1], 0, 0, 0);
+        }
+      }
+    }
+    if (bias_wave) {
+      bs[0] += o.d0.x;
+      bs[1] += o.d0.y;
+      bs[2] += o.d1.x;
+      bs[3] += o.d1.y;
+    }
+  };
+  // rows in blocks of kWgmU, double buffered in registers
+  const int nblk = (r1 - r0) / kWgmU;
+  RowOps b0[kWgmU], b1[kWgmU];
+  if (nblk > 0) {
+#pragma unroll
+    for (int u = 0; u < kWgmU; ++u) load_row(r0 + u, b0[u]);
+  }
+  for (int b = 0; b < nblk; b += 2) {
+    if (b + 1 < nblk) {
+#pragma unroll
+      for (int u = 0; u < kWgmU; ++u) load_row(r0 + (b + 1) * kWgmU + u, b1[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kWgmU; ++u) mma_row(b0[u]);
+    if (b + 1 < nblk) {
+      if (b + 2 < nblk) {
+#pragma unroll
+        for (int u = 0; u < kWgmU; ++u) load_row(r0 + (b + 2) * kWgmU + u, b0[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kWgmU; ++u) mma_row(b1[u]);
+    }
+  }
+  for (int r = r0 + nblk * kWgmU; r < r1; ++r) {
+    RowOps o;
+    load_row(r, o);
+    mma_row(o);
+  }
+
+  // lane holds column i0 + l32, rows j0 + 8 (v / 4) + 4 kk + v % 4
+  const int i = i0 + l32;
+  float* pc = part + (size_t)blockIdx.x * d_out * d_in * 8;
+  if (i < d_in) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int j = j0 + 8 * (v >> 2) + 4 * kk + (v & 3);
+      if (j >= d_out) continue;
+      float4* q = reinterpret_cast<float4*>(pc + ((size_t)j * d_in + i) * 8);
+      q[0] = make_float4(acc[0][0][0][v], acc[0][0][1][v], acc[0][1][0][v], acc[0][1][1][v]);
+      q[1] = make_float4(acc[1][0][0][v], acc[1][0][1][v], acc[1][1][0][v], acc[1][1][1][v]);
+    }
+  }
+  if (bias_wave && j0 + l32 < d_out) {
+    float* q = dbpart + ((size_t)blockIdx.x * d_out + j0 + l32) * 8 + kk * 2;  // [b][k][a]
+    *reinterpret_cast<float2*>(q) = make_float2(bs[0], bs[1]);
+    *reinterpret_cast<float2*>(q + 4) = make_float2(bs[2], bs[3]);
+  }
+}
+
+// dW[e, j, i] = (1/2) blade(sum over the expert's chunks, in order, of the Pauli sums);
+// db[e, j] likewise from the D-row sums.  One thread per (e, j, i) multivector.
+__global__ __launch_bounds__(256) void weight_grad_reduce_kernel(const float* __restrict__ part,
+                                                                 const float* __restrict__ dbpart,
+                                                                 const int32_t* __restrict__ offsets, int E, int d_in,
+                                                                 int d_out, float* __restrict__ dW,
+                                                                 float* __restrict__ db) {
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)E * d_out * d_in) return;
+  const size_t ji = n % ((size_t)d_out * d_in);
+  const int e = (int)(n / ((size_t)d_out * d_in));
+  int cb = 0, beg = offsets[0];
+  for (int x = 0; x < e; ++x) {
+    const int end = offsets[x + 1];
+    cb += (end - beg + kWgmChunk - 1) / kWgmChunk;
+    beg = end;
+  }
+  const int ce = cb + (offsets[e + 1] - beg + kWgmChunk - 1) / kWgmChunk;
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int c = cb; c < ce; ++c) {
+    const float4* q = reinterpret_cast<const float4*>(part + ((size_t)c * d_out * d_in + ji) * 8);
+    const float4 u = q[0], w = q[1];
+    s[0] += u.x; s[1] += u.y; s[2] += u.z; s[3] += u.w;
+    s[4] += w.x; s[5] += w.y; s[6] += w.z; s[7] += w.w;
+  }
+  float o[8];
+  pauli_to_blade(s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7], o);
+  float4* dst = reinterpret_cast<float4*>(dW + n * 8);
+  dst[0] = make_float4(0.5f * o[0], 0.5f * o[1], 0.5f * o[2], 0.5f * o[3]);
+  dst[1] = make_float4(0.5f * o[4], 0.5f * o[5], 0.5f * o[6], 0.5f * o[7]);
+  if (db != nullptr && ji % d_in == 0) {
+    const int j = (int)(ji / d_in);
+    float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // [b][k][a]
+    for (int c = cb; c < ce; ++c) {
+      const float4* q = reinterpret_cast<const float4*>(dbpart + ((size_t)c * d_out + j) * 8);
+      const float4 u = q[0], w = q[1];
+      t[0] += u.x; t[1] += u.y; t[2] += u.z; t[3] += u.w;
+      t[4] += w.x; t[5] += w.y; t[6] += w.z; t[7] += w.w;
+    }
+    // entry (a, b): re at b * 4 + a, im at b * 4 + 2 + a
+    pauli_to_blade(t[0], t[2], t[4], t[6], t[1], t[3], t[5], t[7], o);
+    float4* q = reinterpret_cast<float4*>(db + ((size_t)e * d_out + j) * 8);
+    q[0] = make_float4(0.5f * o[0], 0.5f * o[1], 0.5f * o[2], 0.5f * o[3]);
+    q[1] = make_float4(0.5f * o[4], 0.5f * o[5], 0.5f * o[6], 0.5f * o[7]);
+  }
+}
+
 }  // namespace
 
 int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
@@ -297,6 +503,30 @@ int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, 
   hipLaunchKernelGGL(weight_grad_kernel, dim3((d_out + kWgT - 1) / kWgT, (d_in + kWgT - 1) / kWgT, E), dim3(256), 0,
                      stream, dy, a, gather, offsets, d_in, d_out, dW, db);
   return check_launch("weight gradient");
+}
+
+size_t weight_grad_pauli_workspace_bytes(int P_max, int E, int d_in, int d_out) {
+  const size_t chunks = (size_t)(P_max + kWgmChunk - 1) / kWgmChunk + E;
+  return chunks * ((size_t)d_out * d_in * 8 + (size_t)d_out * 8) * sizeof(float);
+}
+
+int weight_grad_pauli(const float* dy_pauli, const float* a_pauli, const int32_t* gather, const int32_t* offsets,
+                      int P_max, int E, int d_in, int d_out, float* dW, float* db, void* workspace,
+                      hipStream_t stream) {
+  if (E == 0) return 0;
+  const size_t chunks = (size_t)(P_max + kWgmChunk - 1) / kWgmChunk + E;
+  float* part = static_cast<float*>(workspace);
+  float* dbpart = db ? part + chunks * d_out * d_in * 8 : nullptr;
+  if (P_max > 0) {
+    hipLaunchKernelGGL(weight_grad_mfma_kernel,
+                       dim3((unsigned)chunks, (d_out + kWgmTile - 1) / kWgmTile, (d_in + kWgmTile - 1) / kWgmTile),
+                       dim3(256), 0, stream, dy_pauli, a_pauli, gather, offsets, E, d_in, d_out, part, dbpart);
+    if (check_launch("weight gradient (MFMA)")) return -1;
+  }
+  const size_t n = (size_t)E * d_out * d_in;
+  hipLaunchKernelGGL(weight_grad_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, part, dbpart,
+                     offsets, E, d_in, d_out, dW, db);
+  return check_launch("weight gradient (reduction)");
 }
 
 int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream) {
@@ -361,6 +591,25 @@ YGG_API int ygg_grouped_weight_grad_f32(const float* dy, const float* a, const i
                 "ygg_grouped_weight_grad_f32: bad sizes E=%d d_in=%d d_out=%d", E, d_in, d_out);
   YGG_CHECK_ARG(E == 0 || (dy && a && offsets && dW), "ygg_grouped_weight_grad_f32: null pointer argument");
   return grouped_weight_grad(dy, a, gather, offsets, E, d_in, d_out, dW, db, stream);
+}
+
+YGG_API size_t ygg_grouped_weight_grad_pauli_f32_workspace_bytes(int P_max, int E, int d_in, int d_out) {
+  if (P_max < 0 || E < 0 || d_in < 1 || d_out < 1) return 0;
+  return weight_grad_pauli_workspace_bytes(P_max, E, d_in, d_out);
+}
+
+YGG_API int ygg_grouped_weight_grad_pauli_f32(const float* dy_pauli, const float* a_pauli, const int32_t* gather,
+                                              const int32_t* offsets, int P_max, int E, int d_in, int d_out,
+                                              float* dW, float* db, void* workspace, size_t workspace_bytes,
+                                              hipStream_t stream) {
+  YGG_CHECK_ARG(P_max >= 0 && E >= 0 && E <= 65535 && d_in >= 1 && d_out >= 1,
+                "ygg_grouped_weight_grad_pauli_f32: bad sizes P_max=%d E=%d d_in=%d d_out=%d", P_max, E, d_in, d_out);
+  YGG_CHECK_ARG(E == 0 || (offsets && dW && workspace), "ygg_grouped_weight_grad_pauli_f32: null pointer argument");
+  YGG_CHECK_ARG(P_max == 0 || (dy_pauli && a_pauli), "ygg_grouped_weight_grad_pauli_f32: null rows");
+  YGG_CHECK_ARG(workspace_bytes >= weight_grad_pauli_workspace_bytes(P_max, E, d_in, d_out),
+                "ygg_grouped_weight_grad_pauli_f32: workspace of %zu bytes, need %zu", workspace_bytes,
+                weight_grad_pauli_workspace_bytes(P_max, E, d_in, d_out));
+  return weight_grad_pauli(dy_pauli, a_pauli, gather, offsets, P_max, E, d_in, d_out, dW, db, workspace, stream);
 }
 
 YGG_API int ygg_activation_backward(const float* h, const float* grad_out, size_t n_mv, int act, float* grad_in,

@@ -243,6 +243,8 @@ YGG_API int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int
 // same inputs), so perm, slot_pos and offsets match the forward's; so are the
 // activations the backward needs (h before and after the activation, y).
 // The regions of its workspace, in order (each 256-byte aligned).
+constexpr int kWgradMfmaRowsPerExpert = 256;  // mean rows per expert from which the MFMA weight gradient runs
+
 static int bw_regions(int N, int d, int F, int E, int k, size_t* r) {
   const size_t P = (size_t)N * k;
   int n = 0;
@@ -257,6 +259,7 @@ static int bw_regions(int N, int d, int F, int E, int k, size_t* r) {
   r[n++] = (size_t)N * d * 32;  // x in Pauli rows
   for (int q = 0; q < 4; ++q) r[n++] = P * F * 32;  // h_pre, h, Pauli rows of h / dh_pre, dh / dh_pre
   for (int q = 0; q < 3; ++q) r[n++] = P * d * 32;  // y / dx rows, dy, Pauli rows of dy
+  r[n++] = weight_grad_pauli_workspace_bytes((int)P, E, d, F);  // weight-gradient partial sums (either product)
   return n;
 }
 
@@ -309,6 +312,7 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   float* y = static_cast<float*>(take());   // y, then dx rows
   float* dy = static_cast<float*>(take());
   float* dp = static_cast<float*>(take());  // Pauli rows of dy
+  void* wg = take();                        // weight-gradient partial sums
 
   if (logits) {
     if (ygg_route(logits, N, E, k, idx, tw, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
@@ -318,8 +322,11 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   }
   // forward recompute: h_pre (unless the forward kept it), h (blade), y (blade)
   const float* hp_in = h_pre_saved;
+  // the MFMA weight gradient pays off with enough rows per expert; below that the
+  // vector-ALU kernel, which spreads a tile's pairs over more waves, is faster
+  const bool wg_mfma = P >= (size_t)kWgradMfmaRowsPerExpert * E;
+  if ((!hp_in || wg_mfma) && ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
   if (!hp_in) {
-    if (ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
     if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
       return -1;
     hp_in = h_pre;
@@ -334,13 +341,17 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   if (ygg_pauli_rows_from_blade_f32(dy, (int)P, d, dp, stream)) return -1;
   if (ygg_pauli_grouped_linear_f32(dp, nullptr, (int)P, w_down_adj, nullptr, offsets, E, d, F, kActNone, dh, 1, stream))
     return -1;
-  if (grouped_weight_grad(dy, h, nullptr, offsets, E, F, d, dw_down, db_down, stream)) return -1;
+  if (wg_mfma ? weight_grad_pauli(dp, fp, nullptr, offsets, (int)P, E, F, d, dw_down, db_down, wg, stream)
+              : grouped_weight_grad(dy, h, nullptr, offsets, E, F, d, dw_down, db_down, stream))
+    return -1;
   // activation backward (in place), up backward -> dx rows, dW_up, db_up
   if (activation_backward(hp_in, dh, P * F, act, dh, stream)) return -1;
   if (ygg_pauli_rows_from_blade_f32(dh, (int)P, F, fp, stream)) return -1;
   if (ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_up_adj, nullptr, offsets, E, F, d, kActNone, y, 1, stream))
     return -1;
-  if (grouped_weight_grad(dh, x, perm, offsets, E, d, F, dw_up, db_up, stream)) return -1;
+  if (wg_mfma ? weight_grad_pauli(fp, xp, perm, offsets, (int)P, E, d, F, dw_up, db_up, wg, stream)
+              : grouped_weight_grad(dh, x, perm, offsets, E, d, F, dw_up, db_up, stream))
+    return -1;
   // dispatch backward: each token's rows summed, plus dout when the forward added x
   return dispatch_backward(y, N, k, d, slot_pos, residual ? dout : nullptr, dx, stream);
 }

@@ -158,6 +158,13 @@ int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, i
 // is not NULL) and the dispatch's (dx_t = residual_grad_t + sum_s dxs[slot]).
 int grouped_weight_grad(const float* dy, const float* a, const int32_t* gather, const int32_t* offsets, int E,
                         int d_in, int d_out, float* dW, float* db, hipStream_t stream);
+// The same weight and bias gradients on the fp32 MFMA units from fp32 Pauli rows
+// (pauli_f32.hip's layout) of dy (P_max rows) and a; per-chunk partial sums go to
+// `workspace` (weight_grad_pauli_workspace_bytes) and are added in chunk order.
+size_t weight_grad_pauli_workspace_bytes(int P_max, int E, int d_in, int d_out);
+int weight_grad_pauli(const float* dy_pauli, const float* a_pauli, const int32_t* gather, const int32_t* offsets,
+                      int P_max, int E, int d_in, int d_out, float* dW, float* db, void* workspace,
+                      hipStream_t stream);
 int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream);
 int activation_forward(const float* h, size_t n_mv, int act, float* out, hipStream_t stream);
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,

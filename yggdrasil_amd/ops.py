@@ -494,6 +494,27 @@ def grouped_weight_grad(dy: torch.Tensor, a: torch.Tensor, offsets: torch.Tensor
     return dW, db
 
 
+def grouped_weight_grad_pauli(dy_pauli: torch.Tensor, a_pauli: torch.Tensor, offsets: torch.Tensor, E: int,
+                              gather: torch.Tensor | None = None, with_bias: bool = True,
+                              workspace: torch.Tensor | None = None):
+    """:func:`grouped_weight_grad` on the fp32 MFMA units from fp32 Pauli rows
+    (:func:`pauli_rows_from_blade_f32`) of dy (P, d_out, 2, 2, 2) and a (.., d_in, 2, 2, 2)."""
+    dev = _dev(dy_pauli, a_pauli, offsets, gather)
+    for t in (dy_pauli, a_pauli):
+        if t.dtype != torch.float32 or t.dim() != 5 or tuple(t.shape[2:]) != (2, 2, 2):
+            raise ValueError("grouped_weight_grad_pauli: operands must be fp32 Pauli rows (rows, d, 2, 2, 2)")
+    P, d_out, d_in = dy_pauli.shape[0], dy_pauli.shape[1], a_pauli.shape[1]
+    dW = torch.empty((E, d_out, d_in, 8), device=dev, dtype=torch.float32)
+    db = torch.empty((E, d_out, 8), device=dev, dtype=torch.float32) if with_bias else None
+    ws_bytes = lib().ygg_grouped_weight_grad_pauli_f32_workspace_bytes(P, E, d_in, d_out)
+    if workspace is None:
+        workspace = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    check(lib().ygg_grouped_weight_grad_pauli_f32(ptr(dy_pauli), ptr(a_pauli), ptr(gather), ptr(offsets), P, E, d_in,
+                                                  d_out, ptr(dW), ptr(db), ptr(workspace), workspace.numel(),
+                                                  stream_handle(dev)), "grouped_weight_grad_pauli")
+    return dW, db
+
+
 def activation_backward(h: torch.Tensor, grad_out: torch.Tensor, act: str) -> torch.Tensor:
     """Gradient w.r.t. the input of a grade-wise activation; h, grad_out (..., 8) fp32."""
     dev = _dev(h, grad_out)
