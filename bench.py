@@ -402,7 +402,9 @@ def run_train_config(torch, ops, name, c, steps, warmup):
                 kernels_ms=dict(weight_grad_up=ms_wg_up, weight_grad_down=ms_wg_down),
                 step_tflops=6 * flops_proj / (ms * 1e-3) / 1e12,
                 weight_grad_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,
-                weight_grad_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32)
+                weight_grad_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32,
+                # the Pauli form issues half the algorithmic FLOPs (above 1 above means that)
+                weight_grad_issued_frac_f32=flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32)
 
 
 def calibrate_gemm(torch):

@@ -183,8 +183,8 @@ def test_weight_grad_pauli_argument_checks():
         pytest.skip("library not built")
     L = _native.lib()
     need = L.ygg_grouped_weight_grad_pauli_f32_workspace_bytes(3000, 4, 16, 32)
-    # chunks of 1024 rows: ceil(3000 / 1024) + E partial planes of (d_out d_in + d_out) multivectors
-    assert need == (3 + 4) * (32 * 16 * 8 + 32 * 8) * 4
+    # chunks of 384 rows: ceil(3000 / 384) + E partial planes of (d_out d_in + d_out) multivectors
+    assert need == (8 + 4) * (32 * 16 * 8 + 32 * 8) * 4
     assert L.ygg_grouped_weight_grad_pauli_f32_workspace_bytes(-1, 4, 16, 32) == 0
     assert L.ygg_grouped_weight_grad_pauli_f32(None, None, None, None, 10, 2, 0, 4, None, None, None, 0, None) == -1
     assert b"bad sizes" in L.ygg_last_error()

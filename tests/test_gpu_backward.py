@@ -85,7 +85,7 @@ def test_grouped_weight_grad(E, d_in, d_out, P, gathered):
                                                      (4, 64, 128, 700, True), (1, 7, 33, 1029, False),
                                                      (5, 16, 9, 3000, True)])
 def test_grouped_weight_grad_pauli(E, d_in, d_out, P, gathered):
-    """The MFMA weight gradient from Pauli rows: per-chunk partial sums (1024 rows) added in order."""
+    """The MFMA weight gradient from Pauli rows: per-chunk partial sums (384 rows) added in order."""
     ops = _ops()
     g = np.random.default_rng(E * 7 + d_in + P)
     dy = g.standard_normal((P, d_out, 8)).astype(np.float32)

@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void weight_grad_kernel(const float* __restric
 // partial plane of its chunk.  The reduction adds an expert's chunks in chunk
 // order, so the result does not depend on scheduling.  The workgroups of the
 // first i tile also sum the D rows of their chunk for the bias gradient.
-constexpr int kWgmChunk = 1024;  // rows per chunk
+constexpr int kWgmChunk = 384;  // rows per chunk (measured best of 128-2048 at the C3 shape)
 constexpr int kWgmTile = 64;     // j and i per workgroup (2 x 2 waves of 32)
 constexpr int kWgmU = 2;         // rows per register-buffered block
 
