@@ -26,9 +26,13 @@
 // A workgroup of 4 waves owns a tile of 16 tokens (32 GEMM rows) of one
 // expert x 32 output multivectors; the waves split the contraction and add
 // their four 32x32 accumulators (a = 0, 1 x re, im) in LDS in wave order.
-// blockIdx.z optionally splits the contraction further across workgroups
-// into fp32 partial planes (no activation), which the consumer adds in split
-// order.  Deterministic throughout.
+// The column tiles of a row tile run back to back on one XCD, so the row tile's
+// activations come from HBM once.  blockIdx.z optionally splits the
+// contraction further across workgroups into fp32 partial planes (no
+// activation), which the consumer adds in split order.  Deterministic
+// throughout.  (Wider tiles -- 32 tokens x 64 columns, each wave a quadrant
+// over the whole contraction, no cross-wave sum -- were measured 40-80 % slower
+// at the C3 shape.)
 
 #include <algorithm>
 
@@ -45,16 +49,17 @@ constexpr int kF32U = 4;      // input multivectors per register-buffered block 
 
 enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2 };
 
+template <int TOK>  // tokens per tile
 __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E, int tile, int& e, int& row0,
                                      int& row_end) {
   int acc = 0;
   int beg = offsets[0];
   for (int x = 0; x < E; ++x) {
     const int end = offsets[x + 1];
-    const int nt = (end - beg + kF32Tok - 1) / kF32Tok;
+    const int nt = (end - beg + TOK - 1) / TOK;
     if (tile < acc + nt) {
       e = x;
-      row0 = beg + (tile - acc) * kF32Tok;
+      row0 = beg + (tile - acc) * TOK;
       row_end = end;
       return true;
     }
@@ -64,45 +69,13 @@ __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E,
   return false;
 }
 
-template <int ACT, int OUT>
-__global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
-    const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
-    const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
-    float* __restrict__ Y, float* __restrict__ Ypre) {
-  __shared__ float4 part[kF32Waves][2 * kF32Tok][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
-  int e, row0, row_end;
-  if (!f32_find_tile(offsets, E, blockIdx.x, e, row0, row_end)) return;
-  const int col0 = blockIdx.y * kF32Cols;
-  const int split = blockIdx.z, splits = gridDim.z;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the K loop runs on scalars
-  const int l32 = lane & 31, k = lane >> 5;
-
-  // A operand: GEMM row (t, b) = l32, real (k = 0) or imaginary (k = 1) run
-  int m = row0 + (l32 >> 1);
-  m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
-  const int src = gather ? gather[m] : m;
-  const float* arow = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
-  // B operand: output column j (clamped: columns past d_out are not stored)
-  const int jc = min(col0 + l32, d_out - 1);
-  const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
-  const size_t w_step = (size_t)2 * d_out * 8;  // floats from input i to i + 1
-  // contraction range of this (split, wave)
-  const int per_split = (d_in + splits - 1) / splits;
-  const int is0 = split * per_split, is1 = min(d_in, is0 + per_split);
-  const int per_wave = (max(is1 - is0, 0) + kF32Waves - 1) / kF32Waves;
-  const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
-
-  f32x16v_t acc[2][2];
-#pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[a][q][v] = 0.f;
-  // Operands of input multivector i: x (re, im) of the lane's GEMM row and the eight
-  // weight floats of its column.  Blocks of kF32U multivectors are double buffered in
-  // registers, so one block's loads are in flight while the previous block's MFMAs run.
+// The contraction over inputs [i0, i1) of one wave's 32 GEMM rows x 32 columns:
+// operands of input i are x (re, im) of the lane's GEMM row (arow + 8 i) and the
+// eight weight floats of its column (wrow + i w_step).  Blocks of kF32U inputs are
+// double buffered in registers, so one block's loads are in flight while the
+// previous block's MFMAs run.  i0, i1 must be wave-uniform.
+__device__ inline void f32_kloop(f32x16v_t (&acc)[2][2], const float* __restrict__ arow,
+                                 const float* __restrict__ wrow, size_t w_step, int i0, int i1) {
   auto load_op = [&](int i, float2& xa, float4& w0, float4& w1) {
     xa = *reinterpret_cast<const float2*>(arow + (size_t)i * 8);
     w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
@@ -118,6 +91,12 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
     acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.z, acc[1][0], 0, 0, 0);
     acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.w, acc[1][1], 0, 0, 0);
   };
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][q][v] = 0.f;
   const int nblk = max(i1 - i0, 0) / kF32U;
   float2 xa0[kF32U], xa1[kF32U];
   float4 wa0[kF32U], wb0[kF32U], wa1[kF32U], wb1[kF32U];
@@ -147,6 +126,80 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
     load_op(i, xa, w0, w1);
     mma(xa, w0, w1);
   }
+}
+
+// One output multivector (token row, column j) from its Pauli sums Y[a][b] = (re, im):
+// blade map, bias (split 0 only for partial planes), the pre-activation rows when
+// Ypre is set, activation, and the store in the OUT layout.
+template <int ACT, int OUT>
+__device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y01i, float y10r, float y10i, float y11r,
+                                    float y11i, const float* __restrict__ bias, int e, int row, int j, int d_out,
+                                    int split, int P_max, float* __restrict__ Y, float* __restrict__ Ypre) {
+  float y[8];
+  pauli_to_blade(y00r, y00i, y01r, y01i, y10r, y10i, y11r, y11i, y);
+  if (bias != nullptr && (OUT != kF32OutPartial || split == 0)) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) y[c] += bias[((size_t)e * d_out + j) * 8 + blade_to_mask(c)];
+  }
+  if constexpr (OUT == kF32OutPauliRows) {
+    if (Ypre != nullptr) {  // the pre-activation rows, blade order (kept for the backward)
+      float4* q = reinterpret_cast<float4*>(Ypre + ((size_t)row * d_out + j) * 8);
+      q[0] = make_float4(y[0], y[1], y[2], y[3]);
+      q[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    activate_blade<ACT>(y);
+    float c0[4], c1[4];
+    blade_to_pauli(y, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
+    float4* q = reinterpret_cast<float4*>(Y + ((size_t)row * d_out + j) * 8);  // [b][k][c]
+    q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+    q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+  } else {
+    size_t mv = (size_t)row * d_out + j;
+    if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
+    else activate_blade<ACT>(y);
+    float4* p = reinterpret_cast<float4*>(Y + mv * 8);
+    p[0] = make_float4(y[0], y[1], y[2], y[3]);
+    p[1] = make_float4(y[4], y[5], y[6], y[7]);
+  }
+}
+
+template <int ACT, int OUT>
+__global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
+    const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
+    const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
+    float* __restrict__ Y, float* __restrict__ Ypre, int n_xcd) {
+  __shared__ float4 part[kF32Waves][2 * kF32Tok][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
+  int e, row0, row_end;
+  // The column tiles of one row tile run on one XCD, one after the other in
+  // dispatch order, so its rows are read once into that XCD's L2: workgroup b runs
+  // on XCD b mod n_xcd and takes column tile (b / n_xcd) mod n_ct of row tile
+  // (b / (n_xcd n_ct)) n_xcd + b mod n_xcd.
+  const int n_ct = (d_out + kF32Cols - 1) / kF32Cols;
+  const int xcd = blockIdx.x % n_xcd, q = blockIdx.x / n_xcd;
+  const int ct = q % n_ct, rt = (q / n_ct) * n_xcd + xcd;
+  if (!f32_find_tile<kF32Tok>(offsets, E, rt, e, row0, row_end)) return;
+  const int col0 = ct * kF32Cols;
+  const int split = blockIdx.z, splits = gridDim.z;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the K loop runs on scalars
+  const int l32 = lane & 31, k = lane >> 5;
+
+  // A operand: GEMM row (t, b) = l32, real (k = 0) or imaginary (k = 1) part
+  int m = row0 + (l32 >> 1);
+  m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
+  const int src = gather ? gather[m] : m;
+  const float* arow = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
+  // B operand: output column j (clamped: columns past d_out are not stored)
+  const int jc = min(col0 + l32, d_out - 1);
+  const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
+  // contraction range of this (split, wave)
+  const int per_split = (d_in + splits - 1) / splits;
+  const int is0 = split * per_split, is1 = min(d_in, is0 + per_split);
+  const int per_wave = (max(is1 - is0, 0) + kF32Waves - 1) / kF32Waves;
+  const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
+
+  f32x16v_t acc[2][2];
+  f32_kloop(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1);
   // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4
 #pragma unroll
   for (int v = 0; v < 16; ++v)
@@ -167,33 +220,9 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
       s0.x += p0.x; s0.y += p0.y; s0.z += p0.z; s0.w += p0.w;
       s1.x += p1.x; s1.y += p1.y; s1.z += p1.z; s1.w += p1.w;
     }
-    float y[8];
     // Y[a][b]: a = 0 -> (x, y), a = 1 -> (z, w); b from the row
-    pauli_to_blade(s0.x, s0.y, s1.x, s1.y, s0.z, s0.w, s1.z, s1.w, y);
-    if (bias != nullptr && (OUT != kF32OutPartial || split == 0)) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) y[c] += bias[((size_t)e * d_out + j) * 8 + blade_to_mask(c)];
-    }
-    if constexpr (OUT == kF32OutPauliRows) {
-      if (Ypre != nullptr) {  // the pre-activation rows, blade order (kept for the backward)
-        float4* q = reinterpret_cast<float4*>(Ypre + ((size_t)row * d_out + j) * 8);
-        q[0] = make_float4(y[0], y[1], y[2], y[3]);
-        q[1] = make_float4(y[4], y[5], y[6], y[7]);
-      }
-      activate_blade<ACT>(y);
-      float c0[4], c1[4];
-      blade_to_pauli(y, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
-      float4* q = reinterpret_cast<float4*>(Y + ((size_t)row * d_out + j) * 8);  // [b][k][c]
-      q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
-      q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
-    } else {
-      size_t mv = (size_t)row * d_out + j;
-      if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
-      else activate_blade<ACT>(y);
-      float4* p = reinterpret_cast<float4*>(Y + mv * 8);
-      p[0] = make_float4(y[0], y[1], y[2], y[3]);
-      p[1] = make_float4(y[4], y[5], y[6], y[7]);
-    }
+    f32_store_mv<ACT, OUT>(s0.x, s0.y, s1.x, s1.y, s0.z, s0.w, s1.z, s1.w, bias, e, row, j, d_out, split, P_max, Y,
+                           Ypre);
   }
 }
 
@@ -246,11 +275,36 @@ __global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const floa
 using namespace ygg;
 
 namespace {
+int f32_xcds() {  // XCDs that workgroups are dealt to round robin (8 on MI355X)
+  static thread_local int cached_dev = -1, cached = 1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 64;
+    cached = (cus % 8 == 0) ? 8 : 1;
+    cached_dev = dev;
+  }
+  return cached;
+}
+
+// x: (row tile, column tile) pairs, row tiles rounded up to a multiple of the XCD
+// count; z: contraction splits
+dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd) {
+  long long rts = ((long long)P_max + kF32Tok - 1) / kF32Tok + E;
+  rts = (rts + n_xcd - 1) / n_xcd * n_xcd;
+  return dim3((unsigned)(rts * ((d_out + kF32Cols - 1) / kF32Cols)), 1, splits);
+}
+
 template <int OUT>
-int launch_f32_act(int act, dim3 grid, hipStream_t st, const float* X, const int32_t* gather, const float* W,
+int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const int32_t* gather, const float* W,
                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
                    float* Ypre = nullptr) {
-#define YGG_F(A) pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y, Ypre)
+  const int n_xcd = f32_xcds();
+  const dim3 grid = f32_grid(P_max, E, d_out, splits, n_xcd);
+#define YGG_F(A)                                                                                                  \
+  pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y, \
+                                                            Ypre, n_xcd)
   switch (act) {
     case kActNone: YGG_F(kActNone); break;
     case kActGelu: YGG_F(kActGelu); break;
@@ -259,10 +313,6 @@ int launch_f32_act(int act, dim3 grid, hipStream_t st, const float* X, const int
   }
 #undef YGG_F
   return check_launch("pauli_f32");
-}
-
-dim3 f32_grid(int P_max, int E, int d_out, int splits) {
-  return dim3((P_max + kF32Tok - 1) / kF32Tok + E, (d_out + kF32Cols - 1) / kF32Cols, splits);
 }
 }  // namespace
 
@@ -284,16 +334,16 @@ int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, con
                                   const int32_t* offsets, int E, int d_in, int d_out, int splits, float* y_planes,
                                   hipStream_t stream) {
   if (P_max == 0) return 0;
-  return launch_f32_act<kF32OutPartial>(kActNone, f32_grid(P_max, E, d_out, splits), stream, x, nullptr, w, bias,
-                                        offsets, E, d_in, d_out, P_max, y_planes);
+  return launch_f32_act<kF32OutPartial>(kActNone, splits, stream, x, nullptr, w, bias, offsets, E, d_in, d_out, P_max,
+                                        y_planes);
 }
 
 int ygg::pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, const float* w,
                                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act,
                                    float* y_pauli, float* y_pre, hipStream_t stream) {
   if (P_max == 0) return 0;
-  return launch_f32_act<kF32OutPauliRows>(act, f32_grid(P_max, E, d_out, 1), stream, x, gather, w, bias, offsets, E,
-                                          d_in, d_out, P_max, y_pauli, y_pre);
+  return launch_f32_act<kF32OutPauliRows>(act, 1, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y_pauli,
+                                          y_pre);
 }
 
 YGG_API int ygg_pauli_rows_from_blade_f32(const float* x, int rows, int d, float* out, hipStream_t stream) {
@@ -315,8 +365,7 @@ YGG_API int ygg_pauli_grouped_linear_f32(const float* x, const int32_t* gather, 
                 "ygg_pauli_grouped_linear_f32: bad sizes E=%d P=%d d_in=%d d_out=%d", E, P_max, d_in, d_out);
   if (P_max == 0) return 0;
   YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear_f32: null pointer");
-  const dim3 grid = f32_grid(P_max, E, d_out, 1);
   if (y_layout == kF32OutPauliRows)
-    return launch_f32_act<kF32OutPauliRows>(act, grid, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
-  return launch_f32_act<kF32OutBlade>(act, grid, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
+    return launch_f32_act<kF32OutPauliRows>(act, 1, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
+  return launch_f32_act<kF32OutBlade>(act, 1, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
 }
