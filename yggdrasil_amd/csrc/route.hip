@@ -22,11 +22,12 @@
 //                    ranks every slot among the block's slots of that expert
 //                    in token order; the rank goes to slot_pos and the block
 //                    histogram to the workspace.
-//   K2 route_scan    one workgroup: for every expert, the exclusive scan of the
-//                    block histograms over blocks (in place; a wave per expert,
-//                    shuffle scans), counts, offsets.
-//   K3 route_place   one thread per slot: slot_pos += offsets[e] + block base;
-//                    perm[slot_pos] = token.
+//   K2 route_scan_place  one thread per slot, 256 per workgroup: the workgroup
+//                    sums the block histograms it needs (every expert's total,
+//                    an exclusive scan of those gives the offsets, and the base
+//                    of each K1 block its slots come from), then slot_pos +=
+//                    offsets[e] + block base; perm[slot_pos] = token.  Workgroup
+//                    0 writes counts and offsets.
 // Within an expert the rows are in ascending token order, the reference's
 // dispatch order (hlm_block.py:172-178).
 
@@ -37,7 +38,6 @@ namespace ygg {
 
 constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
-constexpr int kScanMaxThreads = 1024;
 
 template <int Q>  // Q = ceil(E / 8) logits per lane
 __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
@@ -81,66 +81,91 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
   }
 }
 
-// One workgroup of 1024 threads.  Wave w scans experts w, w + 16, ...: lane l
-// owns the contiguous blocks [l per, (l + 1) per) of the expert-major block
-// histograms, sums them, a shuffle scan over the lanes gives each lane's base,
-// and the lane rewrites its blocks with their exclusive prefix.  Wave 0 then
-// scans the expert totals into counts and offsets.
-__global__ __launch_bounds__(kScanMaxThreads) void route_scan(int32_t* __restrict__ block_hist, int nblocks, int E,
-                                                              int32_t* __restrict__ counts,
-                                                              int32_t* __restrict__ offsets) {
-  __shared__ int32_t tot[kMaxExperts];
+// The scan and the placement in one launch: every placing workgroup (256 slots)
+// sums the block histograms itself -- each expert's total, and its base in each of
+// the few K1 blocks its slots come from -- so no workgroup waits on another.
+// Workgroup 0 also writes counts and offsets.  The histograms are read, not
+// rewritten.
+constexpr int kPlaceSlots = 256;
+constexpr int kPlaceMaxSel = kPlaceSlots / kSelTokens + 2;  // K1 blocks one placing workgroup can touch
+
+__global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* __restrict__ topk_idx,
+                                                                const int32_t* __restrict__ block_hist, int N, int nb,
+                                                                int E, int k, int32_t* __restrict__ perm,
+                                                                int32_t* __restrict__ slot_pos,
+                                                                int32_t* __restrict__ counts,
+                                                                int32_t* __restrict__ offsets) {
+  __shared__ int32_t s_tot[kMaxExperts];
+  __shared__ int32_t s_off[kMaxExperts];
+  __shared__ int32_t s_base[kMaxExperts][kPlaceMaxSel];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per = (nblocks + 63) / 64;
-  for (int x = wave; x < E; x += kScanMaxThreads / 64) {
-    int32_t* h = block_hist + (size_t)x * nblocks;
-    const int b0 = min(nblocks, lane * per), b1 = min(nblocks, b0 + per);
-    int sum = 0;
-#pragma unroll 8
-    for (int b = b0; b < b1; ++b) sum += h[b];
-    int incl = sum;
+  const long long slots = (long long)N * k;
+  const long long f0 = (long long)blockIdx.x * kPlaceSlots;
+  const long long f1 = f0 + kPlaceSlots < slots ? f0 + kPlaceSlots : slots;
+  // this thread's slot: its loads first, they do not depend on the scan
+  const long long f = f0 + tid;
+  const bool has_slot = f < f1;
+  const int my_e = has_slot ? topk_idx[f] : 0;
+  const int my_rank = has_slot ? slot_pos[f] : 0;
+  // the K1 blocks [sb0, sb1) holding this workgroup's tokens (at most kPlaceMaxSel)
+  const int sb0 = f0 < slots ? (int)(f0 / k) / kSelTokens : 0;
+  const int sb1 = f0 < slots ? (int)((f1 - 1) / k) / kSelTokens + 1 : 0;
+  for (int e = wave; e < E; e += kPlaceSlots / 64) {
+    const int32_t* h = block_hist + (size_t)e * nb;
+    // lane sums of the blocks before sb0 and of all blocks; lanes 0 .. sb1 - sb0 - 1
+    // also hold block sb0 + lane for the bases within [sb0, sb1)
+    int pre = 0, all = 0;
+    int b = lane;
+    for (; b + 192 < nb; b += 256) {
+      const int v0 = h[b], v1 = h[b + 64], v2 = h[b + 128], v3 = h[b + 192];
+      all += (v0 + v1) + (v2 + v3);
+      pre += (b < sb0 ? v0 : 0) + (b + 64 < sb0 ? v1 : 0) + (b + 128 < sb0 ? v2 : 0) + (b + 192 < sb0 ? v3 : 0);
+    }
+    for (; b < nb; b += 64) {
+      const int v = h[b];
+      all += v;
+      pre += b < sb0 ? v : 0;
+    }
+    const int mine = (lane < sb1 - sb0) ? h[sb0 + lane] : 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
+    for (int o = 32; o > 0; o >>= 1) {
+      pre += __shfl_xor(pre, o);
+      all += __shfl_xor(all, o);
+    }
+    int incl = mine;  // prefix over the blocks sb0 .. sb0 + lane
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
       const int v = __shfl_up(incl, o);
       if (lane >= o) incl += v;
     }
-    if (lane == 63) tot[x] = incl;
-    int run = incl - sum;
-#pragma unroll 8
-    for (int b = b0; b < b1; ++b) {
-      const int v = h[b];
-      h[b] = run;
-      run += v;
-    }
+    if (lane < sb1 - sb0) s_base[e][lane] = pre + incl - mine;
+    if (lane == 0) s_tot[e] = all;
   }
   __syncthreads();
-  if (wave == 0) {
-    const int c = lane < E ? tot[lane] : 0;
+  if (wave == 0) {  // exclusive scan of the expert totals
+    const int c = lane < E ? s_tot[lane] : 0;
     int incl = c;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int v = __shfl_up(incl, o);
       if (lane >= o) incl += v;
     }
-    if (lane < E) {
-      counts[lane] = c;
-      offsets[lane] = incl - c;
+    if (lane < E) s_off[lane] = incl - c;
+    if (blockIdx.x == 0) {
+      if (lane < E) {
+        counts[lane] = c;
+        offsets[lane] = incl - c;
+      }
+      if (lane == E - 1) offsets[E] = incl;
     }
-    if (lane == E - 1) offsets[E] = incl;
   }
-}
-
-__global__ __launch_bounds__(256) void route_place(const int32_t* __restrict__ topk_idx,
-                                                   const int32_t* __restrict__ block_base,
-                                                   const int32_t* __restrict__ offsets, int N, int nblocks, int k,
-                                                   int32_t* __restrict__ perm, int32_t* __restrict__ slot_pos) {
-  const size_t f = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (f >= (size_t)N * k) return;
-  const int t = (int)(f / k);
-  const int e = topk_idx[f];
-  const int pos = offsets[e] + block_base[(size_t)e * nblocks + t / kSelTokens] + slot_pos[f];
-  slot_pos[f] = pos;
-  perm[pos] = t;
+  __syncthreads();
+  if (has_slot) {
+    const int t = (int)(f / k);
+    const int pos = s_off[my_e] + s_base[my_e][t / kSelTokens - sb0] + my_rank;
+    slot_pos[f] = pos;
+    perm[pos] = t;
+  }
 }
 
 // Small token counts (decode): the three steps above in one workgroup of
@@ -339,7 +364,7 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   const int nb = (N + kSelTokens - 1) / kSelTokens;
   int32_t* block_hist = static_cast<int32_t*>(workspace);
   if (nb > 0) {
-    // slot ranks go to slot_pos; route_place turns them into rows
+    // slot ranks go to slot_pos; route_scan_place turns them into rows
     switch ((E + 7) / 8) {
 #define YGG_SEL(Q)                                                                                            \
   case Q:                                                                                                     \
@@ -350,15 +375,11 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
     }
     if (check_launch("route_select")) return -1;
   }
-  route_scan<<<1, kScanMaxThreads, 0, stream>>>(block_hist, nb, E, counts, offsets);
-  if (check_launch("route_scan")) return -1;
-  if (nb > 0) {
-    const size_t slots = (size_t)N * k;
-    route_place<<<(unsigned)((slots + 255) / 256), 256, 0, stream>>>(topk_idx, block_hist, offsets, N, nb, k, perm,
-                                                                     slot_pos);
-    if (check_launch("route_place")) return -1;
-  }
-  return 0;
+  const size_t slots = (size_t)N * k;
+  const unsigned place_blocks = slots ? (unsigned)((slots + kPlaceSlots - 1) / kPlaceSlots) : 1u;  // N = 0: counts 0
+  route_scan_place<<<place_blocks, kPlaceSlots, 0, stream>>>(topk_idx, block_hist, N, nb, E, k, perm, slot_pos, counts,
+                                                             offsets);
+  return check_launch("route_scan_place");
 }
 
 // The CliffordLinear(d -> E) head's scalar part (the router of the TinyHLMMoE-style
