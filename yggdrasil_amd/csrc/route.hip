@@ -110,36 +110,38 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
   // the K1 blocks [sb0, sb1) holding this workgroup's tokens (at most kPlaceMaxSel)
   const int sb0 = f0 < slots ? (int)(f0 / k) / kSelTokens : 0;
   const int sb1 = f0 < slots ? (int)((f1 - 1) / k) / kSelTokens + 1 : 0;
-  for (int e = wave; e < E; e += kPlaceSlots / 64) {
-    const int32_t* h = block_hist + (size_t)e * nb;
-    // lane sums of the blocks before sb0 and of all blocks; lanes 0 .. sb1 - sb0 - 1
-    // also hold block sb0 + lane for the bases within [sb0, sb1)
-    int pre = 0, all = 0;
-    int b = lane;
-    for (; b + 192 < nb; b += 256) {
-      const int v0 = h[b], v1 = h[b + 64], v2 = h[b + 128], v3 = h[b + 192];
-      all += (v0 + v1) + (v2 + v3);
-      pre += (b < sb0 ? v0 : 0) + (b + 64 < sb0 ? v1 : 0) + (b + 128 < sb0 ? v2 : 0) + (b + 192 < sb0 ? v3 : 0);
-    }
-    for (; b < nb; b += 64) {
+  // Thread (e, part) sums part `part` of expert e's block counts: `parts` threads per
+  // expert (a power of two, so a group is aligned within a wave), every expert at once.
+  int parts = 1;
+  while (parts < 64 && parts * 2 * E <= kPlaceSlots) parts *= 2;
+  const int e_me = tid / parts, part = tid % parts;
+  int pre = 0, all = 0;  // sums of the blocks before sb0, and of every block
+  if (e_me < E) {
+    const int32_t* h = block_hist + (size_t)e_me * nb;
+    const int per = (nb + parts - 1) / parts;
+    const int b0 = part * per, b1 = min(nb, b0 + per);
+#pragma unroll 8
+    for (int b = b0; b < b1; ++b) {
       const int v = h[b];
       all += v;
       pre += b < sb0 ? v : 0;
     }
-    const int mine = (lane < sb1 - sb0) ? h[sb0 + lane] : 0;
+  }
+  for (int o = parts / 2; o > 0; o >>= 1) {
+    pre += __shfl_xor(pre, o);
+    all += __shfl_xor(all, o);
+  }
+  if (e_me < E && part == 0) {
+    const int32_t* h = block_hist + (size_t)e_me * nb;
+    s_tot[e_me] = all;
+    int run = pre;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      pre += __shfl_xor(pre, o);
-      all += __shfl_xor(all, o);
+    for (int q = 0; q < kPlaceMaxSel; ++q) {
+      if (sb0 + q < sb1) {
+        s_base[e_me][q] = run;
+        run += h[sb0 + q];
+      }
     }
-    int incl = mine;  // prefix over the blocks sb0 .. sb0 + lane
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const int v = __shfl_up(incl, o);
-      if (lane >= o) incl += v;
-    }
-    if (lane < sb1 - sb0) s_base[e][lane] = pre + incl - mine;
-    if (lane == 0) s_tot[e] = all;
   }
   __syncthreads();
   if (wave == 0) {  // exclusive scan of the expert totals
