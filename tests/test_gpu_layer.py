@@ -187,6 +187,13 @@ def test_full_c3_prefill_bf16_sampled(fmt):
     _sampled_layer_check(8192, 128, 512, 32, 4, fmt, logits, 33)
 
 
+def test_full_layer_max_experts_and_top_k_sampled():
+    """E = 64 and k = 8 (the maxima) through the multi-block routing (N > 1024) and the Pauli products."""
+    g = np.random.default_rng(707)
+    logits = g.standard_normal((2048, 64), dtype=np.float32)
+    _sampled_layer_check(2048, 32, 64, 64, 8, "pauli", logits, 77)
+
+
 def test_full_c4_decode_int8_sampled():
     g = np.random.default_rng(404)
     logits = g.standard_normal((64, 32), dtype=np.float32)
