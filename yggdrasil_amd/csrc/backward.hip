@@ -75,7 +75,7 @@ __device__ inline void gate_backward(const float* c, const float* g, float* out)
 // out may alias g (each thread reads its multivector before writing it)
 template <int ACT>
 __global__ __launch_bounds__(256) void act_backward_kernel(const float* __restrict__ h, const float* g, size_t n_mv,
-                                                           float* out) {
+                                                           float* out, float* __restrict__ out_pauli) {
   const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= n_mv) return;
   float x[8], gr[8], o[8];
@@ -101,34 +101,42 @@ __global__ __launch_bounds__(256) void act_backward_kernel(const float* __restri
     const float t = tanhf(x[7]);
     o[7] = gr[7] * (1.0f - t * t);
   }
-  float4* op = reinterpret_cast<float4*>(out + n * 8);
-  op[0] = make_float4(o[0], o[1], o[2], o[3]);
-  op[1] = make_float4(o[4], o[5], o[6], o[7]);
+  if (out != nullptr) {  // may be g itself
+    float4* op = reinterpret_cast<float4*>(out + n * 8);
+    op[0] = make_float4(o[0], o[1], o[2], o[3]);
+    op[1] = make_float4(o[4], o[5], o[6], o[7]);
+  }
+  if (out_pauli != nullptr) store_pauli_f32(out_pauli + n * 8, o);
 }
 
 // The forward activation of blade-order rows (the same activate_blade the fused
 // epilogues apply), for the backward's recompute of h from h before the activation.
 template <int ACT>
 __global__ __launch_bounds__(256) void act_forward_kernel(const float* __restrict__ h, size_t n_mv,
-                                                          float* __restrict__ out) {
+                                                          float* __restrict__ out, float* __restrict__ out_pauli) {
   const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= n_mv) return;
   const float4* hp = reinterpret_cast<const float4*>(h + n * 8);
   const float4 h0 = hp[0], h1 = hp[1];
   float y[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
   activate_blade<ACT>(y);
-  float4* op = reinterpret_cast<float4*>(out + n * 8);
-  op[0] = make_float4(y[0], y[1], y[2], y[3]);
-  op[1] = make_float4(y[4], y[5], y[6], y[7]);
+  if (out != nullptr) {
+    float4* op = reinterpret_cast<float4*>(out + n * 8);
+    op[0] = make_float4(y[0], y[1], y[2], y[3]);
+    op[1] = make_float4(y[4], y[5], y[6], y[7]);
+  }
+  if (out_pauli != nullptr) store_pauli_f32(out_pauli + n * 8, y);
 }
 
 // ---- combine backward: dy[slot] = w dout_t; dw[t, s] = <dout_t, y[slot]> ----------
-// One wave per token.
+// One wave per token, a multivector per lane; dy goes out in blade order and/or as
+// fp32 Pauli rows (whichever is not NULL).
 __global__ __launch_bounds__(256) void combine_backward_kernel(const float* __restrict__ dout,
                                                                const float* __restrict__ y_sorted, int N, int k,
                                                                int d, const float* __restrict__ topk_w,
                                                                const int32_t* __restrict__ slot_pos,
                                                                float* __restrict__ dy_sorted,
+                                                               float* __restrict__ dy_pauli,
                                                                float* __restrict__ dtopk_w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -138,10 +146,26 @@ __global__ __launch_bounds__(256) void combine_backward_kernel(const float* __re
     const size_t row = (size_t)slot_pos[(size_t)t * k + s];
     const float w = topk_w[(size_t)t * k + s];
     float acc = 0.f;
-    for (int u = lane; u < d * 8; u += 64) {
-      const float gv = go[u];
-      dy_sorted[row * d * 8 + u] = w * gv;
-      if (y_sorted) acc += gv * y_sorted[row * d * 8 + u];
+    for (int i = lane; i < d; i += 64) {
+      const float4* gp = reinterpret_cast<const float4*>(go + (size_t)i * 8);
+      const float4 g0 = gp[0], g1 = gp[1];
+      const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[c] = w * gv[c];
+      const size_t mv = row * d + i;
+      if (dy_sorted) {
+        float4* q = reinterpret_cast<float4*>(dy_sorted + mv * 8);
+        q[0] = make_float4(o[0], o[1], o[2], o[3]);
+        q[1] = make_float4(o[4], o[5], o[6], o[7]);
+      }
+      if (dy_pauli) store_pauli_f32(dy_pauli + mv * 8, o);
+      if (y_sorted) {
+        const float4* yp = reinterpret_cast<const float4*>(y_sorted + mv * 8);
+        const float4 y0 = yp[0], y1 = yp[1];
+        acc += gv[0] * y0.x + gv[1] * y0.y + gv[2] * y0.z + gv[3] * y0.w + gv[4] * y1.x + gv[5] * y1.y +
+               gv[6] * y1.z + gv[7] * y1.w;
+      }
     }
     if (dtopk_w) {
 #pragma unroll
@@ -529,35 +553,40 @@ int weight_grad_pauli(const float* dy_pauli, const float* a_pauli, const int32_t
   return check_launch("weight gradient (reduction)");
 }
 
-int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream) {
+int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, float* out_pauli,
+                        hipStream_t stream) {
   if (n_mv == 0) return 0;
   const dim3 grid((unsigned)((n_mv + 255) / 256));
+#define YGG_AB(A) hipLaunchKernelGGL(act_backward_kernel<A>, grid, dim3(256), 0, stream, h, g, n_mv, out, out_pauli)
   switch (act) {
-    case kActNone: hipLaunchKernelGGL(act_backward_kernel<kActNone>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
-    case kActGelu: hipLaunchKernelGGL(act_backward_kernel<kActGelu>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
-    case kActRelu: hipLaunchKernelGGL(act_backward_kernel<kActRelu>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
-    default: hipLaunchKernelGGL(act_backward_kernel<kActSigmoid>, grid, dim3(256), 0, stream, h, g, n_mv, out); break;
+    case kActNone: YGG_AB(kActNone); break;
+    case kActGelu: YGG_AB(kActGelu); break;
+    case kActRelu: YGG_AB(kActRelu); break;
+    default: YGG_AB(kActSigmoid); break;
   }
+#undef YGG_AB
   return check_launch("activation backward");
 }
 
-int activation_forward(const float* h, size_t n_mv, int act, float* out, hipStream_t stream) {
+int activation_forward(const float* h, size_t n_mv, int act, float* out, float* out_pauli, hipStream_t stream) {
   if (n_mv == 0) return 0;
   const dim3 grid((unsigned)((n_mv + 255) / 256));
+#define YGG_AF(A) hipLaunchKernelGGL(act_forward_kernel<A>, grid, dim3(256), 0, stream, h, n_mv, out, out_pauli)
   switch (act) {
-    case kActNone: hipLaunchKernelGGL(act_forward_kernel<kActNone>, grid, dim3(256), 0, stream, h, n_mv, out); break;
-    case kActGelu: hipLaunchKernelGGL(act_forward_kernel<kActGelu>, grid, dim3(256), 0, stream, h, n_mv, out); break;
-    case kActRelu: hipLaunchKernelGGL(act_forward_kernel<kActRelu>, grid, dim3(256), 0, stream, h, n_mv, out); break;
-    default: hipLaunchKernelGGL(act_forward_kernel<kActSigmoid>, grid, dim3(256), 0, stream, h, n_mv, out); break;
+    case kActNone: YGG_AF(kActNone); break;
+    case kActGelu: YGG_AF(kActGelu); break;
+    case kActRelu: YGG_AF(kActRelu); break;
+    default: YGG_AF(kActSigmoid); break;
   }
+#undef YGG_AF
   return check_launch("activation forward");
 }
 
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
-                     const int32_t* slot_pos, float* dy_sorted, float* dtopk_w, hipStream_t stream) {
+                     const int32_t* slot_pos, float* dy_sorted, float* dy_pauli, float* dtopk_w, hipStream_t stream) {
   if (N == 0) return 0;
   hipLaunchKernelGGL(combine_backward_kernel, dim3((N + 3) / 4), dim3(256), 0, stream, dout, y_sorted, N, k, d, topk_w,
-                     slot_pos, dy_sorted, dtopk_w);
+                     slot_pos, dy_sorted, dy_pauli, dtopk_w);
   return check_launch("combine backward");
 }
 
@@ -616,5 +645,5 @@ YGG_API int ygg_activation_backward(const float* h, const float* grad_out, size_
                                     hipStream_t stream) {
   YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_activation_backward: activation %d", act);
   YGG_CHECK_ARG(n_mv == 0 || (h && grad_out && grad_in), "ygg_activation_backward: null pointer argument");
-  return activation_backward(h, grad_out, n_mv, act, grad_in, stream);
+  return activation_backward(h, grad_out, n_mv, act, grad_in, nullptr, stream);
 }

@@ -320,7 +320,7 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
                               rws, rws_bytes, stream)) {
     return -1;
   }
-  // forward recompute: h_pre (unless the forward kept it), h (blade), y (blade)
+  // forward recompute: h_pre (unless the forward kept it), h (Pauli rows), y (blade, for dtopk_w)
   const float* hp_in = h_pre_saved;
   // the MFMA weight gradient pays off with enough rows per expert; below that the
   // vector-ALU kernel, which spreads a tile's pairs over more waves, is faster
@@ -331,22 +331,22 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
       return -1;
     hp_in = h_pre;
   }
-  if (activation_forward(hp_in, P * F, act, h, stream)) return -1;
-  if (ygg_pauli_rows_from_blade_f32(h, (int)P, F, fp, stream)) return -1;
+  // h as Pauli rows for the down product (and in blade order for the vector-ALU weight gradient)
+  if (activation_forward(hp_in, P * F, act, wg_mfma ? nullptr : h, fp, stream)) return -1;
   if (dtopk_w &&
       ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, y, 1, stream))
     return -1;
   // combine backward -> dy; down backward -> dh, dW_down, db_down
-  if (combine_backward(dout, dtopk_w ? y : nullptr, N, k, d, tw, slot_pos, dy, dtopk_w, stream)) return -1;
-  if (ygg_pauli_rows_from_blade_f32(dy, (int)P, d, dp, stream)) return -1;
+  if (combine_backward(dout, dtopk_w ? y : nullptr, N, k, d, tw, slot_pos, wg_mfma ? nullptr : dy, dp, dtopk_w,
+                       stream))
+    return -1;
   if (ygg_pauli_grouped_linear_f32(dp, nullptr, (int)P, w_down_adj, nullptr, offsets, E, d, F, kActNone, dh, 1, stream))
     return -1;
   if (wg_mfma ? weight_grad_pauli(dp, fp, nullptr, offsets, (int)P, E, F, d, dw_down, db_down, wg, stream)
               : grouped_weight_grad(dy, h, nullptr, offsets, E, F, d, dw_down, db_down, stream))
     return -1;
-  // activation backward (in place), up backward -> dx rows, dW_up, db_up
-  if (activation_backward(hp_in, dh, P * F, act, dh, stream)) return -1;
-  if (ygg_pauli_rows_from_blade_f32(dh, (int)P, F, fp, stream)) return -1;
+  // activation backward -> Pauli rows of dh before the activation; up backward -> dx rows, dW_up, db_up
+  if (activation_backward(hp_in, dh, P * F, act, wg_mfma ? nullptr : dh, fp, stream)) return -1;
   if (ygg_pauli_grouped_linear_f32(fp, nullptr, (int)P, w_up_adj, nullptr, offsets, E, F, d, kActNone, y, 1, stream))
     return -1;
   if (wg_mfma ? weight_grad_pauli(fp, xp, perm, offsets, (int)P, E, d, F, dw_up, db_up, wg, stream)

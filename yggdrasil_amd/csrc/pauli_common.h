@@ -94,6 +94,16 @@ __device__ inline void pauli_to_blade(float y00r, float y00i, float y01r, float 
   x[2] = y10i - y01i;  // v2
 }
 
+// blade -> one fp32 Pauli row multivector ([b][re, im][c], 8 floats; the layout of
+// pauli_f32.hip) at dst
+__device__ inline void store_pauli_f32(float* dst, const float* x) {
+  float c0[4], c1[4];
+  blade_to_pauli(x, c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
+  float4* q = reinterpret_cast<float4*>(dst);
+  q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+  q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+}
+
 // two floats -> packed bf16 pair (v_cvt_pk_bf16_f32, round to nearest even)
 __device__ inline uint32_t pack2_bf16(float lo, float hi) {
   const pf32x2_t f = {lo, hi};

@@ -165,10 +165,12 @@ size_t weight_grad_pauli_workspace_bytes(int P_max, int E, int d_in, int d_out);
 int weight_grad_pauli(const float* dy_pauli, const float* a_pauli, const int32_t* gather, const int32_t* offsets,
                       int P_max, int E, int d_in, int d_out, float* dW, float* db, void* workspace,
                       hipStream_t stream);
-int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, hipStream_t stream);
-int activation_forward(const float* h, size_t n_mv, int act, float* out, hipStream_t stream);
+// (out may alias g; out and out_pauli -- fp32 Pauli rows -- are each optional)
+int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, float* out_pauli,
+                        hipStream_t stream);
+int activation_forward(const float* h, size_t n_mv, int act, float* out, float* out_pauli, hipStream_t stream);
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
-                     const int32_t* slot_pos, float* dy_sorted, float* dtopk_w, hipStream_t stream);
+                     const int32_t* slot_pos, float* dy_sorted, float* dy_pauli, float* dtopk_w, hipStream_t stream);
 int dispatch_backward(const float* dxs, int N, int k, int d, const int32_t* slot_pos, const float* residual_grad,
                       float* dx, hipStream_t stream);
 
