@@ -23,16 +23,16 @@
 //
 // Work decomposition
 // ------------------
-// A workgroup of 4 waves owns a tile of 16 tokens (32 GEMM rows) of one
-// expert x 32 output multivectors; the waves split the contraction and add
-// their four 32x32 accumulators (a = 0, 1 x re, im) in LDS in wave order.
-// The column tiles of a row tile run back to back on one XCD, so the row tile's
-// activations come from HBM once.  blockIdx.z optionally splits the
-// contraction further across workgroups into fp32 partial planes (no
-// activation), which the consumer adds in split order.  Deterministic
-// throughout.  (Wider tiles -- 32 tokens x 64 columns, each wave a quadrant
-// over the whole contraction, no cross-wave sum -- were measured 40-80 % slower
-// at the C3 shape.)
+// A workgroup of 4 waves owns a tile of 16 tokens (32 GEMM rows) of one expert
+// x 32 output multivectors -- 32 tokens, two row blocks per wave, for long
+// contractions -- and the waves split the contraction and add their 32x32
+// accumulators (a = 0, 1 x re, im) in LDS in a fixed order.  The column tiles
+// of a row tile run back to back on one XCD, so the row tile's activations come
+// from HBM once.  blockIdx.z optionally splits the contraction further across
+// workgroups into fp32 partial planes (no activation), which the consumer adds
+// in split order.  Deterministic throughout.  (Wider tiles -- 32 tokens x 64
+// columns, each wave a quadrant over the whole contraction, no cross-wave sum --
+// were measured 40-80 % slower at the C3 shape.)
 
 #include <algorithm>
 
@@ -46,6 +46,7 @@ constexpr int kF32Waves = 4;
 constexpr int kF32Tok = 16;  // tokens per tile (32 GEMM rows)
 constexpr int kF32Cols = 32;  // output multivectors per tile
 constexpr int kF32U = 4;      // input multivectors per register-buffered block of the K loop
+constexpr long long kF32TwoBlockMinGroups = 2048;  // 32-token tiles from this many workgroups (8 per CU)
 
 enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2 };
 
@@ -69,62 +70,78 @@ __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E,
   return false;
 }
 
-// The contraction over inputs [i0, i1) of one wave's 32 GEMM rows x 32 columns:
-// operands of input i are x (re, im) of the lane's GEMM row (arow + 8 i) and the
-// eight weight floats of its column (wrow + i w_step).  Blocks of kF32U inputs are
-// double buffered in registers, so one block's loads are in flight while the
-// previous block's MFMAs run.  i0, i1 must be wave-uniform.
-__device__ inline void f32_kloop(f32x16v_t (&acc)[2][2], const float* __restrict__ arow,
+// The contraction over inputs [i0, i1) of one wave's WR blocks of 32 GEMM rows x 32
+// columns: operands of input i are x (re, im) of the lane's GEMM row in block r
+// (arow[r] + 8 i) and the eight weight floats of its column (wrow + i w_step), which
+// every row block shares.  Blocks of U inputs are double buffered in registers, so
+// one block's loads are in flight while the previous block's MFMAs run.  i0, i1
+// must be wave-uniform.
+template <int WR>
+__device__ inline void f32_kloop(f32x16v_t (&acc)[WR][2][2], const float* const (&arow)[WR],
                                  const float* __restrict__ wrow, size_t w_step, int i0, int i1) {
-  auto load_op = [&](int i, float2& xa, float4& w0, float4& w1) {
-    xa = *reinterpret_cast<const float2*>(arow + (size_t)i * 8);
-    w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
-    w1 = *reinterpret_cast<const float4*>(wrow + i * w_step + 4);  // c = 1
+  constexpr int U = WR == 1 ? kF32U : kF32U / 2;
+  struct Ops {
+    float2 xa[WR];
+    float4 w0, w1;
   };
-  auto mma = [&](const float2& xa, const float4& w0, const float4& w1) {
-    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.x, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.y, acc[0][1], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.z, acc[1][0], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.x, w0.w, acc[1][1], 0, 0, 0);
-    acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.x, acc[0][0], 0, 0, 0);
-    acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.y, acc[0][1], 0, 0, 0);
-    acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.z, acc[1][0], 0, 0, 0);
-    acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa.y, w1.w, acc[1][1], 0, 0, 0);
+  auto load_op = [&](int i, Ops& o) {
+#pragma unroll
+    for (int r = 0; r < WR; ++r) o.xa[r] = *reinterpret_cast<const float2*>(arow[r] + (size_t)i * 8);
+    o.w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
+    o.w1 = *reinterpret_cast<const float4*>(wrow + i * w_step + 4);  // c = 1
+  };
+  auto mma = [&](const Ops& o) {
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      f32x16v_t(&a)[2][2] = acc[r];
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.w, a[1][1], 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      f32x16v_t(&a)[2][2] = acc[r];
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.w, a[1][1], 0, 0, 0);
+    }
   };
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int r = 0; r < WR; ++r)
 #pragma unroll
-    for (int q = 0; q < 2; ++q)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[a][q][v] = 0.f;
-  const int nblk = max(i1 - i0, 0) / kF32U;
-  float2 xa0[kF32U], xa1[kF32U];
-  float4 wa0[kF32U], wb0[kF32U], wa1[kF32U], wb1[kF32U];
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[r][a][q][v] = 0.f;
+  const int nblk = max(i1 - i0, 0) / U;
+  Ops b0[U], b1[U];
   if (nblk > 0) {
 #pragma unroll
-    for (int u = 0; u < kF32U; ++u) load_op(i0 + u, xa0[u], wa0[u], wb0[u]);
+    for (int u = 0; u < U; ++u) load_op(i0 + u, b0[u]);
   }
   for (int b = 0; b < nblk; b += 2) {  // buffer 0 holds block b, buffer 1 block b + 1
     if (b + 1 < nblk) {
 #pragma unroll
-      for (int u = 0; u < kF32U; ++u) load_op(i0 + (b + 1) * kF32U + u, xa1[u], wa1[u], wb1[u]);
+      for (int u = 0; u < U; ++u) load_op(i0 + (b + 1) * U + u, b1[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kF32U; ++u) mma(xa0[u], wa0[u], wb0[u]);
+    for (int u = 0; u < U; ++u) mma(b0[u]);
     if (b + 1 < nblk) {
       if (b + 2 < nblk) {
 #pragma unroll
-        for (int u = 0; u < kF32U; ++u) load_op(i0 + (b + 2) * kF32U + u, xa0[u], wa0[u], wb0[u]);
+        for (int u = 0; u < U; ++u) load_op(i0 + (b + 2) * U + u, b0[u]);
       }
 #pragma unroll
-      for (int u = 0; u < kF32U; ++u) mma(xa1[u], wa1[u], wb1[u]);
+      for (int u = 0; u < U; ++u) mma(b1[u]);
     }
   }
-  for (int i = i0 + nblk * kF32U; i < i1; ++i) {
-    float2 xa;
-    float4 w0, w1;
-    load_op(i, xa, w0, w1);
-    mma(xa, w0, w1);
+  for (int i = i0 + nblk * U; i < i1; ++i) {
+    Ops o;
+    load_op(i, o);
+    mma(o);
   }
 }
 
@@ -163,12 +180,16 @@ __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y0
   }
 }
 
-template <int ACT, int OUT>
-__global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
+template <int ACT, int OUT, int WR>  // WR row blocks of 16 tokens per wave
+__global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(2))) void pauli_f32_kernel(
     const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
     float* __restrict__ Y, float* __restrict__ Ypre, int n_xcd) {
-  __shared__ float4 part[kF32Waves][2 * kF32Tok][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
+  constexpr int TOK = kF32Tok * WR;  // tokens per tile
+  // the waves' partial sums: one round for WR = 1; for WR = 2 waves 2, 3 hand theirs
+  // to waves 0, 1 first, so the buffer holds two waves' tiles
+  constexpr int PW = WR == 1 ? kF32Waves : 2;
+  __shared__ float4 part[PW][2 * TOK][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
   int e, row0, row_end;
   // The column tiles of one row tile run on one XCD, one after the other in
   // dispatch order, so its rows are read once into that XCD's L2: workgroup b runs
@@ -177,18 +198,22 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
   const int n_ct = (d_out + kF32Cols - 1) / kF32Cols;
   const int xcd = blockIdx.x % n_xcd, q = blockIdx.x / n_xcd;
   const int ct = q % n_ct, rt = (q / n_ct) * n_xcd + xcd;
-  if (!f32_find_tile<kF32Tok>(offsets, E, rt, e, row0, row_end)) return;
+  if (!f32_find_tile<TOK>(offsets, E, rt, e, row0, row_end)) return;
   const int col0 = ct * kF32Cols;
   const int split = blockIdx.z, splits = gridDim.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the K loop runs on scalars
   const int l32 = lane & 31, k = lane >> 5;
 
-  // A operand: GEMM row (t, b) = l32, real (k = 0) or imaginary (k = 1) part
-  int m = row0 + (l32 >> 1);
-  m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
-  const int src = gather ? gather[m] : m;
-  const float* arow = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
+  // A operand: GEMM row (t, b) = l32 of row block r, real (k = 0) or imaginary (k = 1) part
+  const float* arow[WR];
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    int m = row0 + r * kF32Tok + (l32 >> 1);
+    m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
+    const int src = gather ? gather[m] : m;
+    arow[r] = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
+  }
   // B operand: output column j (clamped: columns past d_out are not stored)
   const int jc = min(col0 + l32, d_out - 1);
   const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
@@ -198,24 +223,52 @@ __global__ __launch_bounds__(64 * kF32Waves) void pauli_f32_kernel(
   const int per_wave = (max(is1 - is0, 0) + kF32Waves - 1) / kF32Waves;
   const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
 
-  f32x16v_t acc[2][2];
-  f32_kloop(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1);
-  // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4
+  f32x16v_t acc[WR][2][2];
+  f32_kloop<WR>(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1);
+  // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4 of each row block
+  if constexpr (WR == 2) {
+    if (wave >= 2) {
 #pragma unroll
-  for (int v = 0; v < 16; ++v)
-    part[wave][8 * (v >> 2) + 4 * k + (v & 3)][l32] =
-        make_float4(acc[0][0][v], acc[0][1][v], acc[1][0][v], acc[1][1][v]);
+      for (int r = 0; r < WR; ++r)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          part[wave - 2][r * 32 + 8 * (v >> 2) + 4 * k + (v & 3)][l32] =
+              make_float4(acc[r][0][0][v], acc[r][0][1][v], acc[r][1][0][v], acc[r][1][1][v]);
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+      for (int r = 0; r < WR; ++r)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float4 o = part[wave][r * 32 + 8 * (v >> 2) + 4 * k + (v & 3)][l32];
+          acc[r][0][0][v] += o.x;
+          acc[r][0][1][v] += o.y;
+          acc[r][1][0][v] += o.z;
+          acc[r][1][1][v] += o.w;
+        }
+    }
+    __syncthreads();
+  }
+  if (WR == 1 || wave < 2) {
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        part[wave][r * 32 + 8 * (v >> 2) + 4 * k + (v & 3)][l32] =
+            make_float4(acc[r][0][0][v], acc[r][0][1][v], acc[r][1][0][v], acc[r][1][1][v]);
+  }
   __syncthreads();
 
 #pragma unroll
-  for (int h = 0; h < (kF32Tok * kF32Cols) / (64 * kF32Waves); ++h) {
+  for (int h = 0; h < (TOK * kF32Cols) / (64 * kF32Waves); ++h) {
     const int o = tid + h * 64 * kF32Waves;
     const int t = o / kF32Cols, jj = o % kF32Cols;
     const int row = row0 + t, j = col0 + jj;
     if (row >= row_end || j >= d_out) continue;
     float4 s0 = part[0][2 * t][jj], s1 = part[0][2 * t + 1][jj];  // b = 0, 1
 #pragma unroll
-    for (int w = 1; w < kF32Waves; ++w) {
+    for (int w = 1; w < PW; ++w) {
       const float4 p0 = part[w][2 * t][jj], p1 = part[w][2 * t + 1][jj];
       s0.x += p0.x; s0.y += p0.y; s0.z += p0.z; s0.w += p0.w;
       s1.x += p1.x; s1.y += p1.y; s1.z += p1.z; s1.w += p1.w;
@@ -290,21 +343,31 @@ int f32_xcds() {  // XCDs that workgroups are dealt to round robin (8 on MI355X)
 
 // x: (row tile, column tile) pairs, row tiles rounded up to a multiple of the XCD
 // count; z: contraction splits
-dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd) {
-  long long rts = ((long long)P_max + kF32Tok - 1) / kF32Tok + E;
+dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd, int tok) {
+  long long rts = ((long long)P_max + tok - 1) / tok + E;
   rts = (rts + n_xcd - 1) / n_xcd * n_xcd;
   return dim3((unsigned)(rts * ((d_out + kF32Cols - 1) / kF32Cols)), 1, splits);
 }
 
+// 32-token tiles (two row blocks per wave, sharing the weight loads) for long
+// contractions (d_in >= 2 d_out, where a tile's weight stream dominates) when there
+// are enough of them to fill the chip; 16-token tiles otherwise.  (At the C3 shape:
+// the d_in = 512 products 1.94 -> 1.59 ms, the d_in = 128 ones 1.39 -> 1.66 ms.)
 template <int OUT>
 int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const int32_t* gather, const float* W,
                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
                    float* Ypre = nullptr) {
   const int n_xcd = f32_xcds();
-  const dim3 grid = f32_grid(P_max, E, d_out, splits, n_xcd);
-#define YGG_F(A)                                                                                                  \
-  pauli_f32_kernel<A, OUT><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, P_max, Y, \
-                                                            Ypre, n_xcd)
+  const dim3 g2 = f32_grid(P_max, E, d_out, splits, n_xcd, 2 * kF32Tok);
+  const bool two = d_in >= 2 * d_out && (long long)g2.x * g2.z >= kF32TwoBlockMinGroups;
+  const dim3 grid = two ? g2 : f32_grid(P_max, E, d_out, splits, n_xcd, kF32Tok);
+#define YGG_F(A)                                                                                              \
+  if (two)                                                                                                    \
+    pauli_f32_kernel<A, OUT, 2><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
+                                                                 P_max, Y, Ypre, n_xcd);                      \
+  else                                                                                                        \
+    pauli_f32_kernel<A, OUT, 1><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
+                                                                 P_max, Y, Ypre, n_xcd)
   switch (act) {
     case kActNone: YGG_F(kActNone); break;
     case kActGelu: YGG_F(kActGelu); break;
