@@ -342,8 +342,9 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   };
 
   // ---- the stream of (tile, chunk) steps ------------------------------------
-  // chunk f lives in register set f % 2 and LDS buffer f % 2; step f loads
-  // chunk f + 2, computes chunk f, stores chunk f + 1, then one barrier.
+  // step f loads chunk f + 1 into registers, computes chunk f from LDS buffer
+  // f % 2, stores chunk f + 1 into the other buffer, then one barrier.  (Keeping
+  // two chunks in flight, in two register sets, measured no faster.)
   uint4 ra[A_PER], rw[W_PER];
   zero_acc();
   if (total > 0) {
