@@ -328,18 +328,19 @@ __global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const floa
 using namespace ygg;
 
 namespace {
-int f32_xcds() {  // XCDs that workgroups are dealt to round robin (8 on MI355X)
-  static thread_local int cached_dev = -1, cached = 1;
+int f32_cus() {  // CUs of the current device
+  static thread_local int cached_dev = -1, cached = 64;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   if (dev != cached_dev) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 64;
-    cached = (cus % 8 == 0) ? 8 : 1;
+    cached = cus;
     cached_dev = dev;
   }
   return cached;
 }
+int f32_xcds() { return (f32_cus() % 8 == 0) ? 8 : 1; }  // XCDs workgroups are dealt to round robin (8 on MI355X)
 
 // x: (row tile, column tile) pairs, row tiles rounded up to a multiple of the XCD
 // count; z: contraction splits
@@ -349,18 +350,25 @@ dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd, int tok) {
   return dim3((unsigned)(rts * ((d_out + kF32Cols - 1) / kF32Cols)), 1, splits);
 }
 
-// 32-token tiles (two row blocks per wave, sharing the weight loads) for long
-// contractions (d_in >= 2 d_out, where a tile's weight stream dominates) when there
-// are enough of them to fill the chip; 16-token tiles otherwise.  (At the C3 shape:
-// the d_in = 512 products 1.94 -> 1.59 ms, the d_in = 128 ones 1.39 -> 1.66 ms.)
+// 16- or 32-token tiles (32: two row blocks per wave, sharing the weight loads).
+// Small grids: 16 while every workgroup gets a CU of its own, 32 when that keeps
+// every workgroup on a CU of its own and 16 would put two on some (C1 step 65 ->
+// 53 us).  Large grids: 32 for long contractions (d_in >= 2 d_out, where a tile's
+// weight stream dominates: at the C3 shape the d_in = 512 products 1.94 -> 1.59 ms,
+// while the d_in = 128 ones go 1.39 -> 1.66 ms), 16 otherwise.
 template <int OUT>
 int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const int32_t* gather, const float* W,
                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
                    float* Ypre = nullptr) {
   const int n_xcd = f32_xcds();
+  const dim3 g1 = f32_grid(P_max, E, d_out, splits, n_xcd, kF32Tok);
   const dim3 g2 = f32_grid(P_max, E, d_out, splits, n_xcd, 2 * kF32Tok);
-  const bool two = d_in >= 2 * d_out && (long long)g2.x * g2.z >= kF32TwoBlockMinGroups;
-  const dim3 grid = two ? g2 : f32_grid(P_max, E, d_out, splits, n_xcd, kF32Tok);
+  const long long n1 = (long long)g1.x * g1.z, n2 = (long long)g2.x * g2.z, cus = f32_cus();
+  bool two;
+  if (n1 <= cus) two = false;        // one workgroup per CU already: the shorter chains win
+  else if (n2 <= cus) two = true;    // 32-token tiles fit in one workgroup per CU, 16-token ones would double up
+  else two = d_in >= 2 * d_out && n2 >= kF32TwoBlockMinGroups;
+  const dim3 grid = two ? g2 : g1;
 #define YGG_F(A)                                                                                              \
   if (two)                                                                                                    \
     pauli_f32_kernel<A, OUT, 2><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
