@@ -59,7 +59,9 @@ def test_pauli_rows_from_blade_f32_bit_exact():
     ("sigmoid", 9, 40, 5, 77, 60), ("gelu", 128, 512, 4, 700, 256), ("none", 256, 64, 2, 129, 64),
     ("gelu", 1, 33, 3, 17, 17),
     # enough tiles for the wide-tile kernel (32 tokens x 64 columns per workgroup)
-    ("gelu", 8, 1024, 3, 2000, 1500), ("none", 5, 1100, 2, 1900, 700)])
+    ("gelu", 8, 1024, 3, 2000, 1500), ("none", 5, 1100, 2, 1900, 700),
+    # 32-token tiles on a small grid (they keep one workgroup per CU), ragged d_in and d_out
+    ("relu", 9, 70, 7, 1500, 900)])
 def test_pauli_f32_product(act, d_in, d_out, E, P, N):
     ops = _ops()
     g = np.random.default_rng(d_in * 5 + d_out + E)
