@@ -270,3 +270,33 @@ def test_decode_routing_inside_up_product(N, d, F, E, k, act):
             e = idx[t, s]
             ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu_q[e], bu[e], wd_q[e], bd[e], act)[0]
     assert normwise_err(y, ref) < TOL_BF16
+
+
+@pytest.mark.parametrize("fmt,router", [("pauli_f32", "energy"), ("f32", "logits"), ("pauli", "logits"),
+                                        ("bf16", "clifford_head"), ("int8", "logits")])
+def test_layer_with_no_tokens(fmt, router):
+    """An empty batch (the reference's _moe_forward on zero tokens): an empty output, every
+    expert's count and offset zero; the fp32 Pauli layer's weight gradients are zero."""
+    yggdrasil_amd, _ = _mods()
+    g = np.random.default_rng(11)
+    d, F, E, k = 16, 32, 4, 2
+    dt = torch.float32 if fmt in ("f32", "pauli_f32") else torch.bfloat16
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, dtype=dt, weight_format=fmt,
+                                     router=router)
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F, bias_std=0.1)
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    x = torch.zeros((1, 0, d, 8), device="cuda", dtype=dt, requires_grad=fmt == "pauli_f32")
+    lg = torch.zeros((0, E), device="cuda") if router == "logits" else None
+    say(f"empty batch {fmt} {router}")
+    y = layer.moe_forward(x, logits=lg)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (1, 0, d, 8)
+    assert layer.last_routing["counts"].cpu().tolist() == [0] * E
+    assert layer.last_routing["offsets"].cpu().tolist() == [0] * (E + 1)
+    if fmt == "pauli_f32":
+        y.sum().backward()
+        torch.cuda.synchronize()
+        for name in ("w_up", "b_up", "w_down", "b_down"):
+            grad = getattr(layer, name).grad
+            assert grad is not None and not grad.any(), name

@@ -19,6 +19,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "pauli_common.h"
 #include "ygg_common.h"
 
@@ -580,6 +582,18 @@ int activation_forward(const float* h, size_t n_mv, int act, float* out, float* 
   }
 #undef YGG_AF
   return check_launch("activation forward");
+}
+
+// a kernel rather than hipMemsetAsync, so a captured graph replays it like the other launches
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0.f;
+}
+
+int fill_zero_f32(float* p, size_t n, hipStream_t stream) {
+  if (n == 0) return 0;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream, p, n);
+  return check_launch("zero fill");
 }
 
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,

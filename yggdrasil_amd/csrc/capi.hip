@@ -100,8 +100,11 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format),
                 "ygg_moe_forward: workspace of %zu bytes, need %zu", workspace_bytes,
                 ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format));
-  YGG_CHECK_ARG(logits || (router_w && router_b), "ygg_moe_forward: need logits or router parameters");
-  if (N == 0) return 0;
+  YGG_CHECK_ARG(N == 0 || logits || (router_w && router_b), "ygg_moe_forward: need logits or router parameters");
+  if (N == 0)  // no tokens: every expert's count and offset is zero, as ygg_route writes them
+    return (counts && offsets) ? ygg_route(nullptr, 0, E, k, nullptr, nullptr, counts, offsets, nullptr, nullptr,
+                                           nullptr, 0, stream)
+                               : 0;
   const size_t P = (size_t)N * k;
   const size_t es = (dtype == kF32) ? 4 : 2;
   char* p = static_cast<char*>(workspace);
@@ -226,8 +229,7 @@ YGG_API int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_block_ffn: dtype %d unsupported", dtype);
   const size_t need = ygg_moe_block_ffn_workspace_bytes(N, d, F, E, k, dtype, w_format);
   YGG_CHECK_ARG(workspace_bytes >= need, "ygg_moe_block_ffn: workspace of %zu bytes, need %zu", workspace_bytes, need);
-  YGG_CHECK_ARG(out != x, "ygg_moe_block_ffn: out must not alias x");
-  if (N == 0) return 0;
+  YGG_CHECK_ARG(N == 0 || out != x, "ygg_moe_block_ffn: out must not alias x");
   // x_norm = ffn_norm(x) at the front of the workspace; the MoE layer gets the
   // rest, and adds x back in its combine
   const size_t xn_bytes = align256((size_t)N * d * 8 * ((dtype == kF32) ? 4 : 2));
@@ -281,9 +283,15 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_backward_workspace_bytes(N, d, F, E, k),
                 "ygg_moe_backward: workspace of %zu bytes, need %zu", workspace_bytes,
                 ygg_moe_backward_workspace_bytes(N, d, F, E, k));
-  YGG_CHECK_ARG(logits || (router_w && router_b), "ygg_moe_backward: need logits or router parameters");
+  YGG_CHECK_ARG(N == 0 || logits || (router_w && router_b), "ygg_moe_backward: need logits or router parameters");
   YGG_CHECK_ARG(w_up && w_up_adj && w_down && w_down_adj && dw_up && dw_down, "ygg_moe_backward: null weights");
-  if (N == 0) return 0;
+  if (N == 0) {  // no tokens: the weight and bias gradients are zero
+    const size_t nw = (size_t)E * F * d * 8;
+    if (fill_zero_f32(dw_up, nw, stream) || fill_zero_f32(dw_down, nw, stream)) return -1;
+    if (db_up && fill_zero_f32(db_up, (size_t)E * F * 8, stream)) return -1;
+    if (db_down && fill_zero_f32(db_down, (size_t)E * d * 8, stream)) return -1;
+    return 0;
+  }
   YGG_CHECK_ARG(x && dout && dx, "ygg_moe_backward: null x, dout or dx");
   const size_t P = (size_t)N * k;
   size_t sz[24];

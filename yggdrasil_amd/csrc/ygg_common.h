@@ -169,6 +169,7 @@ int weight_grad_pauli(const float* dy_pauli, const float* a_pauli, const int32_t
 int activation_backward(const float* h, const float* g, size_t n_mv, int act, float* out, float* out_pauli,
                         hipStream_t stream);
 int activation_forward(const float* h, size_t n_mv, int act, float* out, float* out_pauli, hipStream_t stream);
+int fill_zero_f32(float* p, size_t n, hipStream_t stream);  // n floats at p set to zero
 int combine_backward(const float* dout, const float* y_sorted, int N, int k, int d, const float* topk_w,
                      const int32_t* slot_pos, float* dy_sorted, float* dy_pauli, float* dtopk_w, hipStream_t stream);
 int dispatch_backward(const float* dxs, int N, int k, int d, const int32_t* slot_pos, const float* residual_grad,
