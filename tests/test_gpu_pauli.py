@@ -135,6 +135,21 @@ def test_pauli_rows_roundtrip_exact_for_representable_values():
     assert np.array_equal(xp[:, 0], col0) and np.array_equal(xp[:, 1], col1)
 
 
+@pytest.mark.parametrize("rows,d", [(300, 130), (5, 2), (1, 128)])
+def test_pauli_rows_random_against_numpy(rows, d):
+    """Random bf16 rows: every Pauli coordinate is the fp32 pairwise sum rounded to nearest even bf16."""
+    ops = _ops()
+    g = np.random.default_rng(rows + d)
+    x = _inputs.bf16_round(g.standard_normal((rows, d, 8), dtype=np.float32))
+    say(f"pauli rows random rows={rows} d={d}")
+    xp = ops.pauli_rows_from_blade(torch.from_numpy(x).cuda().bfloat16()).float().cpu().numpy()
+    s, v1, v2, v3, b12, b13, b23, t = [x[..., i] for i in range(8)]
+    col0 = _inputs.bf16_round(np.stack([s + v3, t + b12, v1 + b13, b23 + v2], -1))
+    col1 = _inputs.bf16_round(np.stack([v1 - b13, b23 - v2, s - v3, t - b12], -1))
+    assert xp.shape == (rows, 2, d, 4)
+    assert np.array_equal(xp[:, 0], col0) and np.array_equal(xp[:, 1], col1)
+
+
 def test_pauli_small_integer_product_is_exact():
     """Integer operands whose Pauli coordinates and sums stay exact in bf16/fp32 give exact results."""
     ops = _ops()
