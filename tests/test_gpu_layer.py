@@ -187,6 +187,15 @@ def test_full_c3_prefill_bf16_sampled(fmt):
     _sampled_layer_check(8192, 128, 512, 32, 4, fmt, logits, 33)
 
 
+def test_full_c5_layer_bf16_sampled():
+    """One layer of BASELINE config 5 at full size (N=4096, d=256, F=1024, E=64, k=2):
+    logits N(0,1) plus a per-expert bias N(0, 0.5), as the config draws them."""
+    g = np.random.default_rng(505)
+    logits = (g.standard_normal((4096, 64), dtype=np.float32)
+              + (0.5 * g.standard_normal(64)).astype(np.float32)[None, :])
+    _sampled_layer_check(4096, 256, 1024, 64, 2, "pauli", logits, 55, n_sample=8)
+
+
 def test_full_layer_max_experts_and_top_k_sampled():
     """E = 64 and k = 8 (the maxima) through the multi-block routing (N > 1024) and the Pauli products."""
     g = np.random.default_rng(707)
