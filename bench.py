@@ -553,7 +553,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU is design-only: "
-                                   "see DESIGN.md, 'How the path would shard')"}))
+                                   "tokens shard with no exchange, experts with one all-to-all each way)"}))
         sys.exit(2)
     import torch
 
