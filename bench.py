@@ -197,12 +197,12 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         h = torch.empty((N * k, 2, F, 4), device="cuda", dtype=x.dtype)
 
         def up():
-            ops.check(L.ygg_pauli_grouped_linear(xp.data_ptr(), 1, r.perm.data_ptr(), N * k,
+            ops.check(L.ygg_pauli_grouped_linear(xp.data_ptr(), 1, N, r.perm.data_ptr(), N * k,
                                                  P0["w_up"].data.data_ptr(), None, r.offsets.data_ptr(), E, d, F, 1,
                                                  h.data_ptr(), 0, dt_code, st))
 
         def down():
-            ops.check(L.ygg_pauli_grouped_linear(h.data_ptr(), 1, None, N * k, P0["w_down"].data.data_ptr(), None,
+            ops.check(L.ygg_pauli_grouped_linear(h.data_ptr(), 1, N * k, None, N * k, P0["w_down"].data.data_ptr(), None,
                                                  r.offsets.data_ptr(), E, F, d, 0, ys.data_ptr(), 1, dt_code, st))
     elif c["fmt"] == "pauli_f32":
         # as above in fp32 split rows; the layer's down product splits its contraction
@@ -298,9 +298,9 @@ def run_ep_config(torch, ops, name, c, steps, warmup):
 
     def step():
         ops.check(Lb.ygg_pauli_rows_from_blade(x_local.data_ptr(), P, d, xp.data_ptr(), st))
-        ops.check(Lb.ygg_pauli_grouped_linear(xp.data_ptr(), 1, None, P, pu.data.data_ptr(), None, offs.data_ptr(),
+        ops.check(Lb.ygg_pauli_grouped_linear(xp.data_ptr(), 1, P, None, P, pu.data.data_ptr(), None, offs.data_ptr(),
                                               per, d, F, 1, h.data_ptr(), 0, dt, st))
-        ops.check(Lb.ygg_pauli_grouped_linear(h.data_ptr(), 1, None, P, pd.data.data_ptr(), None, offs.data_ptr(),
+        ops.check(Lb.ygg_pauli_grouped_linear(h.data_ptr(), 1, P, None, P, pd.data.data_ptr(), None, offs.data_ptr(),
                                               per, F, d, 0, y.data_ptr(), 1, dt, st))
 
     ms = time_fn(torch, step, steps, warmup)

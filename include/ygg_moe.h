@@ -147,13 +147,17 @@ int ygg_grouped_clifford_linear(const void* x, int P_max, const void* w_prepared
  * x_layout 1: x holds "Pauli half-rows" (rows, 2, d_in, 4) bf16, the layout
  *   this call writes for y_layout 0 (see ygg_pauli_rows_from_blade); row r of
  *   the product reads x[gather[r]] (gather NULL: x[r]).
+ * x_rows: the rows x holds (N above, or `rows`); without a gather at least
+ *   P_max.  A gather index at or past x_rows reads a zero row.
  * y_layout 0: Pauli half-rows (P, 2, d_out, 4) bf16 (d_out even);
  * y_layout 1: blade-order rows (P, d_out, 8) of y_dtype (0 fp32, 1 bf16).
  * bias: prepared with ygg_prepare_bias (mask order) or NULL.  act as above.
- * x and one expert's prepared weights must each be smaller than 2 GiB.
+ * x (x_rows * d_in * 16 bytes) and one expert's prepared weights must each be
+ * smaller than 2 GiB; larger calls are rejected (-1).
  * Replaces CliffordLinear.forward (clifford_linear.py:101-123) of every
  * expert, with the activation (activations.py:15-128) fused. */
-int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather, int P_max, const void* w_prepared,
+int ygg_pauli_grouped_linear(const void* x, int x_layout, int x_rows, const int32_t* gather, int P_max,
+                             const void* w_prepared,
                              const float* bias_prepared, const int32_t* offsets, int E, int d_in, int d_out, int act,
                              void* y, int y_layout, int y_dtype, ygg_stream_t stream);
 

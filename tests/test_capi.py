@@ -76,15 +76,75 @@ def test_argument_errors_are_reported_not_aborted():
     assert L.ygg_grouped_clifford_linear(None, 1, None, 2, None, None, None, 1, 1, 1, 1, None, 1, 0, None) == -1
     assert b"scales" in L.ygg_last_error()
     # Pauli products: odd d_in, unknown layouts, Pauli rows in fp32 are rejected before any launch
-    assert L.ygg_pauli_grouped_linear(None, 0, None, 4, None, None, None, 1, 3, 4, 0, None, 1, 1, None) == -1
+    assert L.ygg_pauli_grouped_linear(None, 0, 4, None, 4, None, None, None, 1, 3, 4, 0, None, 1, 1, None) == -1
     assert b"even" in L.ygg_last_error()
-    assert L.ygg_pauli_grouped_linear(None, 5, None, 4, None, None, None, 1, 2, 4, 0, None, 1, 1, None) == -1
+    assert L.ygg_pauli_grouped_linear(None, 5, 4, None, 4, None, None, None, 1, 2, 4, 0, None, 1, 1, None) == -1
     assert b"x layout" in L.ygg_last_error()
-    assert L.ygg_pauli_grouped_linear(None, 1, None, 4, None, None, None, 1, 2, 4, 0, None, 0, 0, None) == -1
+    assert L.ygg_pauli_grouped_linear(None, 1, 4, None, 4, None, None, None, 1, 2, 4, 0, None, 0, 0, None) == -1
     assert b"dtype" in L.ygg_last_error()
+    # x of 2 GiB or more, gathered or not, is refused before any launch (32-bit staging offsets)
+    big = (1 << 31) // (128 * 16) + 1
+    assert L.ygg_pauli_grouped_linear(1, 1, big, 1, 64, 1, None, 1, 1, 128, 64, 0, 1, 1, 1, None) == -1
+    assert b"2 GiB" in L.ygg_last_error()
+    assert L.ygg_pauli_grouped_linear(1, 0, big, None, big, 1, None, 1, 1, 128, 64, 0, 1, 1, 1, None) == -1
+    assert b"2 GiB" in L.ygg_last_error()
+    # without a gather, x must hold every row the product reads
+    assert L.ygg_pauli_grouped_linear(1, 1, 3, None, 4, 1, None, 1, 1, 8, 8, 0, 1, 1, 1, None) == -1
+    assert b"without a gather" in L.ygg_last_error()
     assert L.ygg_prepared_weight_bytes(2, 4, 3, 3) == 0  # odd d_in has no Pauli layout
     assert L.ygg_prepared_weight_bytes(2, 4, 6, 3) == 2 * 4 * 6 * 16
     assert L.ygg_prepared_weight_bytes(2, 4, 3, 4) == 2 * 4 * 3 * 64  # fp32 Pauli takes odd d_in
+
+
+def test_layer_rejects_bad_routing_sizes():
+    """Every path of ygg_moe_forward checks E and k before any launch, including the int8
+    decode path that routes inside its up product (k > E would leave slots unwritten)."""
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    ws = L.ygg_moe_workspace_bytes(8, 16, 32, 2, 2, 1, 2)
+
+    def fwd(E, k, fmt=2, act=1):  # bf16 activations, int8 weights, given logits, dummy non-null pointers
+        return L.ygg_moe_forward(1, 1, 8, 16, 32, E, k, act, 1, None, None, 1, 1, None, 1, 1, None, fmt, None, 1,
+                                 1, 1, 1, 1, 1, ws, None)
+
+    assert fwd(2, 3) == -1 and b"k=3" in L.ygg_last_error()
+    assert fwd(2, 0) == -1 and b"k=0" in L.ygg_last_error()
+    assert fwd(0, 1) == -1 and b"E=0" in L.ygg_last_error()
+    assert fwd(65, 2) == -1 and b"E=65" in L.ygg_last_error()
+    assert fwd(4, 9) == -1 and b"k=9" in L.ygg_last_error()
+    assert fwd(2, 2, act=7) == -1 and b"activation" in L.ygg_last_error()
+    # int8 weights without scales
+    assert L.ygg_moe_forward(1, 1, 8, 16, 32, 2, 2, 1, 1, None, None, 1, None, None, 1, None, None, 2, None, 1,
+                             1, 1, 1, 1, 1, ws, None) == -1
+    assert b"scales" in L.ygg_last_error()
+
+
+def test_backward_workspace_holds_either_weight_gradient():
+    """The weight-gradient region is shared by the up (d -> F) and down (F -> d) products, so
+    its size does not shrink below the down product's needs when d_model > d_ff."""
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    N, E, k, chunk = 1024, 4, 2, 384
+    P = N * k
+    chunks = (P + chunk - 1) // chunk + E
+
+    def wg(d_in, d_out):  # per-chunk partial dW planes plus partial db planes, fp32
+        return chunks * (d_out * d_in * 8 + d_out * 8) * 4
+
+    def al(b):
+        return (b + 255) // 256 * 256
+
+    for d, F in ((32, 16), (16, 32)):
+        regions = [N * k * 4, N * k * 4, E * 4, (E + 1) * 4, P * 4, P * 4, N * E * 4,
+                   L.ygg_route_workspace_bytes(N, E, k), N * d * 32] + [P * F * 32] * 4 + [P * d * 32] * 3
+        want = sum(al(r) for r in regions) + al(max(wg(d, F), wg(F, d)))
+        assert L.ygg_moe_backward_workspace_bytes(N, d, F, E, k) == want, (d, F)
 
 
 def test_config_validation():
@@ -194,3 +254,33 @@ def test_weight_grad_pauli_argument_checks():
     assert b"workspace" in L.ygg_last_error()
     assert L.ygg_grouped_weight_grad_pauli_f32(None, None, None, fake, 10, 2, 4, 4, fake, None, fake, 1 << 20,
                                                None) == -1
+
+
+def test_layer_wrappers_validate_tensors_before_launch():
+    """ops' layer wrappers refuse logits, residuals, router parameters and biases of the wrong
+    shape or dtype (host-side, before any pointer reaches a kernel)."""
+    from yggdrasil_amd import ops
+
+    N, d, F, E, k = 6, 4, 8, 3, 2
+    x = torch.zeros(N, d, 8, dtype=torch.bfloat16)
+    ok = dict(logits=torch.zeros(N, E), residual=torch.zeros(N, d, 8, dtype=torch.bfloat16),
+              b_up=torch.zeros(E, F, 8), b_down=torch.zeros(E, d, 8))
+    ops._check_layer_args(x, k, E, F, **ok)
+    ops._check_layer_args(x, k, E, F, router_weight=torch.zeros(E, 4), router_bias=torch.zeros(E))
+    bad = [
+        dict(ok, logits=torch.zeros(N, E, dtype=torch.bfloat16)),
+        dict(ok, logits=torch.zeros(N, E + 1)),
+        dict(ok, residual=torch.zeros(N, d, 8)),
+        dict(ok, residual=torch.zeros(N + 1, d, 8, dtype=torch.bfloat16)),
+        dict(ok, b_up=torch.zeros(E, d, 8)),
+        dict(ok, b_down=torch.zeros(E, d, 8, dtype=torch.bfloat16)),
+        dict(logits=None),
+        dict(logits=None, router_weight=torch.zeros(E, 3), router_bias=torch.zeros(E)),
+        dict(logits=None, router_weight=torch.zeros(E, 4), router_bias=torch.zeros(E + 1)),
+    ]
+    for kw in bad:
+        with pytest.raises(ValueError):
+            ops._check_layer_args(x, k, E, F, **kw)
+    for kk in (0, E + 1, 9):
+        with pytest.raises(ValueError):
+            ops._check_layer_args(x, kk, E, F, **ok)

@@ -131,6 +131,9 @@ def _layer_case(g, N, d, F, E, k, act, router):
     (130, 8, 24, 5, 3, "relu", "logits", True),
     (1200, 16, 32, 8, 2, "gelu", "energy", False),
     (2600, 8, 24, 2, 2, "gelu", "logits", True),  # 2600 rows per expert: the weight gradient's row chunks
+    # d_model > d_ff with the MFMA weight gradient (512 rows per expert): the down product's
+    # partial sums (d-wide bias planes) are the larger use of the shared workspace region
+    (1024, 32, 16, 4, 2, "gelu", "logits", False),
 ])
 def test_layer_autograd_against_oracle(N, d, F, E, k, act, router, residual):
     g = np.random.default_rng(N + d + F)

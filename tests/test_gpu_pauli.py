@@ -172,7 +172,7 @@ def test_pauli_rejects_bad_arguments():
     with pytest.raises(ValueError):
         ops.prepare_weights(torch.zeros(1, 4, 3, 8, device="cuda"), "pauli")
     L = ops.lib()
-    assert L.ygg_pauli_grouped_linear(None, 0, None, 4, None, None, None, 65, 4, 4, 0, None, 1, 1, None) == -1
+    assert L.ygg_pauli_grouped_linear(None, 0, 4, None, 4, None, None, None, 65, 4, 4, 0, None, 1, 1, None) == -1
     assert b"E <= 64" in L.ygg_last_error()
 
 

@@ -35,8 +35,8 @@ SIGNATURES = {
     "ygg_prepare_bias": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
     "ygg_grouped_clifford_linear": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                                              _c_int, _vp, _c_int, _c_int, _vp]),
-    "ygg_pauli_grouped_linear": (_c_int, [_vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
-                                          _vp, _c_int, _c_int, _vp]),
+    "ygg_pauli_grouped_linear": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int,
+                                          _c_int, _vp, _c_int, _c_int, _vp]),
     "ygg_pauli_rows_from_blade": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
     "ygg_pauli_grouped_linear_f32": (_c_int, [_vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
                                               _c_int, _vp]),

@@ -11,6 +11,7 @@
 #include <stdio.h>
 
 #include "ygg_common.h"
+#include "route_select.h"
 
 namespace ygg {
 
@@ -55,7 +56,7 @@ extern "C" int ygg_combine(const void*, int, int, int, int, int, const int32_t*,
                            const void*, void*, int, hipStream_t);
 extern "C" int ygg_grouped_clifford_linear(const void*, int, const void*, int, const float*, const float*,
                                            const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
-extern "C" int ygg_pauli_grouped_linear(const void*, int, const int32_t*, int, const void*, const float*,
+extern "C" int ygg_pauli_grouped_linear(const void*, int, int, const int32_t*, int, const void*, const float*,
                                         const int32_t*, int, int, int, int, void*, int, int, hipStream_t);
 extern "C" int ygg_pauli_rows_from_blade(const void*, int, int, void*, hipStream_t);
 extern "C" int ygg_pauli_rows_from_blade_f32(const float*, int, int, float*, hipStream_t);
@@ -91,6 +92,15 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
                             float* topk_w, int32_t* counts, int32_t* offsets, void* workspace,
                             size_t workspace_bytes, hipStream_t stream,
                             float* h_pre_out) {
+  // every path checks the sizes here, also those that route inside a product
+  YGG_CHECK_ARG(N >= 0 && d >= 1 && F >= 1, "ygg_moe_forward: bad sizes N=%d d=%d F=%d", N, d, F);
+  YGG_CHECK_ARG(E >= 1 && E <= kMaxExperts, "ygg_moe_forward: E=%d out of range [1, %d]", E, kMaxExperts);
+  YGG_CHECK_ARG(k >= 1 && k <= kMaxTopK && k <= E, "ygg_moe_forward: k=%d out of range [1, min(%d, E=%d)]", k,
+                kMaxTopK, E);
+  YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_moe_forward: activation %d", act);
+  YGG_CHECK_ARG(N == 0 || (x && out && w_up && w_down && topk_idx && topk_w && counts && offsets && workspace),
+                "ygg_moe_forward: null pointer");
+  YGG_CHECK_ARG(w_format != kWI8 || N == 0 || (s_up && s_down), "ygg_moe_forward: int8 weights need their scales");
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
   YGG_CHECK_ARG(dtype == kF32 ? (w_format == kWF32 || w_format == kWPauliF32)
                              : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
@@ -154,10 +164,10 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     // rows through perm inside the product -> h in Pauli half-rows; down: h -> y_sorted
     // in blade order.  No expert-grouped copy of x is made.
     if (ygg_pauli_rows_from_blade(x, N, d, xs, stream)) return -1;
-    if (ygg_pauli_grouped_linear(xs, /*Pauli rows*/ 1, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h,
+    if (ygg_pauli_grouped_linear(xs, /*Pauli rows*/ 1, N, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h,
                                  /*Pauli rows*/ 0, kBF16, stream))
       return -1;
-    if (ygg_pauli_grouped_linear(h, /*Pauli rows*/ 1, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, ys,
+    if (ygg_pauli_grouped_linear(h, /*Pauli rows*/ 1, (int)P, nullptr, (int)P, w_down, b_down, offsets, E, F, d, kActNone, ys,
                                  /*blade*/ 1, kBF16, stream))
       return -1;
     return ygg_combine(ys, kBF16, /*y_mask=*/0, N, k, d, topk_idx, topk_w, slot_pos, residual, out, dtype, stream);
@@ -261,7 +271,12 @@ static int bw_regions(int N, int d, int F, int E, int k, size_t* r) {
   r[n++] = (size_t)N * d * 32;  // x in Pauli rows
   for (int q = 0; q < 4; ++q) r[n++] = P * F * 32;  // h_pre, h, Pauli rows of h / dh_pre, dh / dh_pre
   for (int q = 0; q < 3; ++q) r[n++] = P * d * 32;  // y / dx rows, dy, Pauli rows of dy
-  r[n++] = weight_grad_pauli_workspace_bytes((int)P, E, d, F);  // weight-gradient partial sums (either product)
+  // weight-gradient partial sums, reused by both products: the up product's
+  // (d_in = d, d_out = F) and the down product's (d_in = F, d_out = d, whose
+  // bias planes are d-wide), so the larger of the two
+  const size_t wg_up = weight_grad_pauli_workspace_bytes((int)P, E, d, F);
+  const size_t wg_down = weight_grad_pauli_workspace_bytes((int)P, E, F, d);
+  r[n++] = wg_up > wg_down ? wg_up : wg_down;
   return n;
 }
 

@@ -991,8 +991,8 @@ int ygg::decode_linear_gather(const uint16_t* x, const int32_t* perm, int P_max,
 }
 
 bool ygg::decode_route_fusable(int N, int E, int k, int d_in) {
-  return N >= 1 && N <= kFuseMaxTokens && N * k <= kFuseMaxSlots && E <= kMaxExperts && k <= kMaxTopK &&
-         d_in <= kDecChunk;
+  return N >= 1 && N <= kFuseMaxTokens && N * k <= kFuseMaxSlots && E >= 1 && E <= kMaxExperts && k >= 1 &&
+         k <= kMaxTopK && k <= E && d_in <= kDecChunk;
 }
 
 template <int ACT>

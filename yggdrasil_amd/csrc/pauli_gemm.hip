@@ -90,7 +90,7 @@ template <int ACT, int IN, int OUT, int OUT_DT, class TL>
 __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_kernel(
     const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
-    void* __restrict__ Y, int n_xcd) {
+    void* __restrict__ Y, int n_xcd, uint32_t x_bytes) {
   constexpr int NT = TL::NT, T = TL::T, BN = TL::BN, KC = TL::KC, WR = TL::WR, WC = TL::WC, BWT = TL::BWT;
   constexpr int A_PER = TL::A_PER, W_PER = TL::W_PER;
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TL::STAGE];
@@ -146,9 +146,11 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   // ---- staging: global -> registers -> LDS --------------------------------
   // Staging loads are raw buffer loads: an offset past the end of the
   // descriptor's range reads zero, so the K tail and out-of-range columns
-  // need no branches.  Row offsets are 32-bit (operands below 2 GiB).
+  // need no branches.  Row offsets are 32-bit: the host admits only operands
+  // below 2 GiB, and x's range is its true size, so a row index past x's rows
+  // reads zero rather than another row.
   const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0,
-                                                                          0x7fffffff, kBufferFlags);
+                                                                          x_bytes, kBufferFlags);
   constexpr uint32_t kOff = 0x80000000u;  // reads zero
   PauliTileInfo ld = {0, 0, 1, 0};  // tile of the chunk being loaded
   __amdgpu_buffer_rsrc_t w_rsrc = x_rsrc;
@@ -448,8 +450,8 @@ DeviceShape device_shape() {
 }
 
 template <int ACT, int IN, int OUT, int ODT>
-int launch_pauli(hipStream_t st, const uint16_t* X, const int32_t* gather, const uint16_t* Wp, const float* bias,
-                      const int32_t* offsets, int E, int P_max, int d_in, int d_out, void* Y) {
+int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int32_t* gather, const uint16_t* Wp,
+                 const float* bias, const int32_t* offsets, int E, int P_max, int d_in, int d_out, void* Y) {
   const DeviceShape ds = device_shape();
   // never more workgroups than tiles can exist
   const long long max_tiles =
@@ -461,15 +463,16 @@ int launch_pauli(hipStream_t st, const uint16_t* X, const int32_t* gather, const
     xcds = 1;
   }
   pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
-      <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds);
+      <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
   return check_launch("pauli_gemm");
 }
 
 template <int ACT>
-int launch_pauli_act(hipStream_t st, int in_layout, int out_layout, int y_dtype, const uint16_t* X,
+int launch_pauli_act(hipStream_t st, int in_layout, int out_layout, int y_dtype, const uint16_t* X, uint32_t x_bytes,
                      const int32_t* gather, const uint16_t* Wp, const float* bias, const int32_t* offsets, int E,
                      int P_max, int d_in, int d_out, void* Y) {
-#define YGG_PL(IN, OUT, ODT) launch_pauli<ACT, IN, OUT, ODT>(st, X, gather, Wp, bias, offsets, E, P_max, d_in, d_out, Y)
+#define YGG_PL(IN, OUT, ODT) \
+  launch_pauli<ACT, IN, OUT, ODT>(st, X, x_bytes, gather, Wp, bias, offsets, E, P_max, d_in, d_out, Y)
   if (in_layout == kInBladeGather) {
     if (out_layout == kOutPauliRows) return YGG_PL(kInBladeGather, kOutPauliRows, kBF16);
     if (y_dtype == kBF16) return YGG_PL(kInBladeGather, kOutBlade, kBF16);
@@ -503,7 +506,8 @@ YGG_API int ygg_pauli_rows_from_blade(const void* x, int rows, int d, void* out,
   return check_launch("blade_to_pauli_rows");
 }
 
-YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t* gather, int P_max, const void* w,
+YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, int x_rows, const int32_t* gather, int P_max,
+                                     const void* w,
                                      const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int act,
                                      void* y, int y_layout, int y_dtype, hipStream_t stream) {
   YGG_CHECK_ARG(x_layout == kInBladeGather || x_layout == kInPauliRows, "ygg_pauli_grouped_linear: x layout %d",
@@ -517,28 +521,31 @@ YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, const int32_t*
                 "ygg_pauli_grouped_linear: bad sizes E=%d P=%d d_in=%d d_out=%d (E <= %d; d_in, and d_out of Pauli "
                 "rows, must be even)",
                 E, P_max, d_in, d_out, kPauliMaxExperts);
+  YGG_CHECK_ARG(x_rows >= 0 && (gather != nullptr || x_rows >= P_max),
+                "ygg_pauli_grouped_linear: x has %d rows, the product reads %d without a gather", x_rows, P_max);
+  // staging uses 32-bit buffer offsets: every operand stays below 2 GiB (x's
+  // rows, blade or Pauli half-row pairs, are 16 d_in bytes either way)
+  const size_t lim = (size_t)1 << 31;
+  YGG_CHECK_ARG((size_t)d_out * d_in * 16 < lim && (size_t)E * d_out * 32 < lim && (size_t)x_rows * d_in * 16 < lim,
+                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (x rows=%d d_in=%d d_out=%d)",
+                x_rows, d_in, d_out);
   if (P_max == 0) return 0;
   YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear: null pointer");
-  // staging uses 32-bit buffer offsets: every operand stays below 2 GiB
-  const size_t lim = (size_t)1 << 31;
-  YGG_CHECK_ARG((size_t)d_out * d_in * 16 < lim && (size_t)E * d_out * 32 < lim &&
-                    (gather != nullptr || (size_t)P_max * d_in * 16 < lim),
-                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (P=%d d_in=%d d_out=%d)",
-                P_max, d_in, d_out);
+  const uint32_t x_bytes = (uint32_t)((size_t)x_rows * d_in * 16);
   const uint16_t* X = static_cast<const uint16_t*>(x);
   const uint16_t* Wp = static_cast<const uint16_t*>(w);
   switch (act) {
     case kActNone:
-      return launch_pauli_act<kActNone>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+      return launch_pauli_act<kActNone>(stream, x_layout, y_layout, y_dtype, X, x_bytes, gather, Wp, bias, offsets, E, P_max,
                                         d_in, d_out, y);
     case kActGelu:
-      return launch_pauli_act<kActGelu>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+      return launch_pauli_act<kActGelu>(stream, x_layout, y_layout, y_dtype, X, x_bytes, gather, Wp, bias, offsets, E, P_max,
                                         d_in, d_out, y);
     case kActRelu:
-      return launch_pauli_act<kActRelu>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E, P_max,
+      return launch_pauli_act<kActRelu>(stream, x_layout, y_layout, y_dtype, X, x_bytes, gather, Wp, bias, offsets, E, P_max,
                                         d_in, d_out, y);
     default:
-      return launch_pauli_act<kActSigmoid>(stream, x_layout, y_layout, y_dtype, X, gather, Wp, bias, offsets, E,
+      return launch_pauli_act<kActSigmoid>(stream, x_layout, y_layout, y_dtype, X, x_bytes, gather, Wp, bias, offsets, E,
                                            P_max, d_in, d_out, y);
   }
 }

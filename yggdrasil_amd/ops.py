@@ -40,6 +40,29 @@ def _dtype_code(t: torch.Tensor) -> int:
         raise ValueError(f"unsupported dtype {t.dtype}; use float32 or bfloat16") from None
 
 
+def _check_layer_args(x, k, E, F, logits=None, residual=None, router_weight=None, router_bias=None, b_up=None,
+                      b_down=None):
+    """Shapes and dtypes of a layer call's tensors, checked before their pointers reach the kernels."""
+    if x.dim() != 3 or x.shape[2] != 8:
+        raise ValueError(f"x must be (N, d, 8), got {tuple(x.shape)}")
+    Nt, d = x.shape[0], x.shape[1]
+    if not 1 <= k <= min(8, E):
+        raise ValueError(f"top_k={k} must lie in [1, min(8, E={E})]")
+    if logits is not None and (logits.dtype != torch.float32 or tuple(logits.shape) != (Nt, E)):
+        raise ValueError(f"logits must be float32 ({Nt}, {E}), got {logits.dtype} {tuple(logits.shape)}")
+    if logits is None and (router_weight is None or router_bias is None):
+        raise ValueError("need logits or the router's weight and bias")
+    if router_weight is not None and tuple(router_weight.shape) != (E, 4):
+        raise ValueError(f"router_weight must be ({E}, 4), got {tuple(router_weight.shape)}")
+    if router_bias is not None and tuple(router_bias.shape) != (E,):
+        raise ValueError(f"router_bias must be ({E},), got {tuple(router_bias.shape)}")
+    if residual is not None and (residual.dtype != x.dtype or tuple(residual.shape) != tuple(x.shape)):
+        raise ValueError("residual must have x's shape and dtype")
+    for name, b, want in (("b_up", b_up, (E, F, 8)), ("b_down", b_down, (E, d, 8))):
+        if b is not None and (b.dtype != torch.float32 or tuple(b.shape) != want):
+            raise ValueError(f"{name} must be a prepared float32 bias {want}, got {b.dtype} {tuple(b.shape)}")
+
+
 # ---------------------------------------------------------------------------
 # operator boundary
 # ---------------------------------------------------------------------------
@@ -308,7 +331,7 @@ def pauli_grouped_linear(x: torch.Tensor, pw: PreparedWeights, offsets: torch.Te
         y = torch.empty((rows, 2, pw.d_out, 4), device=dev, dtype=torch.bfloat16)
     else:
         y = torch.empty((rows, pw.d_out, 8), device=dev, dtype=out_dtype)
-    check(lib().ygg_pauli_grouped_linear(ptr(x), X_LAYOUT[x_layout], ptr(gather), rows, ptr(pw.data),
+    check(lib().ygg_pauli_grouped_linear(ptr(x), X_LAYOUT[x_layout], x.shape[0], ptr(gather), rows, ptr(pw.data),
                                          ptr(bias_prepared), ptr(offsets), pw.E, pw.d_in, pw.d_out, ACT_CODE[act],
                                          ptr(y), Y_LAYOUT[y_layout], DTYPE_CODE[y.dtype], stream_handle(dev)),
           "pauli_grouped_linear")
@@ -377,13 +400,14 @@ def moe_forward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: Prepared
                 router_bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
                 workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
     """The whole layer in one call (``ygg_moe_forward``). x: (N, d, 8). Returns (out, Routing-lite)."""
-    dev = _dev(x, logits, residual)
+    dev = _dev(x, logits, residual, router_weight, router_bias, b_up, b_down)
     Nt, d = x.shape[0], x.shape[1]
     E, F = w_up.E, w_up.d_out
     if w_down.d_in != F or w_down.d_out != d or w_up.d_in != d or w_down.E != E:
         raise ValueError("expert weight shapes do not chain d -> F -> d")
     if w_up.fmt != w_down.fmt:
         raise ValueError("up and down weights must share a format")
+    _check_layer_args(x, k, E, F, logits, residual, router_weight, router_bias, b_up, b_down)
     ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
@@ -434,7 +458,7 @@ def moe_block_ffn(x: torch.Tensor, k: int, norm_gamma: torch.Tensor, norm_beta: 
                   router_bias: torch.Tensor | None = None, norm_eps: float = 1e-6,
                   workspace: torch.Tensor | None = None, out: torch.Tensor | None = None):
     """``x + moe(ffn_norm(x))`` in one call (``ygg_moe_block_ffn``, ``hlm_block.py:144-151``). x: (N, d, 8)."""
-    dev = _dev(x, logits, norm_gamma, norm_beta)
+    dev = _dev(x, logits, norm_gamma, norm_beta, router_weight, router_bias, b_up, b_down)
     if x.dim() != 3 or x.shape[2] != 8 or not x.is_contiguous():
         raise ValueError(f"moe_block_ffn: x must be contiguous (N, d, 8), got {tuple(x.shape)}")
     Nt, d = x.shape[0], x.shape[1]
@@ -443,6 +467,7 @@ def moe_block_ffn(x: torch.Tensor, k: int, norm_gamma: torch.Tensor, norm_beta: 
         raise ValueError("expert weight shapes do not chain d -> F -> d")
     if w_up.fmt != w_down.fmt:
         raise ValueError("up and down weights must share a format")
+    _check_layer_args(x, k, E, F, logits, None, router_weight, router_bias, b_up, b_down)
     if tuple(norm_gamma.shape) != (d, 8) or tuple(norm_beta.shape) != (d, 8):
         raise ValueError(f"moe_block_ffn: norm gamma and beta must be ({d}, 8)")
     ws_bytes = moe_block_ffn_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
@@ -549,6 +574,7 @@ def moe_backward(x: torch.Tensor, k: int, w_up: PreparedWeights, w_up_adj: Prepa
     if (w_up_adj.d_out, w_up_adj.d_in, w_down.d_out, w_down.d_in, w_down_adj.d_out, w_down_adj.d_in) != \
             (d, F, d, F, F, d):
         raise ValueError("moe_backward: weight shapes do not chain d -> F -> d")
+    _check_layer_args(x, k, E, F, logits, None, router_weight, router_bias, b_up, b_down)
     ws_bytes = lib().ygg_moe_backward_workspace_bytes(Nt, d, F, E, k)
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
@@ -575,11 +601,14 @@ def moe_forward_train(x: torch.Tensor, k: int, w_up: PreparedWeights, w_down: Pr
                       workspace: torch.Tensor | None = None):
     """``moe_forward`` for a training step (fp32, ``pauli_f32``): also returns the up product's
     pre-activation rows ``h_pre`` (N k, F, 8) for ``moe_backward``."""
-    dev = _dev(x, logits, residual)
+    dev = _dev(x, logits, residual, router_weight, router_bias, b_up, b_down)
     if w_up.fmt != "pauli_f32" or w_down.fmt != "pauli_f32" or x.dtype != torch.float32:
         raise ValueError("moe_forward_train: fp32 layers with 'pauli_f32' weights")
     Nt, d = x.shape[0], x.shape[1]
     E, F = w_up.E, w_up.d_out
+    if w_down.d_in != F or w_down.d_out != d or w_up.d_in != d or w_down.E != E:
+        raise ValueError("expert weight shapes do not chain d -> F -> d")
+    _check_layer_args(x, k, E, F, logits, residual, router_weight, router_bias, b_up, b_down)
     ws_bytes = moe_workspace_bytes(Nt, d, F, E, k, x.dtype, w_up.fmt)
     if workspace is None or workspace.numel() < ws_bytes:
         workspace = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
