@@ -68,24 +68,24 @@ def _gate_backward(c, g, fn, dfn):
     return (gated / mag) * g + (dfn(mag) - gated / mag) * direction * dot
 
 
-def activation_backward(act, h, g):
-    """Gradient w.r.t. the activation input ``h`` (..., 8) given ``g`` w.r.t. its output."""
-    h = np.asarray(h, F32)
-    g = np.asarray(g, F32)
+def activation_backward(act, h, g, dtype=F32):
+    """Gradient w.r.t. the activation input ``h`` (..., 8) given ``g`` w.r.t. its output, in ``dtype``."""
+    h = np.asarray(h, dtype)
+    g = np.asarray(g, dtype)
     if act == "none":
         return g.copy()
     out = np.zeros_like(h)
     if act == "relu":
-        out[..., 0:1] = g[..., 0:1] * (h[..., 0:1] > 0).astype(F32)
+        out[..., 0:1] = g[..., 0:1] * (h[..., 0:1] > 0).astype(dtype)
         for sl in (slice(1, 4), slice(4, 7)):
             c = h[..., sl]
             mag = np.sqrt(np.sum(c ** 2, axis=-1, keepdims=True) + 1e-12)
-            active = (mag > 0).astype(F32)
+            active = (mag > 0).astype(dtype)
             direction = c / mag
             dot = np.sum(direction * g[..., sl], axis=-1, keepdims=True)
             gated = np.maximum(mag, 0.0)
             out[..., sl] = active * ((gated / mag) * g[..., sl] + (1.0 - gated / mag) * direction * dot)
-        out[..., 7:8] = g[..., 7:8] * (np.abs(h[..., 7:8]) > 0).astype(F32)
+        out[..., 7:8] = g[..., 7:8] * (np.abs(h[..., 7:8]) > 0).astype(dtype)
         return out
     fn, dfn = (moe._gelu, _gelu_derivative) if act == "gelu" else (moe._sigmoid, _sigmoid_derivative)
     out[..., 0:1] = g[..., 0:1] * dfn(h[..., 0:1])
