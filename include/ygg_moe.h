@@ -5,7 +5,8 @@
  *
  * Conventions (every entry point):
  *  - plain C types only; every pointer is a DEVICE pointer owned by the caller
- *    (the library allocates nothing and keeps no state between calls);
+ *    (the library allocates nothing and keeps no state between calls, except
+ *    the per-GPU scratch array of ygg_moe_forward_noalloc);
  *  - the work is enqueued on `stream` (a hipStream_t; pass the caller's
  *    current stream, e.g. torch.cuda.current_stream().cuda_stream);
  *  - the return value is 0 on success and -1 on a rejected argument or a
@@ -198,6 +199,25 @@ int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k,
                     const float* b_up, const void* w_down, const float* s_down, const float* b_down, int w_format,
                     const void* residual, void* out, int32_t* topk_idx, float* topk_w, int32_t* counts,
                     int32_t* offsets, void* workspace, size_t workspace_bytes, ygg_stream_t stream);
+
+/* Bytes of device scratch the library holds per GPU for ygg_moe_forward_noalloc. */
+#define YGG_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* ygg_moe_forward without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference: its launchers allocate per
+ * call (rune/bindings/mjolnir_cuda_ffi.py:527-542).  The scratch is a device array
+ * the library keeps on each GPU it runs on (YGG_NOALLOC_SCRATCH_BYTES, held until
+ * the process ends); calls whose ygg_moe_workspace_bytes exceeds it are rejected
+ * (-1).  The call allocates nothing; `stream` must belong to the current device.
+ * Calls on one GPU share the scratch, so calls that overlap on one GPU (two
+ * streams, or two host threads) race; calls in stream order do not.  Outputs are
+ * those of ygg_moe_forward on the same arguments. */
+int ygg_moe_forward_noalloc(const void* x, int dtype, int N, int d, int F, int E, int k, int act, const float* logits,
+                            const float* router_w, const float* router_b, const void* w_up, const float* s_up,
+                            const float* b_up, const void* w_down, const float* s_down, const float* b_down,
+                            int w_format, const void* residual, void* out, int32_t* topk_idx, float* topk_w,
+                            int32_t* counts, int32_t* offsets, ygg_stream_t stream);
 
 /* ---- backward (fp32) ---------------------------------------------------------------
  * The reference has no MoE backward (hlm_block.py:202-206); these follow

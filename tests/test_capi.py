@@ -284,3 +284,21 @@ def test_layer_wrappers_validate_tensors_before_launch():
     for kk in (0, E + 1, 9):
         with pytest.raises(ValueError):
             ops._check_layer_args(x, kk, E, F, **ok)
+
+
+def test_noalloc_entry_refuses_oversized_calls_before_touching_a_device():
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    limit = 64 << 20
+    assert L.ygg_moe_workspace_bytes(8192, 128, 512, 32, 4, 1, 3) > limit
+    rc = L.ygg_moe_forward_noalloc(1, 1, 8192, 128, 512, 32, 4, 1, 1, None, None, 1, None, None, 1, None, None, 3,
+                                   None, 1, 1, 1, 1, 1, None)
+    assert rc == -1 and b"more than the 67108864" in L.ygg_last_error()
+    assert L.ygg_moe_forward_noalloc(1, 1, 8, 16, 32, 2, 0, 1, 1, None, None, 1, None, None, 1, None, None, 3,
+                                     None, 1, 1, 1, 1, 1, None) == -1
+    assert b"bad sizes" in L.ygg_last_error()
+    # a decode-sized layer fits
+    assert L.ygg_moe_workspace_bytes(64, 128, 512, 32, 2, 1, 2) <= limit

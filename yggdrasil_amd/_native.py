@@ -45,6 +45,8 @@ SIGNATURES = {
     "ygg_moe_forward": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                  _c_size, _vp]),
+    "ygg_moe_forward_noalloc": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+                                         _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ygg_adjoint_weights_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "ygg_grouped_weight_grad_f32": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
     "ygg_grouped_weight_grad_pauli_f32_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),

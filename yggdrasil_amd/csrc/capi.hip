@@ -10,6 +10,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "ygg_common.h"
 #include "route_select.h"
 
@@ -210,6 +212,81 @@ YGG_API int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E
   return moe_forward_impl(x, dtype, N, d, F, E, k, act, logits, router_w, router_b, w_up, s_up, b_up, w_down, s_down,
                           b_down, w_format, residual, out, topk_idx, topk_w, counts, offsets, workspace,
                           workspace_bytes, stream, nullptr);
+}
+
+// ---- the layer without allocation ------------------------------------------------
+// For callers that cannot allocate device memory (code under graph capture, tight
+// serving loops): ygg_moe_forward with its workspace taken from a file-scope device
+// array instead of a caller-sized buffer.  Every GPU the library runs on holds its
+// own copy of the array, from the first call on that GPU until the process ends.
+// Its host-side name is only a stand-in: the device address of each GPU's copy
+// comes from hipGetSymbolAddress, once per device, and only that address reaches
+// kernels.  No region of it needs to start at zero (the layer writes every byte
+// it later reads), so calls clear nothing; they share the array, so two calls
+// that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;  // YGG_NOALLOC_SCRATCH_BYTES in ygg_moe.h
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` runs on (looked up once per
+// device, with that device current).
+int device_scratch(hipStream_t stream, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) {
+    set_error("ygg_moe_forward_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return -1;
+  }
+  hipDevice_t sdev = cur;
+  if (stream != nullptr && (e = hipStreamGetDevice(stream, &sdev)) != hipSuccess) {
+    set_error("ygg_moe_forward_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    return -1;
+  }
+  if (sdev != cur) {
+    set_error("ygg_moe_forward_noalloc: the stream belongs to device %d, the current device is %d", (int)sdev, cur);
+    return -1;
+  }
+  if (cur < 0 || cur >= kMaxDevices) {
+    set_error("ygg_moe_forward_noalloc: device %d beyond the %d the library tracks", cur, kMaxDevices);
+    return -1;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[cur] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("ygg_moe_forward_noalloc: hipGetSymbolAddress on device %d: %s", cur, hipGetErrorString(e));
+      return -1;
+    }
+    g_scratch_ptr[cur] = p;
+  }
+  *out = g_scratch_ptr[cur];
+  return 0;
+}
+}  // namespace
+
+YGG_API int ygg_moe_forward_noalloc(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
+                                    const float* logits, const float* router_w, const float* router_b,
+                                    const void* w_up, const float* s_up, const float* b_up, const void* w_down,
+                                    const float* s_down, const float* b_down, int w_format, const void* residual,
+                                    void* out, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
+                                    hipStream_t stream) {
+  YGG_CHECK_ARG(N >= 0 && d >= 1 && F >= 1 && k >= 1, "ygg_moe_forward_noalloc: bad sizes N=%d d=%d F=%d k=%d", N, d,
+                F, k);
+  const size_t need = ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format);
+  YGG_CHECK_ARG(need <= kNoAllocScratchBytes,
+                "ygg_moe_forward_noalloc: this layer call needs %zu bytes of scratch, more than the %zu the library "
+                "holds per device; use ygg_moe_forward with a workspace",
+                need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (N > 0 && device_scratch(stream, &ws)) return -1;
+  return moe_forward_impl(x, dtype, N, d, F, E, k, act, logits, router_w, router_b, w_up, s_up, b_up, w_down, s_down,
+                          b_down, w_format, residual, out, topk_idx, topk_w, counts, offsets, ws,
+                          kNoAllocScratchBytes, stream, nullptr);
 }
 
 // The forward of a training step (fp32 Pauli weights): ygg_moe_forward, and the
