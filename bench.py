@@ -52,7 +52,9 @@ CONFIGS = {
     "c3": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1),
     # config 3 again with the 8x8 L(w)-block expert products (comparison; not in the default set)
     "c3l": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="bf16", logits="zipf", layers=1),
-    "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1),
+    # decode: each step runs the layer with the next of 10 weight sets (335 MB, more than the 256 MB
+    # Infinity Cache), so the weights stream from HBM as in a multi-layer decode step
+    "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1, rotate=10),
     "c5": dict(N=4096, d=256, E=64, k=2, F=1024, dtype="bf16", fmt="pauli", logits="normal_bias", layers=12),
     # training step (forward + backward, fp32 Pauli weights) at the config 1 and config 3 shapes
     "c1t": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1, train=True),
@@ -145,7 +147,8 @@ def time_fn(torch, fn, steps, warmup):
 
 
 def run_layer_config(torch, ops, name, c, steps, warmup):
-    x, layers = make_inputs(torch, c, seed=SEEDS[name])
+    rot = c.get("rotate", 0)
+    x, layers = make_inputs(torch, dict(c, layers=rot) if rot else c, seed=SEEDS[name])
     N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
     prepared = []
     for L in layers:
@@ -175,7 +178,22 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
             cur = out
         info["rt"] = rt
 
-    ms = time_fn(torch, step, steps, warmup)
+    all_sets = prepared
+    if rot:  # one layer per step with weight set i mod rot; the warm figure reuses set 0 every step
+        prepared = all_sets[:1]
+        ms_warm = time_fn(torch, step, steps, warmup)
+        counter = [0]
+
+        def step_rot():
+            P = all_sets[counter[0] % rot]
+            counter[0] += 1
+            _, rt = ops.moe_forward(x, k, P["w_up"], P["w_down"], None, None, "gelu", logits=P["logits"],
+                                    workspace=ws, out=bufs[0])
+            info["rt"] = rt
+
+        ms = time_fn(torch, step_rot, steps, warmup)
+    else:
+        ms = time_fn(torch, step, steps, warmup)
     counts = info["rt"]["counts"].cpu()
     # the dominant kernel: both grouped expert products of layer 0, timed alone
     P0 = prepared[0]
@@ -268,6 +286,11 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         moved = n_touched * wbytes_expert + 2 * N * R + 4 * N * E
         res["decode_bytes"] = moved
         res["decode_hbm_frac"] = moved / (ms * 1e-3) / PEAK_HBM
+    if rot:
+        res["weight_sets"] = rot
+        res["ms_per_step_warm"] = ms_warm  # one weight set, resident in the Infinity Cache after the first step
+        if name == "c4":
+            res["decode_hbm_frac_warm"] = moved / (ms_warm * 1e-3) / PEAK_HBM
     res["_flops_per_launch"] = flops_proj
     res["_ms_per_launch"] = (ms_up + ms_down) / 2
     return res

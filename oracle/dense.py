@@ -16,10 +16,11 @@ result lies within fp32 rounding of it.
 The product.  With ``e_a e_b = SIGN[a, b] e_IDX[a, b]``,
     y[m, j, c] = sum_i sum_{a, b : IDX[a, b] = c} SIGN[a, b] W[j, i, a] x[m, i, b].
 For each (a, c) exactly one b = b(a, c) has ``IDX[a, b] = c`` (left multiplication
-by a basis blade permutes the basis), so every output blade c is one matrix product
-    y[:, :, c]^T = W (d_out, (i, a))  .  [SIGN[a, b(a, c)] x[:, i, b(a, c)]^T]_(i, a)
-with W in its own layout and the signed, permuted input planes stacked along the
-contraction (i, a) of length 8 d_in.
+by a basis blade permutes the basis), so the layer is one matrix product
+    Y[j, (c, m)] = sum_(i, a) W[j, (i, a)] Xs[(i, a), (c, m)],
+    Xs[(i, a), (c, m)] = SIGN[a, b(a, c)] x[m, i, b(a, c)],
+with W in its own (d_out, d_in * 8) layout and Xs the signed, permuted input
+planes (8 times the input, built once per chunk of rows; W is read once per chunk).
 The backward uses the left-multiplication matrix ``L(W)`` (``cl3.left_mul_matrix``):
 ``Y = X L^T``, so ``dX = dY L`` and ``dL = dY^T X``, folded back onto the weight
 components ``L(W)[r, q] = SIGN * W[src[r, q]]``.
@@ -53,7 +54,18 @@ for _a in range(8):
 assert all(sorted(_B_OF[a]) == list(range(8)) for a in range(8))
 
 
-def linear(x, W, b=None, chunk: int = 512):
+_BUFS: dict = {}
+
+
+def _buf(name, n):
+    """A reused float64 scratch array of at least n elements (fresh large arrays cost a page fault per page)."""
+    a = _BUFS.get(name)
+    if a is None or a.size < n:
+        a = _BUFS[name] = np.empty(n, F64)
+    return a[:n]
+
+
+def linear(x, W, b=None, chunk_bytes: int = 32 << 20):
     """``y[m, j] = sum_i W[j, i] x[m, i] (+ b[j])``; x (M, d_in, 8), W (d_out, d_in, 8) -> (M, d_out, 8) float64."""
     x = np.asarray(x, F64)
     W = np.asarray(W, F64)
@@ -62,14 +74,18 @@ def linear(x, W, b=None, chunk: int = 512):
     assert W.shape == (d_out, d_in, 8)
     A = W.reshape(d_out, d_in * 8)  # columns (i, a)
     y = np.empty((M, d_out, 8), F64)
+    chunk = max(16, chunk_bytes // (64 * 8 * d_in))
     for m0 in range(0, M, chunk):
         m1 = min(M, m0 + chunk)
-        planes = np.ascontiguousarray(np.transpose(x[m0:m1], (1, 2, 0)))  # (i, b, m)
-        yt = np.empty((8, d_out, m1 - m0), F64)
-        for c in range(8):
-            Bc = planes[:, _B_OF[:, c], :] * _S_OF[:, c][None, :, None]  # (i, a, m)
-            yt[c] = A @ Bc.reshape(d_in * 8, m1 - m0)
-        y[m0:m1] = np.transpose(yt, (2, 1, 0))
+        mc = m1 - m0
+        planes = _buf("planes", d_in * 8 * mc).reshape(d_in, 8, mc)
+        planes[...] = np.transpose(x[m0:m1], (1, 2, 0))  # (i, b, m)
+        Xs = _buf("xs", d_in * 64 * mc).reshape(d_in, 64, mc)
+        np.take(planes, _B_OF.reshape(-1), axis=1, out=Xs)  # (i, (a, c), m)
+        Xs *= _S_OF.reshape(1, 64, 1)
+        Y = _buf("y", d_out * 8 * mc).reshape(d_out, 8 * mc)
+        np.matmul(A, Xs.reshape(d_in * 8, 8 * mc), out=Y)  # (j, (c, m))
+        y[m0:m1] = np.transpose(Y.reshape(d_out, 8, mc), (2, 0, 1))
     if b is not None:
         y += np.asarray(b, F64)
     return y
@@ -107,13 +123,13 @@ def _slots_by_expert(idx, e):
     return np.nonzero(np.asarray(idx) == e)
 
 
-def moe_layer(x, idx, w, w_up, b_up, w_down, b_down, act="gelu", residual=None):
+def moe_layer(x, idx, w, w_up, b_up, w_down, b_down, act="gelu", residual=None, progress=None):
     """``_moe_forward`` for a given routing, float64: x (N, d, 8); idx, w (N, k); stacked expert weights
     w_up (E, F, d, 8), b_up (E, F, 8) or None, w_down (E, d, F, 8), b_down (E, d, 8) or None.
 
     The combine adds each token's expert outputs in ascending expert order
     (``hlm_block.py:180-181``); ``residual`` (N, d, 8) is added first when given
-    (``hlm_block.py:151``).
+    (``hlm_block.py:151``).  ``progress(e)``, when given, is called after each expert.
     """
     x = np.asarray(x, F64)
     idx = np.asarray(idx)
@@ -127,6 +143,8 @@ def moe_layer(x, idx, w, w_up, b_up, w_down, b_down, act="gelu", residual=None):
             continue
         h = bw.activation_f64(act, linear(x[tok], w_up[e], None if b_up is None else b_up[e]))
         y_slot[tok, slot] = linear(h, w_down[e], None if b_down is None else b_down[e])
+        if progress is not None:
+            progress(e)
     out = np.zeros_like(x) if residual is None else np.array(residual, F64)
     order = np.argsort(idx, axis=-1, kind="stable")  # ascending expert per token
     rows = np.arange(N)
@@ -136,9 +154,10 @@ def moe_layer(x, idx, w, w_up, b_up, w_down, b_down, act="gelu", residual=None):
     return out
 
 
-def moe_layer_backward(x, idx, w, w_up, b_up, w_down, b_down, dout, act="gelu", residual=False):
+def moe_layer_backward(x, idx, w, w_up, b_up, w_down, b_down, dout, act="gelu", residual=False, progress=None):
     """Backward of ``moe_layer`` for its routing: returns ``(dx, dW_up, db_up, dW_down, db_down)``, float64,
-    the weight gradients stacked over experts (zero for an expert without rows)."""
+    the weight gradients stacked over experts (zero for an expert without rows).  ``progress(e)``, when
+    given, is called after each expert."""
     x = np.asarray(x, F64)
     dout = np.asarray(dout, F64)
     w = np.asarray(w, F64)
@@ -160,4 +179,6 @@ def moe_layer_backward(x, idx, w, w_up, b_up, w_down, b_down, dout, act="gelu", 
         dh_pre = bw.activation_backward(act, h_pre, dh, dtype=F64)
         dxe, dWu[e], dbu[e] = linear_backward(xe, w_up[e], dh_pre)
         np.add.at(dx, tok, dxe)
+        if progress is not None:
+            progress(e)
     return dx, dWu, dbu, dWd, dbd

@@ -27,7 +27,7 @@ def test_linear_equals_the_dense_einsum_and_the_reference_order(M, d_in, d_out):
     x = g.standard_normal((M, d_in, 8))
     W = g.standard_normal((d_out, d_in, 8))
     b = g.standard_normal((d_out, 8))
-    got = dense.linear(x, W, b, chunk=7)  # several chunks
+    got = dense.linear(x, W, b, chunk_bytes=1)  # chunks of 16 rows
     assert _rel(got, bw.linear_f64(x, W, b)) < 1e-12
     ref32 = moe.clifford_linear(x.astype(np.float32), W.astype(np.float32), b.astype(np.float32))
     assert _rel(got, ref32) < 1e-5
