@@ -69,7 +69,10 @@ extern "C" int ygg_pauli_grouped_linear_f32(const float*, const int32_t*, int, c
 // partial planes of the K-split down product
 static size_t ys_bytes(size_t P, int E, int d, int F, int dtype, int w_format) {
   const size_t es = (dtype == kF32) ? 4 : 2;
-  if (decode_shape((int)P, E, w_format)) return (size_t)decode_splits(F) * P * d * 8 * 4;
+  if (decode_shape((int)P, E, w_format)) {
+    const int planes = decode_splits(F) > decode_layer_planes(F) ? decode_splits(F) : decode_layer_planes(F);
+    return (size_t)planes * P * d * 8 * 4;
+  }
   if (w_format == kWPauliF32) return (size_t)pauli_f32_splits((int)P, E, F, d) * P * d * 8 * 4;
   return P * d * 8 * es;
 }
@@ -137,7 +140,18 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
 
   // decode layers given logits route inside their up product (no routing launch)
   const bool decode = decode_shape((int)P, E, w_format);
-  const bool fused_route = decode && logits && decode_route_fusable(N, E, k, d);
+  const bool fused_layer = decode && logits && dtype == kBF16 && decode_layer_fusable(N, E, k, d, F);
+  const bool fused_route = decode && logits && !fused_layer && decode_route_fusable(N, E, k, d);
+  if (fused_layer) {
+    // decode layers given logits: routing, both products and the activation in one
+    // launch, then the combine of its partial planes
+    if (decode_layer(static_cast<const uint16_t*>(x), logits, N, E, k, d, F, act, static_cast<const int8_t*>(w_up),
+                     s_up, b_up, static_cast<const int8_t*>(w_down), s_down, b_down, topk_idx, topk_w, counts,
+                     offsets, perm, slot_pos, static_cast<float*>(ys), stream))
+      return -1;
+    return combine_planes(static_cast<const float*>(ys), decode_layer_planes(F), (int)P, N, k, d, topk_idx, topk_w,
+                          slot_pos, residual, out, dtype, stream);
+  }
   if (fused_route) {
     // routed below
   } else if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N

@@ -145,6 +145,18 @@ int decode_linear_gather_routed(const uint16_t* x, const float* logits, int N, i
 int decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, const float* scales, const float* bias,
                           const int32_t* offsets, int E, int d_in, int d_out, float* y_planes, hipStream_t stream);
 
+// The decode-shape layer with int8 weights in one launch (decode.hip): routing
+// of every token inside each workgroup, the up product with bias and
+// activation, and the down product cut along its contraction into
+// decode_layer_planes(F) fp32 partial planes (planes, P_max = N k, d, 8),
+// blade order, the down bias in plane 0; the routing arrays as ygg_route.
+bool decode_layer_fusable(int N, int E, int k, int d, int F);
+int decode_layer_planes(int F);
+int decode_layer(const uint16_t* x, const float* logits, int N, int E, int k, int d, int F, int act,
+                 const int8_t* w_up, const float* s_up, const float* b_up, const int8_t* w_dn, const float* s_dn,
+                 const float* b_dn, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
+                 int32_t* perm, int32_t* slot_pos, float* planes, hipStream_t stream);
+
 // combine of fp32 blade-order partial planes (dispatch.hip): the planes of a
 // row are added in plane order, then weighted and combined as ygg_combine does.
 int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
