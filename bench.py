@@ -14,11 +14,17 @@ backward, fp32) at the config 1 and 3 shapes.
 
 One JSON line is printed.  ``roofline`` covers the dominant kernel, the
 grouped CliffordLinear MFMA kernel (both expert products), from HIP events
-around its launches on the stream it runs on; ``cpu_baseline`` times the
-reference's own compiled CPU geometric matmul (``oracle/_ref``, built from
-the reference sources) -- or the C restatement if that is absent -- plus the
-NumPy restatement of routing / dispatch / combine, on a bounded sample of
-the same workload, extrapolated linearly in FLOPs.
+around its launches on the stream it runs on; its ``frac`` counts algorithmic
+FLOPs (64 multiply-adds per multivector pair), ``mfma_issued_frac`` the ones
+the Pauli form issues, and HBM traffic / MFMA-busy counters appear only when
+``profiles/pins.json`` holds them for the current sources of the kernel.
+``cpu_baseline`` (per BASELINE config under "configs", the headline's at the
+top) times the reference's own compiled CPU geometric matmul (``oracle/_ref``,
+built from the reference sources) -- or the C restatement if that is absent --
+plus the NumPy restatement of routing / dispatch / combine, on every row where
+that takes seconds and on a sample extrapolated linearly in FLOPs otherwise,
+with the reference's NumPy broadcast fallback and an OpenMP port beside it.
+The decode config (4) reports the fused layer's bytes per step against HBM.
 """
 
 from __future__ import annotations
@@ -35,8 +41,9 @@ sys.path.insert(0, ROOT)
 PEAK_BF16 = 2.5e15  # dense bf16 MFMA, FLOP/s
 PEAK_F32 = 157.3e12  # fp32 MFMA
 PEAK_HBM = 8.0e12  # bytes/s
-# measured HBM traffic of one C3 Pauli expert product (profiles/pauli_gemm_c3_traffic.md)
-PAULI_C3_TRAFFIC_BYTES = 410.9e6
+# counter figures (HBM traffic, MFMA-busy) measured by rocprofv3 for a kernel build: each entry
+# names the sources it was measured on and their SHA-256, and is used only while they match
+PINS = os.path.join(ROOT, "profiles", "pins.json")
 WGRAD_MFMA_ROWS_PER_EXPERT = 256  # as ygg_moe_backward: mean rows per expert from which it uses the MFMA kernel
 SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5}
 
@@ -81,7 +88,33 @@ def parse():
     # library GEMM rates (hipBLASLt through torch.matmul) on random bf16 operands at the dense
     # shapes the C3 Pauli products issue: the practical reference for the MFMA roofline
     ap.add_argument("--calibrate", action="store_true")
+    # record counter figures measured by rocprofv3 for the current build of a kernel, e.g.
+    # --pin '{"key": "pauli_gemm_kernel_c3", "sources": ["yggdrasil_amd/csrc/pauli_gemm.hip"],
+    #         "traffic_bytes_per_launch": 4.1e8, "mfma_busy": 0.36, "profile": "profiles/....md"}'
+    ap.add_argument("--pin", default=None)
     return ap.parse_args()
+
+
+def write_pin(spec):
+    """Store a kernel's counter figures with the SHA-256 of the sources they were measured on."""
+    import hashlib
+
+    entry = json.loads(spec)
+    key = entry.pop("key")
+    h = hashlib.sha256()
+    for rel in entry["sources"]:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    entry["sha256"] = h.hexdigest()
+    try:
+        with open(PINS) as f:
+            pins = json.load(f)
+    except (OSError, ValueError):
+        pins = {}
+    pins[key] = entry
+    with open(PINS, "w") as f:
+        json.dump(pins, f, indent=1, sort_keys=True)
+        f.write("\n")
 
 
 # ---------------------------------------------------------------------------
@@ -146,6 +179,27 @@ def time_fn(torch, fn, steps, warmup):
     return s.elapsed_time(e) / steps  # ms
 
 
+def pinned(key):
+    """The counter figures measured for kernel `key` if its sources are unchanged since, else None."""
+    import hashlib
+
+    try:
+        with open(PINS) as f:
+            entry = json.load(f)[key]
+    except (OSError, KeyError, ValueError):
+        return None
+    h = hashlib.sha256()
+    for rel in entry["sources"]:
+        try:
+            with open(os.path.join(ROOT, rel), "rb") as f:
+                h.update(f.read())
+        except OSError:
+            return None
+    if h.hexdigest() != entry["sha256"]:
+        return None
+    return entry
+
+
 def run_layer_config(torch, ops, name, c, steps, warmup):
     rot = c.get("rotate", 0)
     x, layers = make_inputs(torch, dict(c, layers=rot) if rot else c, seed=SEEDS[name])
@@ -195,6 +249,24 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     else:
         ms = time_fn(torch, step, steps, warmup)
     counts = info["rt"]["counts"].cpu()
+    P = N * k
+    es = 4 if c["dtype"] == "f32" else 2
+    R = d * 8 * es
+    n_touched = int((counts > 0).sum())
+    wbytes_expert = {"bf16": 2 * 2 * 8 * d * F, "pauli": 2 * 2 * 8 * d * F, "int8": 2 * 8 * d * F + 4 * (d + F),
+                     "f32": 2 * 4 * 8 * d * F, "pauli_f32": 2 * 4 * 8 * d * F}[c["fmt"]]
+    res = dict(
+        workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"], layers=c["layers"],
+        ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), layer_tflops=c["layers"] * 256.0 * d * F * P / (ms * 1e-3) / 1e12,
+        expert_counts_max=int(counts.max()), expert_counts_min=int(counts.min()), experts_touched=n_touched)
+    if rot:  # the decode layer: one fused kernel (routing and both products) and the combine
+        # bytes the step must move: the touched experts' weights (codes and scales), x in,
+        # the logits, and the output written
+        moved = n_touched * wbytes_expert + 2 * N * R + 4 * N * E
+        res.update(weight_sets=rot, decode_bytes=moved, decode_hbm_frac=moved / (ms * 1e-3) / PEAK_HBM,
+                   # one weight set, resident in the Infinity Cache after the first step
+                   ms_per_step_warm=ms_warm, decode_hbm_frac_warm=moved / (ms_warm * 1e-3) / PEAK_HBM)
+        return res
     # the dominant kernel: both grouped expert products of layer 0, timed alone
     P0 = prepared[0]
     if P0["head"] is not None:
@@ -263,34 +335,29 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     out_t = torch.empty_like(x)
     ms_comb = time_fn(torch, lambda: ops.combine(ys, r, out=out_t), steps, warmup)
 
-    P = N * k
-    flops_proj = 128.0 * d * F * P  # per projection (algorithmic)
-    es = 4 if c["dtype"] == "f32" else 2
-    R = d * 8 * es
-    rdc_bytes = (4 * N * E + 8 * N * k + 4 * N * k) + (N * R + P * R + 4 * P) + (P * R + 8 * P + N * R)
-    n_touched = int((counts > 0).sum())
-    wbytes_expert = {"bf16": 2 * 2 * 8 * d * F, "pauli": 2 * 2 * 8 * d * F, "int8": 2 * 8 * d * F + 4 * (d + F),
-                     "f32": 2 * 4 * 8 * d * F, "pauli_f32": 2 * 4 * 8 * d * F}[c["fmt"]]
-    layer_flops = 2 * flops_proj
-    res = dict(
-        workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"], layers=c["layers"],
-        ms_per_step=ms, tokens_per_s=N / (ms * 1e-3),
+    flops_proj = 128.0 * d * F * P  # per projection (algorithmic: 64 multiply-adds per multivector pair)
+    peak = PEAK_F32 if c["dtype"] == "f32" else PEAK_BF16
+    # bytes each timed kernel moves itself.  route: logits in; top-k indices and weights,
+    # slot positions, the permutation and the counts / offsets out.  The pass over x before
+    # the products: for the Pauli formats the conversion to Pauli rows (x in, rows out; the
+    # gather by expert happens inside the up product, whose time counts as FLOPs), else the
+    # dispatch (x rows gathered in, sorted rows out, the permutation read).  combine: the
+    # expert outputs and the slots' routing in, the tokens' outputs out.
+    b_route = 4 * N * E + 12 * P + 4 * P + 8 * E
+    b_pass = 2 * N * R if c["fmt"] in ("pauli", "pauli_f32") else P * R + P * R + 4 * P
+    b_comb = P * R + 12 * P + N * R
+    res.update(
         kernels_ms=dict(route=ms_route, dispatch=ms_disp, expert_up=ms_up, expert_down=ms_down, combine=ms_comb),
         expert_tflops=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
-        expert_mfma_frac=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / (PEAK_F32 if c["dtype"] == "f32" else PEAK_BF16),
-        layer_tflops=c["layers"] * layer_flops / (ms * 1e-3) / 1e12,
-        route_dispatch_combine_hbm_frac=rdc_bytes / ((ms_route + ms_disp + ms_comb) * 1e-3) / PEAK_HBM,
-        expert_counts_max=int(counts.max()), expert_counts_min=int(counts.min()), experts_touched=n_touched,
-    )
-    if name == "c4":
-        moved = n_touched * wbytes_expert + 2 * N * R + 4 * N * E
-        res["decode_bytes"] = moved
-        res["decode_hbm_frac"] = moved / (ms * 1e-3) / PEAK_HBM
-    if rot:
-        res["weight_sets"] = rot
-        res["ms_per_step_warm"] = ms_warm  # one weight set, resident in the Infinity Cache after the first step
-        if name == "c4":
-            res["decode_hbm_frac_warm"] = moved / (ms_warm * 1e-3) / PEAK_HBM
+        expert_mfma_frac=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / peak,
+        kernel_bytes=dict(route=b_route, dispatch=b_pass, combine=b_comb),
+        kernel_hbm_frac=dict(route=b_route / (ms_route * 1e-3) / PEAK_HBM, dispatch=b_pass / (ms_disp * 1e-3) / PEAK_HBM,
+                             combine=b_comb / (ms_comb * 1e-3) / PEAK_HBM),
+        route_dispatch_combine_hbm_frac=(b_route + b_pass + b_comb) / ((ms_route + ms_disp + ms_comb) * 1e-3) / PEAK_HBM)
+    if c["fmt"] in ("pauli", "pauli_f32"):
+        # the Pauli (complex 2x2) form issues 32 of the 64 multiply-adds: the MFMA pipes run at half
+        # the algorithmic rate
+        res["expert_mfma_issued_frac"] = res["expert_mfma_frac"] / 2
     res["_flops_per_launch"] = flops_proj
     res["_ms_per_launch"] = (ms_up + ms_down) / 2
     return res
@@ -425,9 +492,11 @@ def run_train_config(torch, ops, name, c, steps, warmup):
                 kernels_ms=dict(weight_grad_up=ms_wg_up, weight_grad_down=ms_wg_down),
                 step_tflops=6 * flops_proj / (ms * 1e-3) / 1e12,
                 weight_grad_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,
-                weight_grad_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32,
-                # the Pauli form issues half the algorithmic FLOPs (above 1 above means that)
-                weight_grad_issued_frac_f32=flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32)
+                # algorithmic: 64 multiply-adds per multivector pair; the Pauli form issues 32, so this
+                # rate can reach 2x the fp32 peak -- the issued fraction is the MFMA utilisation
+                weight_grad_algorithmic_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32,
+                weight_grad_issued_frac_f32=(flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32
+                                             if wg_kind == "mfma" else None))
 
 
 def calibrate_gemm(torch):
@@ -494,14 +563,22 @@ def run_c2(torch, ops, c, steps, warmup):
 # ---------------------------------------------------------------------------
 
 
-def cpu_baseline(c, sample_rows):
-    """Reference CPU path on a bounded sample of config c, extrapolated to the full layer."""
+def cpu_baseline(name, c, sample_rows):
+    """The reference's CPU path for config c, timed on this host (fp32, as the reference's CPU
+    path computes): routing / dispatch / combine in NumPy over all tokens, the expert FFNs through
+    the reference's compiled geometric matmul (``oracle/_ref``; the C restatement if that is
+    absent) on every token-expert row when they take at most a few seconds, else on a sample
+    extrapolated linearly in FLOPs; a multi-layer step is its layers' sum.  Two flavours beside
+    it: the NumPy broadcast fallback the reference falls back to without its native library
+    (``rune/ops/batched.py:341-344``), on a few rows, and the C restatement with OpenMP."""
     import numpy as np
 
     from oracle import moe, native
+    from oracle.cl3 import geom_prod
 
     g = np.random.default_rng(11)
     N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    layers = c["layers"]
     logits = g.standard_normal((N, E), dtype=np.float32)
     x = g.standard_normal((N, d, 8), dtype=np.float32)
     # routing + dispatch + combine over all tokens (NumPy restatement of the reference)
@@ -517,44 +594,68 @@ def cpu_baseline(c, sample_rows):
             rows = x[tok[m]]
             np.add.at(out, tok[m], w.reshape(-1)[m][:, None, None] * rows)
     t_rdc = time.perf_counter() - t0
-    # expert FFN on `sample_rows` rows of one expert
+    host = dict(nproc=os.cpu_count(), affinity=len(os.sched_getaffinity(0)), cpu=_cpu_model())
+    if not F:
+        return dict(value=N / t_rdc, unit="tokens/s", cores=1, kind="port", dtype="f32",
+                    sample=f"{config_label(c)} config, computed in fp32: NumPy routing / dispatch / combine over "
+                           f"all {N} tokens, "
+                           f"measured {t_rdc:.2f} s", host=host)
+    P = N * k
+    flops_row = 2 * 128.0 * d * F  # both expert products of one token-expert row
+    full = P * flops_row <= 8e9    # about 2-4 s through the reference C on one core
+    # else a sample of about 4 GFLOP (sample_rows at the config 3 shape)
+    rows = P if full else min(P, max(16, int(sample_rows * (2 * 128.0 * 128 * 512) / flops_row)))
     wu = (g.standard_normal((F, d, 8)) / np.sqrt(8 * d)).astype(np.float32)
     wd = (g.standard_normal((d, F, 8)) / np.sqrt(8 * F)).astype(np.float32)
-    xs = x[:sample_rows]
+    xs = np.resize(x, (rows, d, 8))
     if native.ref_lib() is not None:
         gm, kind, what = native.ref_geom_matmul, "reference", "oracle/_ref cl3_geom_matmul_flat (reference C, 1 thread)"
     else:
         gm, kind, what = native.c_geom_matmul, "port", "oracle C restatement of cl3_batch_geom_matmul (1 thread)"
+
+    def ffn(gmm, xr, **kw):
+        h = np.transpose(gmm(wu, np.ascontiguousarray(np.transpose(xr, (1, 0, 2))), **kw), (1, 0, 2))
+        h = moe.gelu(h)
+        return gmm(wd, np.ascontiguousarray(np.transpose(h, (1, 0, 2))), **kw)
+
     t0 = time.perf_counter()
-    xt = np.ascontiguousarray(np.transpose(xs, (1, 0, 2)))
-    h = np.transpose(gm(wu, xt), (1, 0, 2))
-    h = moe.gelu(h)
-    ht = np.ascontiguousarray(np.transpose(h, (1, 0, 2)))
-    y = np.transpose(gm(wd, ht), (1, 0, 2))
+    ffn(gm, xs)
     t_ffn = time.perf_counter() - t0
-    del y
-    per_row = t_ffn / sample_rows
-    t_layer = t_rdc + per_row * N * k
-    # the C restatement with OpenMP on every host core this process may use, on 8x the rows
-    threads = len(os.sched_getaffinity(0))
-    rows_p = min(8 * sample_rows, N * k)
-    xs_p = np.ascontiguousarray(np.transpose(np.resize(x, (rows_p, d, 8)), (1, 0, 2)))
+    t_layer = t_rdc + t_ffn / rows * P
+    how = (f"the expert FFN on all {P} token-expert rows" if full else
+           f"the expert FFN on {rows} of {P} token-expert rows, extrapolated linearly in FLOPs")
+    res = dict(value=N / (layers * t_layer), unit="tokens/s", cores=1, kind=kind, dtype="f32",
+               sample=(f"{config_label(c)} config, computed in fp32: {how} via {what}, measured {t_ffn:.2f} s; "
+                       f"NumPy routing / dispatch / "
+                       f"combine over all {N} tokens ({t_rdc:.2f} s)"
+                       + (f"; one layer timed, the {layers}-layer step is {layers} x that" if layers > 1 else "")),
+               host=host)
+
+    # the NumPy broadcast fallback: per CliffordLinear, the pairwise geometric product over a
+    # broadcast (d_out, d_in, rows, 8) then the sum over d_in, a few rows at a time
+    def gm_broadcast(a, b):
+        return np.stack([geom_prod(a[:, :, None, :], b[None, :, j:j + 1, :]).sum(axis=1)[:, 0]
+                         for j in range(b.shape[1])], axis=1)
+
+    rows_np = 2
     t0 = time.perf_counter()
-    hp = np.transpose(native.c_geom_matmul(wu, xs_p, threads=threads), (1, 0, 2))
-    hp = moe.gelu(hp)
-    native.c_geom_matmul(wd, np.ascontiguousarray(np.transpose(hp, (1, 0, 2))), threads=threads)
+    ffn(gm_broadcast, xs[:rows_np])
+    t_np = time.perf_counter() - t0
+    res["numpy_fallback"] = dict(
+        value=N / (layers * (t_rdc + t_np / rows_np * P)), unit="tokens/s", cores=1, kind="port", dtype="f32",
+        sample=(f"the reference's NumPy fallback (broadcast pairwise geometric product, then sum over d_in; "
+                f"rune/ops/batched.py:341-344) on {rows_np} rows, measured {t_np:.2f} s, same extrapolation"))
+    # the C restatement with OpenMP on every host core this process may use
+    threads = host["affinity"]
+    rows_p = min(8 * rows, P)
+    t0 = time.perf_counter()
+    ffn(native.c_geom_matmul, np.resize(x, (rows_p, d, 8)), threads=threads)
     t_par = time.perf_counter() - t0
-    host = dict(nproc=os.cpu_count(), affinity=threads, cpu=_cpu_model(),
-                env={k_: os.environ[k_] for k_ in ("OMP_NUM_THREADS", "MKL_NUM_THREADS", "OPENBLAS_NUM_THREADS")
-                     if k_ in os.environ})
-    return dict(value=N / t_layer, unit="tokens/s", cores=1, kind=kind,
-                sample=(f"{config_label(c)}: expert FFN on {sample_rows} of {N * k} token-expert rows via {what}, "
-                        f"extrapolated linearly in FLOPs; NumPy routing/dispatch/combine over all {N} tokens "
-                        f"({t_rdc:.2f} s); measured {t_ffn:.1f} s"),
-                parallel=dict(value=N / (t_rdc + t_par / rows_p * N * k), unit="tokens/s", cores=threads, kind="port",
-                              sample=(f"oracle C restatement of cl3_batch_geom_matmul with OpenMP on {threads} "
-                                      f"threads, {rows_p} rows, measured {t_par:.2f} s, same extrapolation")),
-                host=host)
+    res["parallel"] = dict(value=N / (layers * (t_rdc + t_par / rows_p * P)), unit="tokens/s", cores=threads,
+                           kind="port", dtype="f32",
+                           sample=(f"oracle C restatement of cl3_batch_geom_matmul with OpenMP on {threads} "
+                                   f"threads, {rows_p} rows, measured {t_par:.2f} s, same extrapolation"))
+    return res
 
 
 def _cpu_model():
@@ -574,6 +675,9 @@ def config_label(c):
 
 def main():
     args = parse()
+    if args.pin:
+        write_pin(args.pin)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU is design-only: "
                                    "tokens shard with no exchange, experts with one all-to-all each way)"}))
@@ -615,9 +719,14 @@ def main():
     head_name = "c3" if "c3" in results else names[0]
     head = results[head_name]
     cpu = None
-    if not args.no_cpu_baseline and head_name != "c2":
-        print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(CONFIGS[head_name], args.cpu_sample_rows)
+    if not args.no_cpu_baseline:
+        # the reference CPU path for every BASELINE config in this run (the training, block and
+        # expert-parallel variants have none)
+        for name in names:
+            if name in ("c1", "c2", "c3", "c4", "c5"):
+                print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)
+                results[name]["cpu_baseline"] = cpu_baseline(name, CONFIGS[name], args.cpu_sample_rows)
+        cpu = results[head_name].get("cpu_baseline")
     roof = None
     if "_flops_per_launch" in head:
         ach = head["_flops_per_launch"] / (head["_ms_per_launch"] * 1e-3)
@@ -628,13 +737,18 @@ def main():
                     achieved=ach / 1e12, peak=peak / 1e12, unit="TFLOP/s", frac=ach / peak, traffic=None)
         if pauli:
             # achieved counts the algorithmic 64 multiply-adds per multivector pair; the complex
-            # (Pauli) form issues 32, so the MFMA pipes run at half that rate
+            # (Pauli) form issues 32, so frac can reach 2 and the MFMA pipes run at half of it
+            roof["frac_basis"] = "algorithmic FLOPs (64 multiply-adds per multivector pair); issued = frac / 2"
             roof["mfma_issued_frac"] = ach / 2 / peak
-            if head_name == "c3":
-                # HBM bytes per launch (mean of the two products) from rocprofv3 FETCH_SIZE x 2 +
-                # WRITE_SIZE, calibrated on a device copy: profiles/pauli_gemm_c3_traffic.md
-                roof["traffic"] = PAULI_C3_TRAFFIC_BYTES
-                roof["traffic_unit"] = "bytes per launch"
+        pin = pinned(f"{kern}_{head_name}")
+        if pin is not None:
+            # HBM bytes per launch (mean of the two products, rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by
+            # a device copy) and SQ_VALU_MFMA_BUSY_CYCLES, measured on this kernel build
+            roof["traffic"] = pin["traffic_bytes_per_launch"]
+            roof["traffic_unit"] = "bytes per launch"
+            if "mfma_busy" in pin:
+                roof["mfma_busy_counter"] = pin["mfma_busy"]
+            roof["counters_from"] = pin["profile"]
     for r in results.values():
         r.pop("_flops_per_launch", None)
         r.pop("_ms_per_launch", None)
