@@ -45,7 +45,8 @@ PEAK_HBM = 8.0e12  # bytes/s
 # names the sources it was measured on and their SHA-256, and is used only while they match
 PINS = os.path.join(ROOT, "profiles", "pins.json")
 WGRAD_MFMA_ROWS_PER_EXPERT = 256  # as ygg_moe_backward: mean rows per expert from which it uses the MFMA kernel
-SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5}
+SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5,
+         "gm": 6}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
@@ -71,6 +72,9 @@ CONFIGS = {
     "c3ep": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, ep=8),
     # the FFN half of the block around config 3: x + moe(ffn_norm(x)) (pre-norm, residual)
     "c3b": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="pauli", logits="zipf", layers=1, block=True),
+    # the operator boundary geom_matmul (fp32) at CliffordLinear's config 3 shapes: the up
+    # projection W (512, 128) on 8192 token columns, and the down projection (128, 512)
+    "gm": dict(N=8192, d=128, E=1, k=1, F=512, dtype="f32", fmt=None, logits=None, layers=1, gm=True),
 }
 
 
@@ -79,7 +83,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b,c3ep,c1t,c3t")
+    ap.add_argument("--configs", default="c3,c1,c2,c4,c5,c3b,c3ep,c1t,c3t,gm")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=256)
     # a plain device copy of this many MiB, run (3 times) before the configs: the reference
@@ -499,6 +503,27 @@ def run_train_config(torch, ops, name, c, steps, warmup):
                                              if wg_kind == "mfma" else None))
 
 
+def run_gm(torch, ops, name, c, steps, warmup):
+    """geom_matmul at CliffordLinear's shapes, buffers reused across calls (the workspace entry)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEEDS[name])
+    N, d, F = c["N"], c["d"], c["F"]
+    res = dict(workload=name, dtype="f32", kernels=["pauli_f32_prep_kernel", "pauli_f32_rows_t_kernel",
+                                                    "pauli_f32_kernel"])
+    for tag, M, K in (("up", F, d), ("down", d, F)):
+        a = torch.randn(M, K, 8, generator=g, device="cuda") / (8.0 * K) ** 0.5
+        b = torch.randn(K, N, 8, generator=g, device="cuda")
+        ws = torch.empty(ops.geom_matmul_workspace_bytes(M, K, N), device="cuda", dtype=torch.uint8)
+        out = torch.empty((M, N, 8), device="cuda")
+        ms = time_fn(torch, lambda: ops.geom_matmul(a, b, workspace=ws, out=out), steps, warmup)
+        flops = 128.0 * M * K * N  # algorithmic: 64 multiply-adds per multivector pair
+        res[tag] = dict(M=M, K=K, N=N, ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
+                        algorithmic_frac_f32=flops / (ms * 1e-3) / PEAK_F32,
+                        issued_frac_f32=flops / 2 / (ms * 1e-3) / PEAK_F32)
+        del a, b, ws, out
+    return res
+
+
 def calibrate_gemm(torch):
     """hipBLASLt (torch.matmul) bf16 GEMM rates on N(0,1) operands, two timed passes per shape."""
     out = []
@@ -707,6 +732,8 @@ def main():
         print(f"[bench] {name} {config_label(c)}", file=sys.stderr, flush=True)
         if name == "c2":
             results[name] = run_c2(torch, ops, c, args.steps, args.warmup)
+        elif c.get("gm"):
+            results[name] = run_gm(torch, ops, name, c, args.steps, args.warmup)
         elif c.get("ep"):
             results[name] = run_ep_config(torch, ops, name, c, args.steps, args.warmup)
         elif c.get("train"):
@@ -716,7 +743,8 @@ def main():
         else:
             results[name] = run_layer_config(torch, ops, name, c, args.steps, args.warmup)
         torch.cuda.empty_cache()
-    head_name = "c3" if "c3" in results else names[0]
+    # the headline: config 3 when it ran, else the first config that has a token rate
+    head_name = "c3" if "c3" in results else next((n for n in names if "tokens_per_s" in results[n]), names[0])
     head = results[head_name]
     cpu = None
     if not args.no_cpu_baseline:
@@ -755,19 +783,20 @@ def main():
     c = CONFIGS[head_name]
     line = {
         "metric": "MoE-HLM layer tokens/sec (prefill+decode) at 1 GPU; % of MFMA/HBM roofline",
-        "value": head["tokens_per_s"],
+        "value": head.get("tokens_per_s"),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["ms_per_step"],
+        "ms_per_step": head.get("ms_per_step"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16" if c["dtype"] == "bf16" else "f32",
         "data": "synthetic (seeded; random-init weights ~N(0, 1/sqrt(8 fan_in)))",
-        "config": {"workload": f"BASELINE config {head_name[1]}: MoE-HLM layer, " + config_label(c)
-                   + (", Zipf(1.2) expert load" if c["logits"] == "zipf" else ""),
+        "config": {"workload": (f"BASELINE config {head_name[1]}: MoE-HLM layer, " + config_label(c)
+                                + (", Zipf(1.2) expert load" if c["logits"] == "zipf" else ""))
+                   if head_name in ("c1", "c2", "c3", "c4", "c5") else f"{head_name}: " + config_label(c),
                    "tokens": c["N"], "d": c["d"], "experts": c["E"], "top_k": c["k"], "d_ff": c["F"],
                    "parallelism": "single GPU"},
         "roofline": roof,

@@ -49,8 +49,16 @@ int ygg_version(void);
  * bound at rune/bindings/mjolnir_cuda_ffi.py:127-128,505-525) and
  * cl3_geom_matmul_flat (mjolnir/src/cpu/batch_ops.c:165-172, declared
  * mjolnir/include/cl3_ops.h:210, bound at rune/bindings/mjolnir_ffi.py:208-209).
- * Unlike those, it reports errors and takes the stream explicitly. */
+ * Unlike those, it reports errors and takes the stream explicitly.  Computed as
+ * one fp32 Pauli MFMA product (a as the weight of a single expert, the columns
+ * of b as its rows); its scratch (the converted operands) is taken from the
+ * device's stream-ordered pool for the call. */
 int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K, int N, ygg_stream_t stream);
+/* The same with the caller's workspace of at least
+ * ygg_geom_matmul_f32_workspace_bytes(M, K, N) bytes (no allocation). */
+size_t ygg_geom_matmul_f32_workspace_bytes(int M, int K, int N);
+int ygg_geom_matmul_f32_ws(const float* a, const float* b, float* out, int M, int K, int N, void* workspace,
+                           size_t workspace_bytes, ygg_stream_t stream);
 
 /* ---- router --------------------------------------------------------------
  * Grade-energy logits of CliffordRouter (holograph/layers/clifford_router.py:

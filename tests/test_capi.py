@@ -302,3 +302,28 @@ def test_noalloc_entry_refuses_oversized_calls_before_touching_a_device():
     assert b"bad sizes" in L.ygg_last_error()
     # a decode-sized layer fits
     assert L.ygg_moe_workspace_bytes(64, 128, 512, 32, 2, 1, 2) <= limit
+
+
+def test_geom_matmul_workspace_checks_before_touching_a_device():
+    """The workspace form of the operator boundary sizes its scratch on the host and refuses a
+    short workspace (or operands past 2^31 floats) with -1 and a message, before any launch."""
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+    M, K, N = 512, 128, 8192
+    need = L.ygg_geom_matmul_f32_workspace_bytes(M, K, N)
+    rnd = lambda b: (b + 255) // 256 * 256
+    assert need == rnd(M * K * 64) + rnd(N * K * 32) + 256
+    assert L.ygg_geom_matmul_f32_workspace_bytes(0, K, N) == 0
+    fake = 1 << 20  # never dereferenced: every check below fails first
+    assert L.ygg_geom_matmul_f32_ws(fake, fake, fake, M, K, N, fake, need - 1, None) == -1
+    assert b"workspace" in L.ygg_last_error()
+    assert L.ygg_geom_matmul_f32_ws(fake, fake, fake, M, K, N, None, need, None) == -1
+    assert L.ygg_geom_matmul_f32_ws(fake, fake, fake, 4, 1 << 20, 1 << 10, fake, 1 << 40, None) == -1
+    assert b"2^31" in L.ygg_last_error()
+    assert L.ygg_geom_matmul_f32_ws(fake, fake, fake, -1, K, N, fake, need, None) == -1
+    assert L.ygg_geom_matmul_f32_ws(None, fake, fake, M, K, N, fake, need, None) == -1
+    # empty outputs are a no-op that touches nothing
+    assert L.ygg_geom_matmul_f32_ws(None, None, None, 0, K, N, None, 0, None) == 0

@@ -22,6 +22,8 @@ SIGNATURES = {
     "ygg_last_error": (ctypes.c_char_p, []),
     "ygg_version": (_c_int, []),
     "ygg_geom_matmul_f32": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]),
+    "ygg_geom_matmul_f32_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
+    "ygg_geom_matmul_f32_ws": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size, _vp]),
     "ygg_router_head_logits": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _vp]),
     "ygg_router_energy_logits": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "ygg_route_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),

@@ -793,35 +793,6 @@ __global__ __launch_bounds__(256) void grouped_cl_f32(const float* __restrict__ 
   }
 }
 
-// ---------------------------------------------------------------------------
-// plain geometric matmul operator (blade order, fp32)
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void geom_matmul_kernel(const float* __restrict__ a, const float* __restrict__ b,
-                                                          float* __restrict__ out, int M, int K, int N) {
-  const int n = blockIdx.x * 64 + (threadIdx.x & 63);
-  const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
-  if (m >= M || n >= N) return;
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int k = 0; k < K; ++k) {
-    const float4* pa = reinterpret_cast<const float4*>(a + ((size_t)m * K + k) * 8);
-    const float4* pb = reinterpret_cast<const float4*>(b + ((size_t)k * N + n) * 8);
-    const float4 a0 = pa[0], a1 = pa[1], b0 = pb[0], b1 = pb[1];
-    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-    for (int p = 0; p < 8; ++p)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int mp = blade_to_mask(p), mq = blade_to_mask(q);
-        const int o = mask_to_blade(mp ^ mq);
-        acc[o] = fmaf((float)mask_product_sign(mp, mq) * av[p], bv[q], acc[o]);
-      }
-  }
-  float4* po = reinterpret_cast<float4*>(out + ((size_t)m * N + n) * 8);
-  po[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  po[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
-}
-
 }  // namespace ygg
 
 using namespace ygg;
@@ -1037,12 +1008,4 @@ int ygg::decode_linear_partial(const uint16_t* x, int P_max, const int8_t* Wq, c
   return check_launch("grouped_cl_decode_i8 (K split)");
 }
 
-// Operator boundary of the path: out[m, n] = sum_k gp(a[m, k], b[k, n]).
-YGG_API int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K, int N, hipStream_t stream) {
-  YGG_CHECK_ARG(M >= 0 && K >= 0 && N >= 0, "ygg_geom_matmul_f32: bad sizes");
-  if (M == 0 || N == 0) return 0;
-  YGG_CHECK_ARG(a && b && out, "ygg_geom_matmul_f32: null pointer");
-  dim3 grid((N + 63) / 64, (M + 3) / 4);
-  geom_matmul_kernel<<<grid, 256, 0, stream>>>(a, b, out, M, K, N);
-  return check_launch("geom_matmul");
-}
+

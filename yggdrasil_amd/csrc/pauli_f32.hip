@@ -48,7 +48,10 @@ constexpr int kF32Cols = 32;  // output multivectors per tile
 constexpr int kF32U = 4;      // input multivectors per register-buffered block of the K loop
 constexpr long long kF32TwoBlockMinGroups = 2048;  // 32-token tiles from this many workgroups (8 per CU)
 
-enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2 };
+// output layouts: Pauli rows (for the next product), blade rows (row, d_out), fp32
+// partial planes, and blade columns (d_out, rows) -- the transposed product geom_matmul
+// returns
+enum PauliF32Out : int { kF32OutPauliRows = 0, kF32OutBlade = 1, kF32OutPartial = 2, kF32OutBladeT = 3 };
 
 template <int TOK>  // tokens per tile
 __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E, int tile, int& e, int& row0,
@@ -171,7 +174,7 @@ __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y0
     q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
     q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
   } else {
-    size_t mv = (size_t)row * d_out + j;
+    size_t mv = OUT == kF32OutBladeT ? (size_t)j * P_max + row : (size_t)row * d_out + j;
     if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
     else activate_blade<ACT>(y);
     float4* p = reinterpret_cast<float4*>(Y + mv * 8);
@@ -323,6 +326,42 @@ __global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const floa
   q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
 }
 
+// b (K, N, 8) fp32 blade -> Pauli rows of its transpose (N, K): row n holds b[:, n].
+// Tiles of 32 columns n x 8 rows k pass through LDS, so both the reads (32
+// consecutive n of one k) and the writes (8 consecutive k of one n) are contiguous.
+// Thread 0 of workgroup 0 also writes the one-expert offsets {0, N}.
+__global__ __launch_bounds__(256) void pauli_f32_rows_t_kernel(const float* __restrict__ b, int K, int N,
+                                                               float* __restrict__ out, int32_t* __restrict__ offsets) {
+  __shared__ float4 tile[8][32][2];
+  const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 8, t = threadIdx.x;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && t == 0) {
+    offsets[0] = 0;
+    offsets[1] = N;
+  }
+  {
+    const int kk = t >> 5, nn = t & 31, k = k0 + kk, n = n0 + nn;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (k < K && n < N) {
+      const float4 p0 = reinterpret_cast<const float4*>(b + ((size_t)k * N + n) * 8)[0];
+      const float4 p1 = reinterpret_cast<const float4*>(b + ((size_t)k * N + n) * 8)[1];
+      v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w; v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+    }
+    float c0[4], c1[4];
+    blade_to_pauli(v, c0, c1);
+    tile[kk][nn][0] = make_float4(c0[0], c0[2], c0[1], c0[3]);  // [b][k][c], as blade_to_pauli_f32_rows_kernel
+    tile[kk][nn][1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+  }
+  __syncthreads();
+  {
+    const int nn = t >> 3, kk = t & 7, k = k0 + kk, n = n0 + nn;
+    if (k < K && n < N) {
+      float4* q = reinterpret_cast<float4*>(out + ((size_t)n * K + k) * 8);
+      q[0] = tile[kk][nn][0];
+      q[1] = tile[kk][nn][1];
+    }
+  }
+}
+
 }  // namespace ygg
 
 using namespace ygg;
@@ -439,4 +478,67 @@ YGG_API int ygg_pauli_grouped_linear_f32(const float* x, const int32_t* gather, 
   if (y_layout == kF32OutPauliRows)
     return launch_f32_act<kF32OutPauliRows>(act, 1, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
   return launch_f32_act<kF32OutBlade>(act, 1, stream, x, gather, w, bias, offsets, E, d_in, d_out, P_max, y);
+}
+
+// ---------------------------------------------------------------------------
+// geom_matmul: out[m, n] = sum_k a[m, k] b[k, n] as one fp32 Pauli product --
+// a is the weight (d_out = M, d_in = K) of a single expert, the columns of b are
+// the rows, and the output is written transposed, straight into (M, N, 8).
+// ---------------------------------------------------------------------------
+
+namespace {
+__global__ __launch_bounds__(256) void gm_zero_kernel(float* __restrict__ out, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) out[i] = 0.f;
+}
+
+constexpr size_t kGmAlign = 256;
+size_t gm_align(size_t n) { return (n + kGmAlign - 1) / kGmAlign * kGmAlign; }
+size_t gm_w_bytes(int M, int K) { return gm_align((size_t)M * K * 2 * 8 * sizeof(float)); }
+size_t gm_x_bytes(int K, int N) { return gm_align((size_t)N * K * 8 * sizeof(float)); }
+}  // namespace
+
+YGG_API size_t ygg_geom_matmul_f32_workspace_bytes(int M, int K, int N) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return gm_w_bytes(M, K) + gm_x_bytes(K, N) + kGmAlign;
+}
+
+YGG_API int ygg_geom_matmul_f32_ws(const float* a, const float* b, float* out, int M, int K, int N, void* workspace,
+                                   size_t workspace_bytes, hipStream_t stream) {
+  YGG_CHECK_ARG(M >= 0 && K >= 0 && N >= 0, "ygg_geom_matmul_f32: bad sizes M=%d K=%d N=%d", M, K, N);
+  if (M == 0 || N == 0) return 0;
+  YGG_CHECK_ARG(out, "ygg_geom_matmul_f32: null output");
+  if (K == 0) {  // an empty sum (a fill kernel, no memset node, so that the call can be captured)
+    const size_t n = (size_t)M * N * 8;
+    gm_zero_kernel<<<(unsigned)std::min<size_t>((n + 255) / 256, 65535), 256, 0, stream>>>(out, n);
+    return check_launch("geom_matmul (K = 0)");
+  }
+  YGG_CHECK_ARG(a && b, "ygg_geom_matmul_f32: null input");
+  YGG_CHECK_ARG((size_t)N * K * 8 < ((size_t)1 << 31) && (size_t)M * K * 16 < ((size_t)1 << 31),
+                "ygg_geom_matmul_f32: operands of 2^31 floats or more (M=%d K=%d N=%d)", M, K, N);
+  const size_t need = ygg_geom_matmul_f32_workspace_bytes(M, K, N);
+  YGG_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                "ygg_geom_matmul_f32: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  char* ws = static_cast<char*>(workspace);
+  float* wp = reinterpret_cast<float*>(ws);
+  float* xp = reinterpret_cast<float*>(ws + gm_w_bytes(M, K));
+  int32_t* off = reinterpret_cast<int32_t*>(ws + gm_w_bytes(M, K) + gm_x_bytes(K, N));
+  if (pauli_f32_prepare_weights(a, 1, M, K, wp, stream)) return -1;
+  const dim3 tgrid((unsigned)((N + 31) / 32), (unsigned)((K + 7) / 8));
+  pauli_f32_rows_t_kernel<<<tgrid, 256, 0, stream>>>(b, K, N, xp, off);
+  if (check_launch("pauli_f32_rows_t")) return -1;
+  return launch_f32_act<kF32OutBladeT>(kActNone, 1, stream, xp, nullptr, wp, nullptr, off, 1, K, M, N, out);
+}
+
+YGG_API int ygg_geom_matmul_f32(const float* a, const float* b, float* out, int M, int K, int N, hipStream_t stream) {
+  YGG_CHECK_ARG(M >= 0 && K >= 0 && N >= 0, "ygg_geom_matmul_f32: bad sizes M=%d K=%d N=%d", M, K, N);
+  const size_t need = ygg_geom_matmul_f32_workspace_bytes(M, K, N);
+  if (need == 0) return ygg_geom_matmul_f32_ws(a, b, out, M, K, N, nullptr, 0, stream);
+  void* ws = nullptr;  // stream-ordered, returned to the pool after the product
+  const hipError_t me = hipMallocAsync(&ws, need, stream);
+  YGG_CHECK_ARG(me == hipSuccess, "ygg_geom_matmul_f32: workspace of %zu bytes: %s", need, hipGetErrorString(me));
+  const int rc = ygg_geom_matmul_f32_ws(a, b, out, M, K, N, ws, need, stream);
+  const hipError_t fe = hipFreeAsync(ws, stream);
+  if (rc) return rc;
+  YGG_CHECK_ARG(fe == hipSuccess, "ygg_geom_matmul_f32: freeing the workspace: %s", hipGetErrorString(fe));
+  return 0;
 }

@@ -238,6 +238,15 @@ class CliffordMoELayer(nn.Module):
         out = self.moe_forward(x4, logits=logits)
         return (out.reshape(x.shape) if flat_in else out), self.aux_loss()
 
+    def experts(self, x_sorted: torch.Tensor, expert_offsets: torch.Tensor,
+                expert_counts: torch.Tensor) -> torch.Tensor:
+        """geoformer's grouped-expert interface (``FusedMoEExperts.forward``,
+        ``geoformer/triton_kernels/fused_expert.py:306-331``) over this layer's
+        experts: rows already sorted by expert -> y_sorted (forward only)."""
+        prep = self._get_prepared()
+        return ops.grouped_experts(x_sorted, expert_offsets, expert_counts, prep["w_up"], prep["w_down"],
+                                   prep["b_up"], prep["b_down"], self.cfg.activation)
+
     def aux_loss(self) -> torch.Tensor:
         """CliffordRouter.load_balance_loss (clifford_router.py:108-117) on this call's counts.
 

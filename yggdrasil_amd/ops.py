@@ -68,20 +68,39 @@ def _check_layer_args(x, k, E, F, logits=None, residual=None, router_weight=None
 # ---------------------------------------------------------------------------
 
 
-def geom_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+def geom_matmul_workspace_bytes(M: int, K: int, N: int) -> int:
+    return int(lib().ygg_geom_matmul_f32_workspace_bytes(M, K, N))
+
+
+def geom_matmul(a: torch.Tensor, b: torch.Tensor, *, workspace: torch.Tensor | None = None,
+                out: torch.Tensor | None = None) -> torch.Tensor:
     """``out[m, n] = sum_k gp(a[m, k], b[k, n])`` (fp32, blade order).
 
-    Drop-in for ``rune.ops.batched.geom_matmul`` (``rune/ops/batched.py:320-344``).
+    Drop-in for ``rune.ops.batched.geom_matmul`` (``rune/ops/batched.py:320-344``):
+    one fp32 Pauli MFMA product with ``a`` as the weight.  ``workspace`` (uint8,
+    at least :func:`geom_matmul_workspace_bytes`) and ``out`` may be given to reuse
+    buffers across calls; otherwise they are allocated here.
     """
     dev = _dev(a, b)
     if a.dtype != torch.float32 or b.dtype != torch.float32:
         raise ValueError("geom_matmul is fp32")
     if a.dim() != 3 or b.dim() != 3 or a.shape[2] != 8 or b.shape[2] != 8 or a.shape[1] != b.shape[0]:
         raise ValueError(f"shapes {tuple(a.shape)} x {tuple(b.shape)} do not form (M,K,8) x (K,N,8)")
+    a, b = a.contiguous(), b.contiguous()
     M, K, _ = a.shape
     Nn = b.shape[1]
-    out = torch.empty((M, Nn, 8), device=dev, dtype=torch.float32)
-    check(lib().ygg_geom_matmul_f32(ptr(a), ptr(b), ptr(out), M, K, Nn, stream_handle(dev)), "geom_matmul")
+    if out is None:
+        out = torch.empty((M, Nn, 8), device=dev, dtype=torch.float32)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (M, Nn, 8) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous float32 ({M}, {Nn}, 8) tensor")
+    need = geom_matmul_workspace_bytes(M, K, Nn)
+    if workspace is None:
+        workspace = torch.empty((max(need, 1),), device=dev, dtype=torch.uint8)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace of {workspace.numel() * workspace.element_size()} bytes, {need} needed")
+    check(lib().ygg_geom_matmul_f32_ws(ptr(a), ptr(b), ptr(out), M, K, Nn, ptr(workspace),
+                                       workspace.numel() * workspace.element_size(), stream_handle(dev)),
+          "geom_matmul")
     return out
 
 
@@ -388,6 +407,58 @@ def pauli_rows_from_blade(x: torch.Tensor) -> torch.Tensor:
     out = torch.empty((rows, 2, d, 4), device=dev, dtype=torch.bfloat16)
     check(lib().ygg_pauli_rows_from_blade(ptr(x), rows, d, ptr(out), stream_handle(dev)), "pauli_rows_from_blade")
     return out
+
+
+def grouped_experts(x_sorted: torch.Tensor, expert_offsets: torch.Tensor, expert_counts: torch.Tensor,
+                    w_up: PreparedWeights, w_down: PreparedWeights, b_up: torch.Tensor | None = None,
+                    b_down: torch.Tensor | None = None, act: str = "gelu", validate: bool = False) -> torch.Tensor:
+    """Every expert's CliffordFFN on rows already grouped by expert: ``y_sorted``.
+
+    The grouped-expert boundary of geoformer's ``FusedMoEExperts.forward(x_sorted,
+    expert_offsets, expert_counts) -> y_sorted``
+    (``geoformer/triton_kernels/fused_expert.py:306-331``), with this layer's expert
+    (``CliffordFFN.forward``, ``holograph/models/hlm_block.py:55-61``: up product with
+    bias and the grade-wise activation, then the down product with bias).
+
+    x_sorted: (P, d, 8) blade order, or (P, 8 d) as geoformer passes it; the rows of
+    expert e are ``expert_offsets[e] .. + expert_counts[e]``, the experts' ranges
+    contiguous and ascending from row 0 (as a sort by expert leaves them).  Weights
+    and biases are prepared (:func:`prepare_weights`, :func:`prepare_bias`); the
+    weight format picks the products (bf16 / fp32 Pauli, or the L(w) blocks).
+    ``validate`` checks the ranges on the host (one synchronisation).
+    Returns y_sorted in x_sorted's shape and dtype.
+    """
+    dev = _dev(x_sorted, expert_offsets, expert_counts, b_up, b_down)
+    E, d, F = w_up.E, w_up.d_in, w_up.d_out
+    if (w_down.E, w_down.d_in, w_down.d_out, w_down.fmt) != (E, F, d, w_up.fmt):
+        raise ValueError("w_down must be (E, d, F) in w_up's format")
+    flat = x_sorted.dim() == 2
+    x = x_sorted.reshape(x_sorted.shape[0], d, 8) if flat else x_sorted
+    if x.dim() != 3 or tuple(x.shape[1:]) != (d, 8):
+        raise ValueError(f"x_sorted must be (P, {d}, 8) or (P, {8 * d}), got {tuple(x_sorted.shape)}")
+    if expert_offsets.shape != (E,) or expert_counts.shape != (E,):
+        raise ValueError(f"expert_offsets and expert_counts must have shape ({E},)")
+    x = x.contiguous()
+    P = x.shape[0]
+    offs = torch.cat([expert_offsets.reshape(E), (expert_offsets[-1:] + expert_counts[-1:])]).to(torch.int32)
+    if validate:
+        o, c = expert_offsets.long().cpu(), expert_counts.long().cpu()
+        if int(o[0]) != 0 or bool((c < 0).any()) or bool((o[1:] != o[:-1] + c[:-1]).any()) or int(o[-1] + c[-1]) != P:
+            raise ValueError("expert ranges must be contiguous, ascending and cover the rows from 0")
+    if P == 0:
+        return x_sorted.clone()
+    fmt = w_up.fmt
+    if fmt == "pauli":
+        h = pauli_grouped_linear(x, w_up, offs, b_up, act, x_layout="blade", y_layout="pauli")
+        y = pauli_grouped_linear(h, w_down, offs, b_down, "none", x_layout="pauli", y_layout="blade",
+                                 out_dtype=x.dtype)
+    elif fmt == "pauli_f32":
+        h = pauli_grouped_linear_f32(pauli_rows_from_blade_f32(x), w_up, offs, b_up, act, y_layout="pauli")
+        y = pauli_grouped_linear_f32(h, w_down, offs, b_down, "none", y_layout="blade")
+    else:  # L(w) blocks read and write mask order between the products
+        h = grouped_clifford_linear(to_mask_order(x), w_up, offs, b_up, act, out_blade_order=False)
+        y = grouped_clifford_linear(h, w_down, offs, b_down, "none", out_dtype=x.dtype, out_blade_order=True)
+    return y.reshape(x_sorted.shape) if flat else y
 
 
 def moe_workspace_bytes(Nt: int, d: int, F: int, E: int, k: int, dtype: torch.dtype, fmt: str) -> int:
