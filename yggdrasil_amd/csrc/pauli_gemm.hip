@@ -53,6 +53,8 @@
 // Activation rows are gathered through the expert-grouped row index, which
 // fuses the dispatch copy into the up projection.
 
+#include <type_traits>
+
 #include "pauli_common.h"
 
 namespace ygg {
@@ -84,6 +86,7 @@ struct PauliTile {
 
 struct PauliTileInfo {
   int e, row0, row_end, col0;
+  int half;  // -1: the whole tile; 0 / 1: only row block `half` of every wave
 };
 
 template <int ACT, int IN, int OUT, int OUT_DT, class TL>
@@ -118,11 +121,19 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   const int per_xcd = gridDim.x / n_xcd;
   const int xcd = blockIdx.x % n_xcd, slot = blockIdx.x / n_xcd;
   const int lo = (int)((long long)n_tiles * xcd / n_xcd), hi = (int)((long long)n_tiles * (xcd + 1) / n_xcd);
-  const int n_mine = (hi - lo > slot) ? (hi - lo - slot + per_xcd - 1) / per_xcd : 0;
+  // Whole rounds of per_xcd tiles first.  A remainder of at most per_xcd / 2 tiles
+  // would leave most workgroups idle while a few run one more tile, so each of those
+  // tiles is cut in two halves -- a half computes one of each wave's two row blocks --
+  // and the halves go to twice as many workgroups.
+  const int R = hi - lo, rounds = R / per_xcd, rem = R - rounds * per_xcd;
+  const bool split = WR == 2 && rem > 0 && 2 * rem <= per_xcd;
+  const int n_full = split ? rounds : (R > slot ? (R - slot + per_xcd - 1) / per_xcd : 0);
+  const int n_mine = n_full + ((split && slot < 2 * rem) ? 1 : 0);
   const int total = n_mine * nk;
 
-  auto decode = [&](int n) {  // n-th tile of this workgroup
-    const int L = lo + slot + n * per_xcd;
+  auto decode = [&](int n) __attribute__((always_inline)) {  // n-th tile of this workgroup
+    const bool half = n >= n_full;
+    const int L = half ? lo + rounds * per_xcd + (slot >> 1) : lo + slot + n * per_xcd;
     const int rt = L / CT, ct = L - rt * CT;
     int a = 0, b = E - 1;  // last expert with s_tbeg <= rt (experts with no tiles are skipped)
     while (a < b) {
@@ -135,6 +146,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
     t.row0 = s_off[a] + (rt - s_tbeg[a]) * T;
     t.row_end = s_off[a + 1];
     t.col0 = ct * BN;
+    t.half = half ? (slot & 1) : -1;
     return t;
   };
 
@@ -152,7 +164,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0,
                                                                           x_bytes, kBufferFlags);
   constexpr uint32_t kOff = 0x80000000u;  // reads zero
-  PauliTileInfo ld = {0, 0, 1, 0};  // tile of the chunk being loaded
+  PauliTileInfo ld = {0, 0, 1, 0, -1};  // tile of the chunk being loaded
   __amdgpu_buffer_rsrc_t w_rsrc = x_rsrc;
   uint32_t a_row[A_PER];  // byte offset of each staged A item's row, fixed for a tile
   auto load_chunk = [&](int f, uint4 (&ra)[A_PER], uint4 (&rw)[W_PER]) {
@@ -229,7 +241,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   };
 
   pf32x16_t acc[WR][WC][2][2];
-  auto zero_acc = [&]() {
+  auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int a = 0; a < WR; ++a)
 #pragma unroll
@@ -242,15 +254,18 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
             for (int v = 0; v < 16; ++v) acc[a][b][c][d][v] = 0.f;
   };
 
-  auto compute_chunk = [&](int buf) {
+  // NR row blocks per wave from row block rb0 on (NR = WR for a whole tile; a half
+  // tile computes NR = 1 block, rb0 = its half, into the first accumulators)
+  auto compute_chunk = [&](int buf, auto nr_tag, int rb0) __attribute__((always_inline)) {
+    constexpr int NR = decltype(nr_tag)::value;
     const unsigned char* As = smem + buf * TL::STAGE;
     const unsigned char* Ws = As + TL::A_BYTES;
 #pragma unroll
     for (int s = 0; s < KC / 4; ++s) {
       uint4 av[WR], wv[WC][2];
 #pragma unroll
-      for (int rb = 0; rb < WR; ++rb) {
-        const int row = (wt * WR + rb) * 32 + l32;
+      for (int rb = 0; rb < NR; ++rb) {
+        const int row = (wt * WR + rb0 + rb) * 32 + l32;
         av[rb] = *reinterpret_cast<const uint4*>(As + row * TL::A_STRIDE + (4 * s + 2 * g) * 8);
       }
 #pragma unroll
@@ -261,7 +276,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
           wv[cb][a] = *reinterpret_cast<const uint4*>(Ws + col * TL::W_STRIDE + (2 * s + g) * 32 + a * 16);
       }
 #pragma unroll
-      for (int rb = 0; rb < WR; ++rb) {
+      for (int rb = 0; rb < NR; ++rb) {
         const uint4 ap = make_uint4(rot_conj(av[rb].x), rot_conj(av[rb].y), rot_conj(av[rb].z), rot_conj(av[rb].w));
         const pbf16x8_t A0 = __builtin_bit_cast(pbf16x8_t, av[rb]);
         const pbf16x8_t A1 = __builtin_bit_cast(pbf16x8_t, ap);
@@ -282,7 +297,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(bias), (short)0, bias ? (uint32_t)E * d_out * 32 : 0u, kBufferFlags);
   float bvs[WC][8];
-  auto load_bias = [&](const PauliTileInfo& ti) {
+  auto load_bias = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
 #pragma unroll
     for (int cb = 0; cb < WC; ++cb) {
       const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
@@ -295,7 +310,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
   };
 
-  auto epilogue = [&](const PauliTileInfo& ti) {
+  auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
 #pragma unroll
     for (int cb = 0; cb < WC; ++cb) {
       const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
@@ -303,11 +318,13 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
       const float* bv = bvs[cb];
 #pragma unroll
       for (int rb = 0; rb < WR; ++rb) {
+        if (ti.half >= 0 && rb > 0) break;  // a half tile: the first accumulators hold block `half`
+        const int rbr = ti.half >= 0 ? ti.half : rb;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const int t = (wt * WR + rb) * 16 + 4 * q + 2 * g + h;
+            const int t = (wt * WR + rbr) * 16 + 4 * q + 2 * g + h;
             const int row = ti.row0 + t;
             if (row >= ti.row_end) continue;
             const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
@@ -354,22 +371,27 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
     store_chunk(0, ra, rw);
   }
   __syncthreads();
-  PauliTileInfo cur = {0, 0, 1, 0};  // tile being computed
-  for (int f = 0; f < total; ++f) {
+  PauliTileInfo cur = {0, 0, 1, 0, -1};  // tile being computed
+  auto step = [&](int f, auto nr_tag) __attribute__((always_inline)) {
     const int buf = f & 1;
     if (f % nk == 0) {
       cur = decode(f / nk);
       load_bias(cur);
     }
     if (f + 1 < total) load_chunk(f + 1, ra, rw);
-    compute_chunk(buf);
+    compute_chunk(buf, nr_tag, cur.half < 0 ? 0 : cur.half);
     if (f % nk == nk - 1) {
       epilogue(cur);
       zero_acc();
     }
     if (f + 1 < total) store_chunk(buf ^ 1, ra, rw);
     __syncthreads();
-  }
+  };
+  // the whole tiles, then the half tile (if any) in a loop of its own, so that the
+  // second row block's accumulators are dead there
+  int f = 0;
+  for (; f < n_full * nk; ++f) step(f, std::integral_constant<int, WR>{});
+  for (; f < total; ++f) step(f, std::integral_constant<int, 1>{});
 }
 
 // ---------------------------------------------------------------------------
