@@ -282,6 +282,97 @@ __global__ __launch_bounds__(256) void combine_planes_kernel(const float* __rest
   store_mv<OT>(out, n, acc);
 }
 
+// The same combine with PL planes known at compile time: one thread per half
+// multivector (four blade components, one 16-byte piece), so twice the threads,
+// and the loads of two slots x all planes issued together -- one wait for the
+// routing, one for the rows.  Same additions in the same order as above, so the
+// result is identical.
+template <int OT, bool RESID, int PL>
+__global__ __launch_bounds__(256) void combine_planes_half_kernel(const float* __restrict__ ys, int N, int k, int d,
+                                                                  const int32_t* __restrict__ topk_idx,
+                                                                  const float* __restrict__ topk_w,
+                                                                  const int32_t* __restrict__ slot_pos,
+                                                                  const void* __restrict__ resid,
+                                                                  void* __restrict__ out, size_t plane_stride) {
+#pragma clang fp contract(off)
+  const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= (size_t)N * d * 2) return;
+  const size_t mv = n >> 1;
+  const int half = (int)(n & 1);
+  const int t = (int)(mv / d), i = (int)(mv % d);
+  int ex[8], row[8];
+  float w[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
+    const size_t f = (size_t)t * k + min(s, k - 1);
+    const int e = topk_idx[f], rw = slot_pos[f];
+    const float ws = topk_w[f];
+    const bool on = s < k;
+    ex[s] = on ? e : 0x7fffffff;
+    row[s] = on ? rw : 0;
+    w[s] = on ? ws : 0.f;
+  }
+  float r[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (RESID) {
+    if constexpr (OT == kF32) {
+      const float4 q = reinterpret_cast<const float4*>(resid)[n];
+      r[0] = q.x; r[1] = q.y; r[2] = q.z; r[3] = q.w;
+    } else {
+      const uint2 q = reinterpret_cast<const uint2*>(resid)[n];
+      r[0] = bf16_bits_to_f32((uint16_t)(q.x & 0xffffu)); r[1] = bf16_bits_to_f32((uint16_t)(q.x >> 16));
+      r[2] = bf16_bits_to_f32((uint16_t)(q.y & 0xffffu)); r[3] = bf16_bits_to_f32((uint16_t)(q.y >> 16));
+    }
+  }
+#pragma unroll
+  for (int a = 1; a < 8; ++a)
+#pragma unroll
+    for (int b = a; b > 0; --b)
+      if (ex[b] < ex[b - 1]) {
+        int te = ex[b]; ex[b] = ex[b - 1]; ex[b - 1] = te;
+        int tr = row[b]; row[b] = row[b - 1]; row[b - 1] = tr;
+        float tw = w[b]; w[b] = w[b - 1]; w[b - 1] = tw;
+      }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < k; s0 += 2) {
+    float4 v[2][PL];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int su = min(s0 + u, k - 1);
+      int rs = row[0];  // row[su] without indexing the register array
+#pragma unroll
+      for (int q = 1; q < 8; ++q)
+        if (q == su) rs = row[q];
+#pragma unroll
+      for (int p = 0; p < PL; ++p)
+        v[u][p] = reinterpret_cast<const float4*>(ys + p * plane_stride + ((size_t)rs * d + i) * 8)[half];
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      if (s0 + u >= k) continue;
+      float y[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
+#pragma unroll
+      for (int p = 1; p < PL; ++p) {
+        y[0] = y[0] + v[u][p].x; y[1] = y[1] + v[u][p].y; y[2] = y[2] + v[u][p].z; y[3] = y[3] + v[u][p].w;
+      }
+      float ws = w[0];
+#pragma unroll
+      for (int s = 1; s < 8; ++s)
+        if (s == s0 + u) ws = w[s];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c] = acc[c] + ws * y[c];
+    }
+  }
+  if constexpr (RESID) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = r[c] + acc[c];
+  }
+  if constexpr (OT == kF32) {
+    reinterpret_cast<float4*>(out)[n] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  } else {
+    reinterpret_cast<uint2*>(out)[n] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+  }
+}
+
 }  // namespace ygg
 
 using namespace ygg;
@@ -321,8 +412,21 @@ int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int
                         const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
                         hipStream_t stream) {
   if (N == 0) return 0;
-  const unsigned grid = (unsigned)(((size_t)N * d + 255) / 256);
   const size_t stride = (size_t)P_max * d;
+  if (planes == 4 || planes == 8) {  // the decode layer's partial planes: the half-multivector kernel
+    const unsigned hgrid = (unsigned)(((size_t)N * d * 2 + 255) / 256);
+#define YGG_CH(OT, RS, PL)                                                                                          \
+  combine_planes_half_kernel<OT, RS, PL><<<hgrid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos, \
+                                                                     residual, out, stride * 8)
+#define YGG_CH2(PL)                                                                        \
+  if (out_dtype == kF32) { if (residual) YGG_CH(kF32, true, PL); else YGG_CH(kF32, false, PL); } \
+  else { if (residual) YGG_CH(kBF16, true, PL); else YGG_CH(kBF16, false, PL); }
+    if (planes == 8) { YGG_CH2(8) } else { YGG_CH2(4) }
+#undef YGG_CH2
+#undef YGG_CH
+    return check_launch("combine (partial planes)");
+  }
+  const unsigned grid = (unsigned)(((size_t)N * d + 255) / 256);
 #define YGG_CP(OT, RS)                                                                                            \
   combine_planes_kernel<OT, RS><<<grid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, \
                                                           out, planes, stride)
