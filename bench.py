@@ -24,7 +24,9 @@ built from the reference sources) -- or the C restatement if that is absent --
 plus the NumPy restatement of routing / dispatch / combine, on every row where
 that takes seconds and on a sample extrapolated linearly in FLOPs otherwise,
 with the reference's NumPy broadcast fallback and an OpenMP port beside it.
-The decode config (4) reports the fused layer's bytes per step against HBM.
+The decode config (4) reports the fused layer's bytes per step against HBM, timed as
+HIP graph replay of the steps (a Python loop of such short steps is host-bound; its
+figure is reported beside it as ms_per_step_eager).
 """
 
 from __future__ import annotations
@@ -45,8 +47,8 @@ PEAK_HBM = 8.0e12  # bytes/s
 # names the sources it was measured on and their SHA-256, and is used only while they match
 PINS = os.path.join(ROOT, "profiles", "pins.json")
 WGRAD_MFMA_ROWS_PER_EXPERT = 256  # as ygg_moe_backward: mean rows per expert from which it uses the MFMA kernel
-SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4, "c5": 5,
-         "gm": 6}
+SEEDS = {"c1": 1, "c1e": 1, "c1l": 1, "c1t": 1, "c2": 2, "c3": 3, "c3l": 3, "c3b": 3, "c3ep": 3, "c3t": 3, "c4": 4,
+         "c4l": 4, "c5": 5, "gm": 6}
 
 CONFIGS = {
     # name: N, d, E, k, F, dtype, weight format, logits kind, layers
@@ -62,7 +64,9 @@ CONFIGS = {
     "c3l": dict(N=8192, d=128, E=32, k=4, F=512, dtype="bf16", fmt="bf16", logits="zipf", layers=1),
     # decode: each step runs the layer with the next of 10 weight sets (335 MB, more than the 256 MB
     # Infinity Cache), so the weights stream from HBM as in a multi-layer decode step
-    "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1, rotate=10),
+    # (int8 Pauli weights: the one-launch decode layer); "c4l" the same with int8 L(w)-block weights
+    "c4": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8_pauli", logits="normal", layers=1, rotate=10),
+    "c4l": dict(N=64, d=128, E=32, k=2, F=512, dtype="bf16", fmt="int8", logits="normal", layers=1, rotate=10),
     "c5": dict(N=4096, d=256, E=64, k=2, F=1024, dtype="bf16", fmt="pauli", logits="normal_bias", layers=12),
     # training step (forward + backward, fp32 Pauli weights) at the config 1 and config 3 shapes
     "c1t": dict(N=256, d=64, E=8, k=2, F=256, dtype="f32", fmt="pauli_f32", logits="energy", layers=1, train=True),
@@ -238,18 +242,39 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
 
     all_sets = prepared
     if rot:  # one layer per step with weight set i mod rot; the warm figure reuses set 0 every step
-        prepared = all_sets[:1]
-        ms_warm = time_fn(torch, step, steps, warmup)
+        def layer(P):
+            _, rt = ops.moe_forward(x, k, P["w_up"], P["w_down"], None, None, "gelu", logits=P["logits"],
+                                    workspace=ws, out=bufs[0])
+            info["rt"] = rt
+
+        def graph_of(sets):
+            # a decode loop as serving runs it: the steps captured once in a HIP graph and replayed,
+            # so the host's per-call cost (Python, argument checks, launches) is outside the figure
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for P in sets:
+                    layer(P)
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for P in sets:
+                    layer(P)
+            return g
+
+        reps = max(1, steps // rot)
+        g_rot, g_warm = graph_of(all_sets), graph_of([all_sets[0]] * rot)
+        ms = time_fn(torch, g_rot.replay, reps, max(1, warmup // rot)) / rot
+        ms_warm = time_fn(torch, g_warm.replay, reps, max(1, warmup // rot)) / rot
         counter = [0]
 
         def step_rot():
             P = all_sets[counter[0] % rot]
             counter[0] += 1
-            _, rt = ops.moe_forward(x, k, P["w_up"], P["w_down"], None, None, "gelu", logits=P["logits"],
-                                    workspace=ws, out=bufs[0])
-            info["rt"] = rt
+            layer(P)
 
-        ms = time_fn(torch, step_rot, steps, warmup)
+        ms_eager = time_fn(torch, step_rot, steps, warmup)
+        info["ms_eager"] = ms_eager
     else:
         ms = time_fn(torch, step, steps, warmup)
     counts = info["rt"]["counts"].cpu()
@@ -258,6 +283,7 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     R = d * 8 * es
     n_touched = int((counts > 0).sum())
     wbytes_expert = {"bf16": 2 * 2 * 8 * d * F, "pauli": 2 * 2 * 8 * d * F, "int8": 2 * 8 * d * F + 4 * (d + F),
+                     "int8_pauli": 2 * 8 * d * F + 4 * (d + F),
                      "f32": 2 * 4 * 8 * d * F, "pauli_f32": 2 * 4 * 8 * d * F}[c["fmt"]]
     res = dict(
         workload=name, N=N, d=d, E=E, k=k, F=F, dtype=c["dtype"], weights=c["fmt"], layers=c["layers"],
@@ -268,8 +294,11 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         # the logits, and the output written
         moved = n_touched * wbytes_expert + 2 * N * R + 4 * N * E
         res.update(weight_sets=rot, decode_bytes=moved, decode_hbm_frac=moved / (ms * 1e-3) / PEAK_HBM,
+                   timing="HIP graph replay of the layer steps (launch cost on the device only)",
                    # one weight set, resident in the Infinity Cache after the first step
-                   ms_per_step_warm=ms_warm, decode_hbm_frac_warm=moved / (ms_warm * 1e-3) / PEAK_HBM)
+                   ms_per_step_warm=ms_warm, decode_hbm_frac_warm=moved / (ms_warm * 1e-3) / PEAK_HBM,
+                   # the same steps launched one by one from Python (host-bound at this size)
+                   ms_per_step_eager=info["ms_eager"])
         return res
     # the dominant kernel: both grouped expert products of layer 0, timed alone
     P0 = prepared[0]

@@ -21,7 +21,9 @@
  *  - dtype codes: 0 = fp32, 1 = bf16 (activations); weight formats:
  *    0 = fp32, 1 = bf16 (dual, sign-folded), 2 = int8 per-output-channel,
  *    3 = bf16 Pauli (the weights as 2x2 complex matrices; even d_in),
- *    4 = fp32 Pauli (fp32 layers on the fp32 MFMA units).
+ *    4 = fp32 Pauli (fp32 layers on the fp32 MFMA units),
+ *    5 = int8 Pauli (the entries of each weight's 2x2 complex matrix, int8 per
+ *        output channel; bf16 decode layers of at most 128 tokens, d <= 128).
  *    activation codes: 0 none, 1 gelu, 2 relu, 3 sigmoid
  *    (holograph/models/hlm_block.py:28-32).
  */
@@ -128,7 +130,11 @@ size_t ygg_prepared_weight_bytes(int E, int d_out, int d_in, int format);
  * reference's CliffordLinear.weight layout (clifford_linear.py:95-96) stacked
  * over experts -- into `format`.  int8: scales (E, d_out) fp32 are written,
  * s = max(absmax over (d_in, 8), 1e-12) / 127, q = clip(rint(w / s), -127, 127)
- * (conventions of bifrost/quantization/grade_quantize.py:85-117,198-203). */
+ * (conventions of bifrost/quantization/grade_quantize.py:85-117,198-203).
+ * Format 5 applies the same conventions to the eight real entries of each
+ * weight's 2x2 complex matrix, M00 = (s + v3) + i (t + b12), M01 = (v1 - b13) +
+ * i (b23 - v2), M10 = (v1 + b13) + i (b23 + v2), M11 = (s - v3) + i (t - b12),
+ * in float64. */
 int ygg_prepare_weights(const float* W, int E, int d_out, int d_in, int format, void* out, float* scales,
                         ygg_stream_t stream);
 
@@ -198,8 +204,10 @@ size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dtype, int
 /* HLMBlock._moe_forward (hlm_block.py:154-183): x (N, d, 8) of dtype ->
  * out (N, d, 8) of dtype (+ residual if not NULL).  logits (N, E) or NULL
  * (then router_w/router_b give the grade-energy logits).  Expert weights
- * prepared with ygg_prepare_weights (format 0 or 4 for fp32, 1, 2 or 3 for bf16;
- * format 3 gathers the token rows inside the up projection),
+ * prepared with ygg_prepare_weights (format 0 or 4 for fp32, 1, 2, 3 or 5 for bf16;
+ * format 3 gathers the token rows inside the up projection; format 5 runs the
+ * routing, both products and the activation in one launch and takes N <= 128,
+ * d <= 128),
  * biases prepared with ygg_prepare_bias or NULL.  topk_idx/topk_w/counts/
  * offsets as in ygg_route. */
 int ygg_moe_forward(const void* x, int dtype, int N, int d, int F, int E, int k, int act, const float* logits,

@@ -355,3 +355,47 @@ def quantize_int8(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
 def dequantize_int8(q: np.ndarray, s: np.ndarray) -> np.ndarray:
     """``q * s`` rounded to fp32 -- the weights the int8 path is checked against."""
     return (q.astype(np.float64) * s.astype(np.float64)[..., None, None]).astype(F32)
+
+
+# ---- int8 Pauli weights (weight format 5) -----------------------------------------------
+# A Cl(3,0) multivector s + v1 e1 + v2 e2 + v3 e3 + b12 e12 + b13 e13 + b23 e23 + t e123 is
+# the 2x2 complex matrix s I + v1 sx + v2 sy + v3 sz + b12 sx sy + b13 sx sz + b23 sy sz
+# + t sx sy sz (sx, sy, sz the Pauli matrices), and the geometric product is the matrix
+# product.  Its eight real entries, ordered [U00, V00, U01, V01, U10, V10, U11, V11]
+# (entry (a, c) of U + iV), are what format 5 quantizes.
+
+
+def pauli_entries(w: np.ndarray) -> np.ndarray:
+    """Blade-order multivectors (..., 8) -> their matrices' real entries (..., 8), float64."""
+    w = np.asarray(w, dtype=np.float64)
+    s, v1, v2, v3, b12, b13, b23, t = (w[..., i] for i in range(8))
+    return np.stack([s + v3, t + b12, v1 - b13, b23 - v2, v1 + b13, b23 + v2, s - v3, t - b12], axis=-1)
+
+
+def from_pauli_entries(p: np.ndarray) -> np.ndarray:
+    """Inverse of :func:`pauli_entries` (float64; exact up to the halving)."""
+    p = np.asarray(p, dtype=np.float64)
+    u00, v00, u01, v01, u10, v10, u11, v11 = (p[..., i] for i in range(8))
+    return 0.5 * np.stack([u00 + u11, u10 + u01, v10 - v01, u00 - u11, v00 - v11, u10 - u01, v10 + v01,
+                           v00 + v11], axis=-1)
+
+
+def quantize_int8_pauli(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric per-output-channel int8 of the weights' matrix entries (format 5).
+
+    ``w``: (..., d_out, d_in, 8) blade order.  Per output channel ``j``:
+    ``s = max(max |entries of W_j.|, 1e-12) / 127`` (float64, stored fp32) and
+    ``q = clip(rint(entries / s), -127, 127)`` -- the conventions of
+    :func:`quantize_int8` (``grade_quantize.py:85-117,198-203``) applied in the
+    matrix basis.  Returns ``q`` (..., d_out, d_in, 8) int8 in entry order and ``s``.
+    """
+    p = pauli_entries(w)
+    absmax = np.max(np.abs(p), axis=(-2, -1))
+    s = (np.maximum(absmax, 1e-12) / 127.0).astype(F32)
+    q = np.clip(np.rint(p / s.astype(np.float64)[..., None, None]), -127, 127).astype(np.int8)
+    return q, s
+
+
+def dequantize_int8_pauli(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """The blade-order weights (float64, exact) that format-5 codes ``q`` with scales ``s`` hold."""
+    return from_pauli_entries(q.astype(np.float64) * s.astype(np.float64)[..., None, None])

@@ -59,6 +59,10 @@ def test_host_side_sizes():
     assert L.ygg_prepared_weight_bytes(2, 5, 7, 2) == 2 * 1 * 4 * 64 * 8
     assert L.ygg_prepared_weight_bytes(2, 5, 7, 0) == 2 * 5 * 7 * 32
     assert L.ygg_prepared_weight_bytes(2, 5, 7, 9) == 0
+    # int8 Pauli: 8 channels x 32 inputs x 8 bytes per block, channels and inputs padded
+    assert L.ygg_prepared_weight_bytes(32, 512, 128, 5) == 32 * 512 * 128 * 8
+    assert L.ygg_prepared_weight_bytes(2, 5, 7, 5) == 2 * 1 * 1 * 2048
+    assert L.ygg_prepared_weight_bytes(1, 9, 33, 5) == 2 * 2 * 2048
 
 
 def test_argument_errors_are_reported_not_aborted():
@@ -120,6 +124,17 @@ def test_layer_rejects_bad_routing_sizes():
     assert L.ygg_moe_forward(1, 1, 8, 16, 32, 2, 2, 1, 1, None, None, 1, None, None, 1, None, None, 2, None, 1,
                              1, 1, 1, 1, 1, ws, None) == -1
     assert b"scales" in L.ygg_last_error()
+    # int8 Pauli weights: the one-launch decode layer takes at most 128 tokens and d <= 128
+    for n_tok, dm in ((129, 16), (8, 129)):
+        ws5 = L.ygg_moe_workspace_bytes(n_tok, dm, 32, 2, 2, 1, 5)
+        assert L.ygg_moe_forward(1, 1, n_tok, dm, 32, 2, 2, 1, 1, None, None, 1, 1, None, 1, 1, None, 5, None, 1,
+                                 1, 1, 1, 1, 1, ws5, None) == -1
+        assert b"format 5" in L.ygg_last_error()
+    assert fwd(2, 3, fmt=5) == -1 and b"k=3" in L.ygg_last_error()
+    # fp32 activations cannot take int8 Pauli weights
+    assert L.ygg_moe_forward(1, 0, 8, 16, 32, 2, 2, 1, 1, None, None, 1, 1, None, 1, 1, None, 5, None, 1,
+                             1, 1, 1, 1, 1, ws, None) == -1
+    assert b"does not match" in L.ygg_last_error()
 
 
 def test_backward_workspace_holds_either_weight_gradient():
@@ -166,6 +181,12 @@ def test_config_validation():
         MoEHLMConfig(d_model=8, d_ff=16, activation="swish")
     with pytest.raises(ValueError):
         MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.float32, weight_format="int8")
+    assert MoEHLMConfig(d_model=7, d_ff=5, dtype=torch.bfloat16, weight_format="int8_pauli").weight_format == \
+        "int8_pauli"
+    with pytest.raises(ValueError):  # fp32 layers, and d_model above the decode layer's 128
+        MoEHLMConfig(d_model=8, d_ff=16, dtype=torch.float32, weight_format="int8_pauli")
+    with pytest.raises(ValueError):
+        MoEHLMConfig(d_model=256, d_ff=16, dtype=torch.bfloat16, weight_format="int8_pauli")
     with pytest.raises(ValueError):
         MoEHLMConfig(d_model=8, d_ff=16, n_experts=65)
     with pytest.raises(ValueError):

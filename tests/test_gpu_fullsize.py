@@ -108,25 +108,30 @@ def test_c3_every_token(c3_case, fmt):
     assert err.max() < TOL_BF16, (int(err.argmax()), float(err.max()))
 
 
-def test_c4_decode_every_token():
+@pytest.mark.parametrize("fmt", ["int8", "int8_pauli"])
+def test_c4_decode_every_token(fmt):
     """BASELINE config 4 (N=64, d=128, F=512, E=32, k=2, int8 weights) against the float64 layer on the
-    dequantized weights the int8 path holds."""
+    dequantized weights the int8 format holds (blade codes, or the codes of the weights' matrix entries)."""
     N, d, E, k, F = 64, 128, 32, 2, 512
     ops = _ops()
     g = np.random.default_rng(4040)
     logits = g.standard_normal((N, E), dtype=np.float32)
     x = _bf16(g.standard_normal((N, d, 8), dtype=np.float32))
     dev, host = _device_weights(4041, E, d, F, torch.float32)
-    P = _layer(ops, dev, "int8")
-    say(f"c4 full layer int8, N={N}")
+    P = _layer(ops, dev, fmt)
+    say(f"c4 full layer {fmt}, N={N}")
     out, rt = ops.moe_forward(torch.from_numpy(x).cuda().bfloat16(), k, P["w_up"], P["w_down"], P["b_up"],
                               P["b_down"], "gelu", logits=torch.from_numpy(logits).cuda())
     idx, w = _check_routing(rt, logits, k)
-    wu = moe.dequantize_int8(*moe.quantize_int8(host["w_up"]))
-    wd = moe.dequantize_int8(*moe.quantize_int8(host["w_down"]))
+    if fmt == "int8":
+        wu = moe.dequantize_int8(*moe.quantize_int8(host["w_up"]))
+        wd = moe.dequantize_int8(*moe.quantize_int8(host["w_down"]))
+    else:
+        wu = moe.dequantize_int8_pauli(*moe.quantize_int8_pauli(host["w_up"]))
+        wd = moe.dequantize_int8_pauli(*moe.quantize_int8_pauli(host["w_down"]))
     ref = dense.moe_layer(x, idx, w, wu, host["b_up"], wd, host["b_down"], "gelu")
     err = _per_token_err(out.float().cpu().numpy(), ref)
-    say(f"c4: worst token error {err.max():.3e}, median {np.median(err):.3e}")
+    say(f"c4 {fmt}: worst token error {err.max():.3e}, median {np.median(err):.3e}")
     assert err.max() < TOL_BF16, (int(err.argmax()), float(err.max()))
 
 

@@ -38,7 +38,8 @@ def _layer(fmt, dtype, N, d, F, E, k, seed):
 
 @pytest.mark.parametrize("fmt,dtype,N,d,F,E,k", [("pauli_f32", torch.float32, 256, 64, 256, 8, 2),
                                                  ("pauli", torch.bfloat16, 2048, 32, 64, 16, 2),
-                                                 ("int8", torch.bfloat16, 64, 32, 64, 8, 2)])
+                                                 ("int8", torch.bfloat16, 64, 32, 64, 8, 2),
+                                                 ("int8_pauli", torch.bfloat16, 64, 128, 512, 32, 2)])
 def test_layer_step_graph_replays_match_eager(fmt, dtype, N, d, F, E, k):
     step = _layer(fmt, dtype, N, d, F, E, k, seed=N + E)
     say(f"graph capture {fmt} N={N} d={d} F={F} E={E} k={k}")

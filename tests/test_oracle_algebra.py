@@ -152,3 +152,32 @@ def test_activation_closed_forms():
     assert np.allclose(rl[:, 7], x[:, 7], atol=0)
     sg = moe.sigmoid(x)
     assert np.allclose(sg[:, 0], 1 / (1 + np.exp(-x64[:, 0])), rtol=1e-6)
+
+
+def _pauli_matrix(w):
+    p = moe.pauli_entries(w)
+    return (p[..., 0::2] + 1j * p[..., 1::2]).reshape(p.shape[:-1] + (2, 2))
+
+
+def test_pauli_entries_are_the_pauli_matrices():
+    # scalar -> I, e1 -> sigma_x, e2 -> sigma_y, e3 -> sigma_z (the textbook matrices)
+    sx = np.array([[0, 1], [1, 0]])
+    sy = np.array([[0, -1j], [1j, 0]])
+    sz = np.array([[1, 0], [0, -1]])
+    for i, want in ((0, np.eye(2)), (1, sx), (2, sy), (3, sz), (4, sx @ sy), (5, sx @ sz), (6, sy @ sz),
+                    (7, sx @ sy @ sz)):
+        assert np.array_equal(_pauli_matrix(basis(i)), want), cl3.BLADE_NAMES[i]
+
+
+def test_pauli_map_is_an_algebra_isomorphism():
+    """The geometric product is the matrix product of the entries' matrices (float64), and
+    from_pauli_entries inverts pauli_entries exactly on fp32 weights."""
+    r = np.random.default_rng(31)
+    a = r.standard_normal((50, 8))
+    b = r.standard_normal((50, 8))
+    ab = cl3.geom_prod_f64(a, b)
+    assert np.allclose(_pauli_matrix(ab), _pauli_matrix(a) @ _pauli_matrix(b), rtol=0, atol=1e-12)
+    # the weight on the left: W x differs from x W
+    assert not np.allclose(_pauli_matrix(ab), _pauli_matrix(b) @ _pauli_matrix(a))
+    a32 = a.astype(np.float32)  # weights are fp32: their entries (sums of two floats) are exact in float64
+    assert np.array_equal(moe.from_pauli_entries(moe.pauli_entries(a32)), a32.astype(np.float64))

@@ -105,3 +105,29 @@ def test_quantize_int8_invariants():
     w2 = (np.arange(-127, 128, dtype=np.float32) * np.float32(0.01)).reshape(1, 1, -1, 1).repeat(8, -1)
     q2, s2 = moe.quantize_int8(w2)
     assert np.array_equal(q2[0, 0, :, 0], np.arange(-127, 128))
+
+
+def test_quantize_int8_pauli_invariants():
+    """Format 5: codes in range, the channel's largest entry at +-127, half-step error on the
+    matrix entries, the dequantized blade weights within the step of the weights, exact on
+    multiples of the scale, zero channels zero."""
+    r = np.random.default_rng(17)
+    w = r.standard_normal((3, 6, 5, 8)).astype(np.float32)
+    w[2, 4] = 0
+    q, s = moe.quantize_int8_pauli(w)
+    assert q.dtype == np.int8 and q.shape == w.shape and s.shape == (3, 6) and s.dtype == np.float32
+    assert np.abs(q.astype(int)).max() <= 127
+    assert (np.abs(q.astype(int)).max(axis=(-2, -1))[s > 1e-10] == 127).all()
+    p = moe.pauli_entries(w)
+    assert (np.abs(q * s.astype(np.float64)[..., None, None] - p) <= s[..., None, None] * 0.5 + 1e-12).all()
+    # the scale is the channel's largest entry over 127, entries being sums of two blades
+    assert np.array_equal(s, (np.abs(p).max(axis=(-2, -1)) / 127.0).clip(1e-12 / 127.0).astype(np.float32))
+    deq = moe.dequantize_int8_pauli(q, s)
+    assert (np.abs(deq - w) <= s[..., None, None] * 0.5 + 1e-7).all()
+    assert (q[2, 4] == 0).all()
+    # exact on multiples of the scale: weights whose entries are integers times 0.01
+    codes = r.integers(-127, 128, size=(1, 2, 7, 8))
+    codes[0, :, 0, 0] = 127  # pin each channel's scale to 0.01
+    wq = moe.from_pauli_entries(codes * 0.01)
+    q3, s3 = moe.quantize_int8_pauli(wq)
+    assert np.array_equal(q3, codes) and np.array_equal(s3, np.full((1, 2), 0.01, np.float32))

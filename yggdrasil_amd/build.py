@@ -18,7 +18,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(OUT_DIR, "libygg_moe.so")
-SOURCES = ["capi.hip", "route.hip", "dispatch.hip", "clifford_gemm.hip", "decode.hip", "pauli_gemm.hip", "pauli_f32.hip",
+SOURCES = ["capi.hip", "route.hip", "dispatch.hip", "clifford_gemm.hip", "decode.hip", "decode_pauli.hip", "pauli_gemm.hip", "pauli_f32.hip",
            "norm.hip", "quantize.hip", "backward.hip"]
 
 HIPCC_FLAGS = [

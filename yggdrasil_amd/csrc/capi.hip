@@ -49,6 +49,8 @@ YGG_API int ygg_version(void) { return 1; }
 extern "C" size_t ygg_route_workspace_bytes(int N, int E, int k);
 extern "C" int ygg_route(const float*, int, int, int, int32_t*, float*, int32_t*, int32_t*, int32_t*, int32_t*, void*,
                          size_t, hipStream_t);
+extern "C" int ygg_router_energy_logits(const void*, int, int, int, const float*, const float*, int, float*, float*,
+                                        hipStream_t);
 extern "C" int ygg_route_energy(const void*, int, int, int, const float*, const float*, int, int, int32_t*, float*,
                                 int32_t*, int32_t*, int32_t*, int32_t*, float*, void*, size_t, hipStream_t);
 extern "C" int ygg_dispatch(const void*, int, int, int, int, const int32_t*, void*, int, hipStream_t);
@@ -69,6 +71,7 @@ extern "C" int ygg_pauli_grouped_linear_f32(const float*, const int32_t*, int, c
 // partial planes of the K-split down product
 static size_t ys_bytes(size_t P, int E, int d, int F, int dtype, int w_format) {
   const size_t es = (dtype == kF32) ? 4 : 2;
+  if (w_format == kWPauliI8) return (size_t)decode_pauli_planes(F) * P * d * 8 * 4;
   if (decode_shape((int)P, E, w_format)) {
     const int planes = decode_splits(F) > decode_layer_planes(F) ? decode_splits(F) : decode_layer_planes(F);
     return (size_t)planes * P * d * 8 * 4;
@@ -105,11 +108,17 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
   YGG_CHECK_ARG(act >= kActNone && act <= kActSigmoid, "ygg_moe_forward: activation %d", act);
   YGG_CHECK_ARG(N == 0 || (x && out && w_up && w_down && topk_idx && topk_w && counts && offsets && workspace),
                 "ygg_moe_forward: null pointer");
-  YGG_CHECK_ARG(w_format != kWI8 || N == 0 || (s_up && s_down), "ygg_moe_forward: int8 weights need their scales");
+  YGG_CHECK_ARG((w_format != kWI8 && w_format != kWPauliI8) || N == 0 || (s_up && s_down),
+                "ygg_moe_forward: int8 weights need their scales");
   YGG_CHECK_ARG(dtype == kF32 || dtype == kBF16, "ygg_moe_forward: dtype %d unsupported", dtype);
   YGG_CHECK_ARG(dtype == kF32 ? (w_format == kWF32 || w_format == kWPauliF32)
-                             : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli),
+                             : (w_format == kWBF16 || w_format == kWI8 || w_format == kWPauli ||
+                                w_format == kWPauliI8),
                 "ygg_moe_forward: weight format %d does not match dtype %d", w_format, dtype);
+  YGG_CHECK_ARG(w_format != kWPauliI8 || N == 0 || decode_pauli_fusable(N, E, k, d, F),
+                "ygg_moe_forward: int8 Pauli weights (format 5) serve decode batches of at most 128 tokens with "
+                "d <= 128 (N=%d d=%d); use format 2 or 3 for larger calls",
+                N, d);
   YGG_CHECK_ARG(w_format != kWPauli || (d % 2 == 0 && F % 2 == 0),
                 "ygg_moe_forward: the Pauli weight format needs even d and F (d=%d F=%d)", d, F);
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format),
@@ -138,6 +147,22 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
   p += align256(P * F * 8 * es);
   void* ys = p;
 
+  if (w_format == kWPauliI8) {
+    // int8 Pauli weights: routing, both products and the activation in one launch
+    // (the grade-energy logits first when the caller gives none), then the combine
+    // of its partial planes
+    if (!logits) {
+      if (ygg_router_energy_logits(x, dtype, N, d, router_w, router_b, E, lg, nullptr, stream)) return -1;
+      logits = lg;
+    }
+    if (decode_pauli_layer(static_cast<const uint16_t*>(x), logits, N, E, k, d, F, act,
+                           static_cast<const int8_t*>(w_up), s_up, b_up, static_cast<const int8_t*>(w_down), s_down,
+                           b_down, topk_idx, topk_w, counts, offsets, perm, slot_pos, static_cast<float*>(ys),
+                           stream))
+      return -1;
+    return combine_planes(static_cast<const float*>(ys), decode_pauli_planes(F), (int)P, N, k, d, topk_idx, topk_w,
+                          slot_pos, residual, out, dtype, stream);
+  }
   // decode layers given logits route inside their up product (no routing launch)
   const bool decode = decode_shape((int)P, E, w_format);
   const bool fused_layer = decode && logits && dtype == kBF16 && decode_layer_fusable(N, E, k, d, F);

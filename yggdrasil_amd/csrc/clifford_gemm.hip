@@ -805,18 +805,20 @@ YGG_API size_t ygg_prepared_weight_bytes(int E, int d_out, int d_in, int format)
     case kWI8: return (size_t)E * JB * IP * 64 * 8;
     case kWPauli: return (d_in % 2) ? 0 : (size_t)E * d_out * d_in * 8 * 2;
     case kWPauliF32: return (size_t)E * d_out * d_in * 16 * 4;
+    case kWPauliI8: return decode_pauli_weight_bytes(E, d_out, d_in);
     default: return 0;
   }
 }
 
 YGG_API int ygg_prepare_weights(const float* W, int E, int d_out, int d_in, int format, void* out, float* scales,
                                 hipStream_t stream) {
-  YGG_CHECK_ARG(format >= kWF32 && format <= kWPauliF32, "ygg_prepare_weights: format %d", format);
+  YGG_CHECK_ARG(format >= kWF32 && format <= kWPauliI8, "ygg_prepare_weights: format %d", format);
   YGG_CHECK_ARG(E >= 1 && d_out >= 1 && d_in >= 1, "ygg_prepare_weights: bad sizes E=%d d_out=%d d_in=%d", E, d_out,
                 d_in);
   YGG_CHECK_ARG(W && out, "ygg_prepare_weights: null pointer");
   if (format == kWPauli) return pauli_prepare_weights(W, E, d_out, d_in, out, stream);
   if (format == kWPauliF32) return pauli_f32_prepare_weights(W, E, d_out, d_in, out, stream);
+  if (format == kWPauliI8) return decode_pauli_prepare_weights(W, E, d_out, d_in, out, scales, stream);
   YGG_CHECK_ARG(format != kWI8 || scales, "ygg_prepare_weights: int8 format needs a scales buffer [E, d_out]");
   if (format == kWI8) {
     quant_scale_kernel<<<E * d_out, 256, 0, stream>>>(W, d_in, scales);

@@ -104,7 +104,7 @@ int check_launch(const char* what);
 enum DType : int { kF32 = 0, kBF16 = 1, kI8 = 2 };
 enum Act : int { kActNone = 0, kActGelu = 1, kActRelu = 2, kActSigmoid = 3 };
 // prepared weight formats (ygg_prepare_weights)
-enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3, kWPauliF32 = 4 };
+enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3, kWPauliF32 = 4, kWPauliI8 = 5 };
 
 // bf16 Pauli weight layout (pauli_gemm.hip)
 int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
@@ -156,6 +156,20 @@ int decode_layer(const uint16_t* x, const float* logits, int N, int E, int k, in
                  const int8_t* w_up, const float* s_up, const float* b_up, const int8_t* w_dn, const float* s_dn,
                  const float* b_dn, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
                  int32_t* perm, int32_t* slot_pos, float* planes, hipStream_t stream);
+
+// The decode-shape layer on int8 Pauli weights (format 5, decode_pauli.hip):
+// the prepared size and preparation (codes plus one fp32 scale per expert and
+// output channel), whether (N, E, k, d, F) fits the one-launch layer, its number
+// of partial planes, and the launch, with the outputs of decode_layer.
+size_t decode_pauli_weight_bytes(int E, int d_out, int d_in);
+int decode_pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, float* scales,
+                                 hipStream_t stream);
+bool decode_pauli_fusable(int N, int E, int k, int d, int F);
+int decode_pauli_planes(int F);
+int decode_pauli_layer(const uint16_t* x, const float* logits, int N, int E, int k, int d, int F, int act,
+                       const int8_t* w_up, const float* s_up, const float* b_up, const int8_t* w_dn,
+                       const float* s_dn, const float* b_dn, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                       int32_t* offsets, int32_t* perm, int32_t* slot_pos, float* planes, hipStream_t stream);
 
 // combine of fp32 blade-order partial planes (dispatch.hip): the planes of a
 // row are added in plane order, then weighted and combined as ygg_combine does.

@@ -41,7 +41,9 @@ class MoEHLMConfig:
     weight_format  fp32 layers: 'pauli_f32' (the default: complex 2x2 weights on the fp32 MFMA
                 units, 32 multiply-adds per multivector pair) or 'f32' (8x8 L(w) blocks on the
                 vector units, 64); bf16 layers: 'pauli' (the default when d_model and d_ff are
-                even), 'bf16' (8x8 L(w) blocks) or 'int8' (per-output-channel int8, L(w) blocks)
+                even), 'bf16' (8x8 L(w) blocks), 'int8' (per-output-channel int8, L(w) blocks) or
+                'int8_pauli' (per-output-channel int8 of the complex 2x2 weights: the one-launch
+                decode layer, batches of at most 128 tokens with d_model <= 128)
     router      'energy' -- CliffordRouter's grade-energy logits (default, the reference);
                 'clifford_head' -- CliffordLinear(d -> E) then the scalar part;
                 'logits' -- the caller passes logits to forward()
@@ -66,11 +68,13 @@ class MoEHLMConfig:
         even = self.d_model % 2 == 0 and self.d_ff % 2 == 0
         if self.weight_format is None:
             self.weight_format = "pauli_f32" if self.dtype == torch.float32 else ("pauli" if even else "bf16")
-        if self.weight_format not in ("f32", "pauli_f32", "bf16", "int8", "pauli"):
-            raise ValueError("weight_format must be 'f32', 'pauli_f32', 'bf16', 'int8' or 'pauli'")
+        if self.weight_format not in ("f32", "pauli_f32", "bf16", "int8", "pauli", "int8_pauli"):
+            raise ValueError("weight_format must be 'f32', 'pauli_f32', 'bf16', 'int8', 'pauli' or 'int8_pauli'")
         if (self.dtype == torch.float32) != (self.weight_format in ("f32", "pauli_f32")):
-            raise ValueError("fp32 layers use 'pauli_f32' or 'f32' weights; bf16 layers use 'pauli', 'bf16' or "
-                             "'int8'")
+            raise ValueError("fp32 layers use 'pauli_f32' or 'f32' weights; bf16 layers use 'pauli', 'bf16', "
+                             "'int8' or 'int8_pauli'")
+        if self.weight_format == "int8_pauli" and self.d_model > 128:
+            raise ValueError("the 'int8_pauli' weight format serves d_model <= 128")
         if self.weight_format == "pauli" and not even:
             raise ValueError("the 'pauli' weight format needs even d_model and d_ff")
         if not 1 <= self.n_experts <= 64 or not 1 <= self.top_k <= min(8, self.n_experts):

@@ -17,7 +17,8 @@ from ._native import check, lib, ptr, stream_handle
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1}
 ACT_CODE = {"none": 0, "gelu": 1, "relu": 2, "sigmoid": 3}
-WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2, "pauli": 3, "pauli_f32": 4}
+WFORMAT_CODE = {"f32": 0, "bf16": 1, "int8": 2, "pauli": 3, "pauli_f32": 4, "int8_pauli": 5}
+INT8_FORMATS = ("int8", "int8_pauli")
 # activation row layouts of pauli_grouped_linear
 X_LAYOUT = {"blade": 0, "pauli": 1}
 Y_LAYOUT = {"pauli": 0, "blade": 1}
@@ -271,7 +272,9 @@ class PreparedWeights:
 
 def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
     """w: (E, d_out, d_in, 8) fp32 blade order -> prepared layout ('f32' | 'bf16' | 'int8' | 'pauli' |
-    'pauli_f32')."""
+    'pauli_f32' | 'int8_pauli').  The int8 formats also hold one fp32 scale per (expert, output channel):
+    'int8' quantizes the blade components, 'int8_pauli' the entries of each weight's 2x2 complex matrix
+    (the decode layer's format)."""
     dev = _dev(w)
     if w.dim() == 3:
         w = w.unsqueeze(0)
@@ -283,7 +286,7 @@ def prepare_weights(w: torch.Tensor, fmt: str) -> PreparedWeights:
     if nbytes == 0:
         raise ValueError(f"weight format {fmt!r} cannot hold shape (E={E}, d_out={d_out}, d_in={d_in})")
     data = torch.empty((nbytes,), device=dev, dtype=torch.uint8)
-    scales = torch.empty((E, d_out), device=dev, dtype=torch.float32) if fmt == "int8" else None
+    scales = torch.empty((E, d_out), device=dev, dtype=torch.float32) if fmt in INT8_FORMATS else None
     check(L.ygg_prepare_weights(ptr(w), E, d_out, d_in, code, ptr(data), ptr(scales), stream_handle(dev)),
           "prepare_weights")
     return PreparedWeights(data, scales, fmt, E, d_out, d_in)
@@ -307,8 +310,9 @@ def grouped_clifford_linear(x_sorted: torch.Tensor, pw: PreparedWeights, offsets
                             bias_prepared: torch.Tensor | None = None, act: str = "none",
                             out_dtype: torch.dtype | None = None, out_blade_order: bool = True) -> torch.Tensor:
     """Per-expert CliffordLinear on expert-grouped rows. x_sorted: (P, d_in, 8) in mask order."""
-    if pw.fmt in ("pauli", "pauli_f32"):
-        raise ValueError("Pauli weights run through pauli_grouped_linear / pauli_grouped_linear_f32")
+    if pw.fmt in ("pauli", "pauli_f32", "int8_pauli"):
+        raise ValueError("Pauli weights run through pauli_grouped_linear / pauli_grouped_linear_f32 / the decode "
+                         "layer (int8_pauli)")
     dev = _dev(x_sorted, offsets, bias_prepared)
     P = x_sorted.shape[0]
     if x_sorted.shape[1] != pw.d_in:
@@ -448,6 +452,9 @@ def grouped_experts(x_sorted: torch.Tensor, expert_offsets: torch.Tensor, expert
     if P == 0:
         return x_sorted.clone()
     fmt = w_up.fmt
+    if fmt == "int8_pauli":
+        raise ValueError("int8_pauli weights run inside the decode layer (moe_forward), which routes its own "
+                         "rows; use 'int8' for grouped experts")
     if fmt == "pauli":
         h = pauli_grouped_linear(x, w_up, offs, b_up, act, x_layout="blade", y_layout="pauli")
         y = pauli_grouped_linear(h, w_down, offs, b_down, "none", x_layout="pauli", y_layout="blade",
