@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
   __shared__ float s_xmax[kDpBatch][2], s_xinv[kDpBatch], s_hinv[kDpBatch];
   __shared__ float s_hmax[kDpRb][kDpWaves][4];
   __shared__ int32_t rows_tok[kDpMaxTokens];           // this expert's tokens, ascending
-  __shared__ int32_t s_cnt[kMaxExperts], s_wv[kDpWaves];
+  __shared__ int32_t s_cnt[kMaxExperts], s_wv[kDpSelPasses * kDpWaves];
   __shared__ int32_t s_sel[kDpMaxTokens * kMaxTopK];  // the selection: expert and weight of every slot
   __shared__ float s_w[kDpMaxTokens * kMaxTopK];
   uint16_t* const a_up16 = reinterpret_cast<uint16_t*>(a_up);
@@ -289,42 +289,68 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       }
   }
 
-  // ---- 2. routing of the whole batch (every workgroup routes it; chunk 0 writes
-  // this expert's part of the routing arrays)
+  // ---- 2. routing of the whole batch (every workgroup routes it).  Only this
+  // expert's tokens, in ascending order, stand between the logits and the input
+  // rows: they come from a ballot over each token's selected slots.  The
+  // renormalised weights, every expert's count and this expert's first row follow
+  // once the input rows and the down weights are in flight.
   if (tid < kMaxExperts) s_cnt[tid] = 0;
+  int sel_e[kDpSelPasses];
+  float sel_raw[kDpSelPasses];
+  uint32_t tok_mask[kDpSelPasses];  // uniform: bit g -- token 64 ps + 8 wave + g chose e
 #pragma unroll
   for (int ps = 0; ps < kDpSelPasses; ++ps) {
+    sel_e[ps] = -1;
+    sel_raw[ps] = 0.f;
+    tok_mask[ps] = 0u;
     if (ps * (kDpThreads / kSelLanes) < N) {
       const int t = ps * (kDpThreads / kSelLanes) + (tid >> 3);
-      int se;
-      float swt;
-      select_from_logits<RQ>(lg[ps], E, k, t < N, sj, lane, se, swt);
-      if (se >= 0) {
-        s_sel[t * k + sj] = se;
-        s_w[t * k + sj] = swt;
-      }
+      select_topk_raw<RQ>(lg[ps], E, k, t < N, sj, lane, sel_e[ps], sel_raw[ps]);
+      if (sel_e[ps] >= 0) s_sel[t * k + sj] = sel_e[ps];
+      const uint64_t b = __ballot(sel_e[ps] == e);
+      uint32_t m = 0u;
+#pragma unroll
+      for (int gq = 0; gq < kDpThreads / kSelLanes / kDpWaves; ++gq)
+        m |= ((b >> (kSelLanes * gq)) & 0xffull) ? (1u << gq) : 0u;
+      tok_mask[ps] = m;
+      if (lane == 0) s_wv[ps * kDpWaves + wave] = __popc(m);
     }
   }
   __syncthreads();
-  for (int f = tid; f < N * k; f += kDpThreads) atomicAdd(&s_cnt[s_sel[f]], 1);
-  bool mine = false;
-  if (tid < N)
-    for (int q = 0; q < k; ++q) mine |= s_sel[tid * k + q] == e;
-  const uint64_t bal = __ballot(mine);
-  if (lane == 0) s_wv[wave] = __popcll(bal);
-  __syncthreads();
-  if (mine) {
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += s_wv[w];
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    rows_tok[base + __popcll(bal & lt)] = tid;
+  // this wave's tokens take the rows after those of the (pass, wave) pairs before it
+  int n_e = 0, tok_base[kDpSelPasses];
+#pragma unroll
+  for (int ps = 0; ps < kDpSelPasses; ++ps) {
+    tok_base[ps] = 0;
+    if (ps * (kDpThreads / kSelLanes) < N)
+      for (int w = 0; w < kDpWaves; ++w) {
+        if (w == wave) tok_base[ps] = n_e;
+        n_e += s_wv[ps * kDpWaves + w];
+      }
   }
-  // this expert's rows start after those of the experts before it (E <= 64: one lane each)
-  const int n_e = s_cnt[e], row_beg = dc_wave_sum(lane < e ? s_cnt[lane] : 0);
-  __syncthreads();
+#pragma unroll
+  for (int ps = 0; ps < kDpSelPasses; ++ps)
+    if (lane < 8 && ((tok_mask[ps] >> lane) & 1u))
+      rows_tok[tok_base[ps] + __popc(tok_mask[ps] & ((1u << lane) - 1u))] =
+          ps * (kDpThreads / kSelLanes) + kSelLanes * wave + lane;
+  // the rest of the routing: renormalised weights and every expert's count (for this
+  // expert's first row and the routing arrays)
+  auto finish_routing = [&]() {
+#pragma unroll
+    for (int ps = 0; ps < kDpSelPasses; ++ps) {
+      if (ps * (kDpThreads / kSelLanes) < N) {
+        const int t = ps * (kDpThreads / kSelLanes) + (tid >> 3);
+        const float w = renorm_slot(sel_raw[ps], k, sj, lane);
+        if (sel_e[ps] >= 0) {
+          s_w[t * k + sj] = w;
+          atomicAdd(&s_cnt[sel_e[ps]], 1);
+        }
+      }
+    }
+  };
   // the routing arrays of this expert's slots, for the combine and the caller: written
   // by chunk 0 once its loads are all in (its loop would otherwise wait for them early)
-  auto write_routing = [&]() {
+  auto write_routing = [&](int row_beg) {
     if (c != 0) return;
     for (int r = tid; r < n_e; r += kDpThreads) {
       const int t = rows_tok[r];
@@ -342,9 +368,12 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
     }
   };
   if (n_e == 0) {  // uniform: no token chose this expert
-    write_routing();
+    finish_routing();
+    __syncthreads();
+    write_routing(dc_wave_sum(lane < e ? s_cnt[lane] : 0));
     return;
   }
+  __syncthreads();  // rows_tok is complete
 
   // ---- 3. the input rows of the first batch (load l: token 4 l + tid / 128, input
   // tid % 128), then the down weights: wave w takes output column blocks 2 w and
@@ -380,6 +409,12 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
           wd[q][s][uv] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
         }
   }
+
+  // with the input rows and the down weights in flight: the rest of the routing; this
+  // expert's rows start after those of the experts before it (E <= 64: one lane each)
+  finish_routing();
+  __syncthreads();
+  const int row_beg = dc_wave_sum(lane < e ? s_cnt[lane] : 0);
 
   // bf16 rows (blade order) -> Pauli entries -> per-token fixed point, hi and lo
   // planes of the up A operand.  Thread (xt, xi) of load l writes the rows (token xt
@@ -542,7 +577,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       }
     }
   }
-  write_routing();
+  write_routing(row_beg);
 }
 
 }  // namespace ygg

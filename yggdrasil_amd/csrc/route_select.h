@@ -23,6 +23,12 @@ template <int STEP>
 __device__ inline float grp_xchg(float v) {
   return __builtin_bit_cast(float, grp_xchg<STEP>(__builtin_bit_cast(int, v)));
 }
+template <int STEP>
+__device__ inline uint64_t grp_xchg64(uint64_t v) {
+  const uint32_t lo = (uint32_t)grp_xchg<STEP>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)grp_xchg<STEP>((int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
 
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
@@ -80,13 +86,14 @@ __device__ inline void energy_logits(const void* __restrict__ x, int x_dtype, in
   }
 }
 
-// The selection of one token, eight lanes per token (lane j = tid % 8), from
-// its logits p (lane j: experts j + 8 q, -inf past E or for an inactive token):
-// probabilities, top-k and renormalised weights; lane j returns slot j
-// (expert, weight), or expert -1 for j >= k or an inactive token.
+// The top-k of one token, eight lanes per token (lane j = tid % 8), from its
+// logits p (lane j: experts j + 8 q, -inf past E or for an inactive token):
+// probabilities and top-k; lane j returns slot j (expert, probability), or
+// expert -1 for j >= k or an inactive token.  select_from_logits adds the
+// renormalised weights.
 template <int Q>  // Q >= ceil(E / 8) logits per lane (-inf past E)
-__device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool active, int j, int lane, int& out_e,
-                                          float& out_w) {
+__device__ inline void select_topk_raw(float (&p)[Q], int E, int k, bool active, int j, int lane, int& out_e,
+                                       float& out_raw) {
   // ---- probabilities (the reference's fp32 softmax, clifford_router.py:18-21)
   float m = -INFINITY;
 #pragma unroll
@@ -128,52 +135,62 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
 #pragma unroll
   for (int q = 0; q < Q; ++q) p[q] = __fdiv_rn(p[q], denom);
 
-  // ---- top-k: k rounds of (max probability, then min index) over the 8 lanes.
-  // The selection key orders NaN probabilities below every real one, so the
-  // order is total, all 8 lanes agree on each winner and every slot gets a
-  // valid expert (with NaN logits the weights are unspecified).
-  float key[Q];
+  // ---- top-k: k rounds of (max probability, then min index) over the 8 lanes,
+  // without branches.  Each candidate is one 64-bit key, (probability bits + 1)
+  // << 32 | (63 - expert): probabilities are >= 0, so their bit patterns order
+  // as the values do, and among equal probabilities the lower index has the
+  // larger key.  A NaN probability keeps 0 in the upper half (below every real
+  // probability, so the order is total and every slot gets a valid expert; its
+  // weight is unspecified), padding experts and taken candidates are 0.
+  uint64_t key[Q];
 #pragma unroll
-  for (int q = 0; q < Q; ++q) key[q] = (p[q] == p[q]) ? p[q] : -1.0f;
+  for (int q = 0; q < Q; ++q) {
+    const int e = j + kSelLanes * q;
+    const uint64_t hi = (p[q] == p[q]) ? (uint64_t)(__builtin_bit_cast(uint32_t, p[q]) + 1u) << 32 : 0ull;
+    key[q] = (e < E) ? (hi | (uint64_t)(63 - e)) : 0ull;
+  }
   // a rolled loop: lane j keeps round j's winner (its slot), so no per-slot arrays
-  uint32_t taken = 0;  // bit q: this lane's element q is selected
-  int my_e = -1;       // lane j holds slot j
+  int my_e = -1;  // lane j holds slot j
   float my_raw = 0.f;
 #pragma unroll 1
   for (int s = 0; s < k; ++s) {
-    float bv = -2.0f;
-    int bi = 0x7fffffff;
+    uint64_t best = key[0];
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
-      const int e = j + kSelLanes * q;
-      if (e < E && !((taken >> q) & 1u) && (key[q] > bv || (key[q] == bv && e < bi))) {
-        bv = key[q];
-        bi = e;
-      }
-    }
-    auto take_better = [&](float ov, int oi) {
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    };
-    take_better(grp_xchg<0>(bv), grp_xchg<0>(bi));
-    take_better(grp_xchg<1>(bv), grp_xchg<1>(bi));
-    take_better(grp_xchg<2>(bv), grp_xchg<2>(bi));
-    // k <= E: at least one candidate remains, so bi is a valid expert
-    if (s == j) {
-      my_e = bi;
-      my_raw = bv;
-    }
-    if ((bi & (kSelLanes - 1)) == j) taken |= 1u << ((bi / kSelLanes) & 31);
+    for (int q = 1; q < Q; ++q) best = key[q] > best ? key[q] : best;
+    uint64_t o = grp_xchg64<0>(best);
+    best = o > best ? o : best;
+    o = grp_xchg64<1>(best);
+    best = o > best ? o : best;
+    o = grp_xchg64<2>(best);
+    best = o > best ? o : best;
+    // k <= E: at least one candidate remains, so the winner is a valid expert
+    const uint32_t bhi = (uint32_t)(best >> 32);
+    my_e = (s == j) ? 63 - (int)(best & 63ull) : my_e;
+    my_raw = (s == j) ? (bhi ? __builtin_bit_cast(float, bhi - 1u) : -1.0f) : my_raw;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) key[q] = key[q] == best ? 0ull : key[q];
   }
-  // renormalise; the sum runs from the least to the most probable slot (lane k-1 down to 0)
-  float ssum = 0.f;
-  for (int s = k - 1; s >= 0; --s) ssum = __fadd_rn(ssum, __shfl(my_raw, (lane & ~(kSelLanes - 1)) + s));
-  ssum = __fadd_rn(ssum, 1e-12f);
-  const float my_w = (j < k) ? __fdiv_rn(my_raw, ssum) : 0.f;
   out_e = active ? my_e : -1;
-  out_w = my_w;
+  out_raw = my_raw;
+}
+
+// The renormalised weight of slot j (lanes j < k of the token's 8 hold the slots'
+// probabilities `raw`; every lane of the wave takes part): the sum runs from the
+// least to the most probable slot (lane k-1 down to 0), then + 1e-12.
+__device__ inline float renorm_slot(float raw, int k, int j, int lane) {
+  float ssum = 0.f;
+  for (int s = k - 1; s >= 0; --s) ssum = __fadd_rn(ssum, __shfl(raw, (lane & ~(kSelLanes - 1)) + s));
+  ssum = __fadd_rn(ssum, 1e-12f);
+  return (j < k) ? __fdiv_rn(raw, ssum) : 0.f;
+}
+
+// select_topk_raw, then the renormalised weights: lane j returns slot j (expert, weight).
+template <int Q>
+__device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool active, int j, int lane, int& out_e,
+                                          float& out_w) {
+  float raw;
+  select_topk_raw<Q>(p, E, k, active, j, lane, out_e, raw);
+  out_w = renorm_slot(raw, k, j, lane);
 }
 
 template <int Q>
