@@ -150,21 +150,32 @@ def test_pauli_rows_random_against_numpy(rows, d):
     assert np.array_equal(xp[:, 0], col0) and np.array_equal(xp[:, 1], col1)
 
 
-def test_pauli_small_integer_product_is_exact():
-    """Integer operands whose Pauli coordinates and sums stay exact in bf16/fp32 give exact results."""
+@pytest.mark.parametrize("E,d_in,d_out,P,N,x_layout,biased", [
+    (2, 8, 6, 40, 40, "blade", False), (3, 42, 70, 300, 120, "pauli", True),
+    (5, 2, 64, 200, 64, "pauli", True), (4, 522, 34, 410, 90, "pauli", False)])
+def test_pauli_small_integer_product_is_exact(E, d_in, d_out, P, N, x_layout, biased):
+    """Integer operands whose Pauli coordinates and sums stay exact in bf16/fp32 give exact results:
+    every staged piece (gathered rows, K tails, ragged column tiles, the bias) lands where it belongs."""
     ops = _ops()
-    g = np.random.default_rng(4)
-    E, d_in, d_out, P = 2, 8, 6, 40
+    g = np.random.default_rng(4 + d_in)
     W = g.integers(-2, 3, size=(E, d_out, d_in, 8)).astype(np.float32)
-    x = g.integers(-2, 3, size=(P, d_in, 8)).astype(np.float32)
-    offsets = np.array([0, 17, P], np.int32)
-    say("pauli integer product")
-    y = ops.pauli_grouped_linear(torch.from_numpy(x).cuda().bfloat16(), ops.prepare_weights(torch.from_numpy(W).cuda(),
-                                 "pauli"), torch.from_numpy(offsets).cuda(), None, "none", x_layout="blade",
+    x = g.integers(-2, 3, size=(N, d_in, 8)).astype(np.float32)
+    b = g.integers(-3, 4, size=(E, d_out, 8)).astype(np.float32) if biased else None
+    gather = g.integers(0, N, P).astype(np.int32) if N != P else np.arange(P, dtype=np.int32)
+    offsets = _offsets(g, E, P)
+    say(f"pauli integer product E={E} d_in={d_in} d_out={d_out} P={P} x={x_layout} bias={biased}")
+    xt = torch.from_numpy(x).cuda().bfloat16()
+    if x_layout == "pauli":
+        xt = ops.pauli_rows_from_blade(xt)
+    pb = ops.prepare_bias(torch.from_numpy(b).cuda()) if biased else None
+    y = ops.pauli_grouped_linear(xt, ops.prepare_weights(torch.from_numpy(W).cuda(), "pauli"),
+                                 torch.from_numpy(offsets).cuda(), pb, "none", x_layout=x_layout,
+                                 gather=torch.from_numpy(gather).cuda() if N != P else None,
                                  y_layout="blade", out_dtype=torch.float32).cpu().numpy()
     for e in range(E):
         rows = slice(offsets[e], offsets[e + 1])
-        assert np.array_equal(y[rows], moe.clifford_linear(x[rows], W[e], None))
+        ref = moe.clifford_linear(x[gather[rows]], W[e], b[e] if biased else None)
+        assert np.array_equal(y[rows], ref), e
 
 
 def test_pauli_rejects_bad_arguments():

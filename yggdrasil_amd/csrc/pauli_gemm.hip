@@ -89,6 +89,65 @@ struct PauliTileInfo {
   int half;  // -1: the whole tile; 0 / 1: only row block `half` of every wave
 };
 
+// Epilogue of one tile for one wave: the inverse Pauli map, bias, grade-wise
+// activation and the output layout, all in the lane that holds the 8 reals of
+// an output multivector.  acc[rb][cb][a][re/im] is wave row block rb (of WR,
+// each 16 tokens x b = 0, 1), column block cb (of WC, 32 output multivectors);
+// bv[cb] is the bias of this lane's column in blade order.
+template <int ACT, int OUT, int OUT_DT, int WR, int WC, int BWT>
+__device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][WC][2][2], const float (&bvs)[WC][8],
+                                                    const PauliTileInfo& ti, int wave, int g, int l32, int d_out,
+                                                    void* __restrict__ Y) {
+  const int wt = wave % BWT, wj = wave / BWT;
+#pragma unroll
+  for (int cb = 0; cb < WC; ++cb) {
+    const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
+    if (j >= d_out) continue;
+    const float* bv = bvs[cb];
+#pragma unroll
+    for (int rb = 0; rb < WR; ++rb) {
+      if (ti.half >= 0 && rb > 0) break;  // a half tile: the first accumulators hold block `half`
+      const int rbr = ti.half >= 0 ? ti.half : rb;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int t = (wt * WR + rbr) * 16 + 4 * q + 2 * g + h;
+          const int row = ti.row0 + t;
+          if (row >= ti.row_end) continue;
+          const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
+          float y[8];
+          pauli_to_blade(acc[rb][cb][0][0][v0], acc[rb][cb][0][1][v0], acc[rb][cb][0][0][v0 + 1],
+                         acc[rb][cb][0][1][v0 + 1], acc[rb][cb][1][0][v0], acc[rb][cb][1][1][v0],
+                         acc[rb][cb][1][0][v0 + 1], acc[rb][cb][1][1][v0 + 1], y);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) y[c] += bv[c];
+          activate_blade<ACT>(y);
+          if constexpr (OUT == kOutPauliRows) {
+            float c0[4], c1[4];
+            blade_to_pauli(y, c0, c1);
+            uint16_t* Yh = static_cast<uint16_t*>(Y);
+            *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row) * d_out + j) * 4) =
+                make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+            *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row + 1) * d_out + j) * 4) =
+                make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+          } else if constexpr (OUT_DT == kBF16) {
+            uint4 o;
+            o.x = pack2_bf16(y[0], y[1]);
+            o.y = pack2_bf16(y[2], y[3]);
+            o.z = pack2_bf16(y[4], y[5]);
+            o.w = pack2_bf16(y[6], y[7]);
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(Y) + ((size_t)row * d_out + j) * 8) = o;
+          } else {
+            float4* p = reinterpret_cast<float4*>(static_cast<float*>(Y) + ((size_t)row * d_out + j) * 8);
+            p[0] = make_float4(y[0], y[1], y[2], y[3]);
+            p[1] = make_float4(y[4], y[5], y[6], y[7]);
+          }
+        }
+    }
+  }
+}
+
 template <int ACT, int IN, int OUT, int OUT_DT, class TL>
 __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_kernel(
     const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
@@ -311,53 +370,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   };
 
   auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
-#pragma unroll
-    for (int cb = 0; cb < WC; ++cb) {
-      const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
-      if (j >= d_out) continue;
-      const float* bv = bvs[cb];
-#pragma unroll
-      for (int rb = 0; rb < WR; ++rb) {
-        if (ti.half >= 0 && rb > 0) break;  // a half tile: the first accumulators hold block `half`
-        const int rbr = ti.half >= 0 ? ti.half : rb;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int t = (wt * WR + rbr) * 16 + 4 * q + 2 * g + h;
-            const int row = ti.row0 + t;
-            if (row >= ti.row_end) continue;
-            const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
-            float y[8];
-            pauli_to_blade(acc[rb][cb][0][0][v0], acc[rb][cb][0][1][v0], acc[rb][cb][0][0][v0 + 1],
-                           acc[rb][cb][0][1][v0 + 1], acc[rb][cb][1][0][v0], acc[rb][cb][1][1][v0],
-                           acc[rb][cb][1][0][v0 + 1], acc[rb][cb][1][1][v0 + 1], y);
-#pragma unroll
-            for (int c = 0; c < 8; ++c) y[c] += bv[c];
-            activate_blade<ACT>(y);
-            if constexpr (OUT == kOutPauliRows) {
-              float c0[4], c1[4];
-              blade_to_pauli(y, c0, c1);
-              uint16_t* Yh = static_cast<uint16_t*>(Y);
-              *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row) * d_out + j) * 4) =
-                  make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
-              *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row + 1) * d_out + j) * 4) =
-                  make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
-            } else if constexpr (OUT_DT == kBF16) {
-              uint4 o;
-              o.x = pack2_bf16(y[0], y[1]);
-              o.y = pack2_bf16(y[2], y[3]);
-              o.z = pack2_bf16(y[4], y[5]);
-              o.w = pack2_bf16(y[6], y[7]);
-              *reinterpret_cast<uint4*>(static_cast<uint16_t*>(Y) + ((size_t)row * d_out + j) * 8) = o;
-            } else {
-              float4* p = reinterpret_cast<float4*>(static_cast<float*>(Y) + ((size_t)row * d_out + j) * 8);
-              p[0] = make_float4(y[0], y[1], y[2], y[3]);
-              p[1] = make_float4(y[4], y[5], y[6], y[7]);
-            }
-          }
-      }
-    }
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT>(acc, bvs, ti, wave, g, l32, d_out, Y);
   };
 
   // ---- the stream of (tile, chunk) steps ------------------------------------
@@ -392,6 +405,394 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   int f = 0;
   for (; f < n_full * nk; ++f) step(f, std::integral_constant<int, WR>{});
   for (; f < total; ++f) step(f, std::integral_constant<int, 1>{});
+}
+
+// ---------------------------------------------------------------------------
+// Pauli half-row input: operands staged by direct-to-LDS buffer loads
+// ---------------------------------------------------------------------------
+// Every staged piece is a 16-byte raw buffer load that writes LDS itself
+// (lane l of an instruction lands at the wave's LDS base + 16 l), so no
+// registers hold operands between their load and their use, and several
+// chunks are in flight.  A step computes K = 8 input multivectors (KC):
+//   W: a chunk per step, 64 columns x 128 B (4 pairs x (a = 0, 1) x 16 B), in
+//      NW = 3 slots, issued two steps ahead; slot s of column j holds piece
+//      s ^ swz_w(j);
+//   A: a chunk per two steps, 128 half-rows (m, b) x 128 B (8 input pairs), in
+//      NA = 3 slots, issued four steps ahead; slot s of half-row r holds pair
+//      s ^ swz_a(r).
+// Both are whole 128-byte lines per half-row or column (the memory system's
+// request unit), and the XOR swizzles keep the MFMA operand reads (16 B per
+// lane over 32 consecutive half-rows or columns) free of bank conflicts; the
+// lanes of a load pick their global pieces so that the fixed LDS order comes
+// out swizzled.  The tile's gather indices and bias arrive the same way, in
+// two slots by tile parity, so no register load queues behind the staged
+// chunks: before each step one explicit vmcnt wait lets exactly the loads of
+// the previous step stay outstanding (loads complete in issue order, and the
+// newest chunk a step needs is the W chunk issued two steps before), and one
+// barrier publishes the chunks and frees the slots computed before.  A tile's
+// gather indices are loaded with the previous tile's first A chunk, which
+// needs at least two A chunks per tile (d_in > 16; smaller products use the
+// register-staged kernel).  The step loop carries its tile and chunk
+// counters: a wave issues at most one instruction every four cycles, so the
+// per-step bookkeeping is a few scalar operations.
+struct PauliDmaTile {
+  static constexpr int NT = 256, T = 64, BN = 64, KC = 8, WR = 2, WC = 1, BWT = 2;
+  static constexpr int NA = 3, NW = 3;
+  static constexpr int A_SLOT = 2 * T * 128;                // 16 KiB: 16 input multivectors
+  static constexpr int W_SLOT = BN * 128;                   // 8 KiB: 8 input multivectors
+  static constexpr int W_OFF = NA * A_SLOT;
+  static constexpr int G_OFF = W_OFF + NW * W_SLOT;         // 2 x 64 row indices (tile parity)
+  static constexpr int B_OFF = G_OFF + 2 * T * 4;           // 2 x 64 columns x 32 B of bias
+  static constexpr int LDS = B_OFF + 2 * BN * 32;           // 78336 B: two workgroups per CU
+  static constexpr int A_AHEAD = 2, W_AHEAD = 2;            // chunks issued ahead of use
+};
+
+__device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+// One direct-to-LDS load of BYTES (4 or 16) bytes per lane at byte offset `off`
+// of buffer `r`; lane l lands at lds + BYTES l (`lds` is the same in every
+// lane).  Written as assembly: the compiler would otherwise wait for every
+// outstanding direct load before any LDS read (it cannot tell the slots
+// apart), which serialises the pipeline; here the explicit waits below are
+// the only ones, and the compiler issues no vector-memory loads of its own in
+// the steps (its waits for earlier loads only grow stricter with these in
+// the queue).
+template <int BYTES>
+__device__ __forceinline__ void dma_to_lds(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t off) {
+  static_assert(BYTES == 4 || BYTES == 16, "direct load size");
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);  // wave-uniform
+  if constexpr (BYTES == 4)
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(r) : "m0");
+  else
+    asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(r) : "m0");
+}
+// wait until at most N vector memory operations of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x3f70 | N);  // expcnt and lgkmcnt at their maxima: no wait on those
+}
+// workgroup barrier without the fences of __syncthreads: the waits that make
+// the staged LDS contents ready are the explicit ones above
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int ACT, int OUT, int OUT_DT>
+__global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_dma_kernel(
+    const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
+    const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
+    void* __restrict__ Y, int n_xcd, uint32_t x_bytes) {
+  using C = PauliDmaTile;
+  constexpr int NT = C::NT, T = C::T, BN = C::BN, KC = C::KC, WR = C::WR, WC = C::WC, BWT = C::BWT;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
+  __shared__ int s_off[kPauliMaxExperts + 1];   // expert row offsets
+  __shared__ int s_tbeg[kPauliMaxExperts + 1];  // first row tile of each expert
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int i = tid; i <= E; i += NT) s_off[i] = offsets[i];
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int x = 0; x < E; ++x) {
+      s_tbeg[x] = acc;
+      acc += (s_off[x + 1] - s_off[x] + T - 1) / T;
+    }
+    s_tbeg[E] = acc;
+  }
+  __syncthreads();
+  // lane x keeps expert x's first row tile and row range: a tile's expert is the
+  // number of experts whose first tile is at or before it, minus one (experts
+  // without rows share their successor's first tile and are never chosen)
+  const int v_tbeg = lane < E ? s_tbeg[lane] : 0x7fffffff;
+  const int v_off = s_off[lane < E ? lane : E], v_end = s_off[lane < E ? lane + 1 : E];
+  // (LDS values are per lane to the compiler; these are the same in every lane)
+  const int n_rows = __builtin_amdgcn_readfirstlane(s_off[E]);
+
+  // the tile stream: as in the register-staged kernel, one contiguous range of
+  // tiles per XCD, whole rounds first, a short remainder cut into half tiles
+  const int CT = (d_out + BN - 1) / BN;
+  const int n_tiles = __builtin_amdgcn_readfirstlane(s_tbeg[E]) * CT;
+  const int nka = (d_in + 2 * KC - 1) / (2 * KC);  // A chunks per tile
+  const int nk = 2 * nka;                          // steps (W chunks) per tile
+  const int per_xcd = gridDim.x / n_xcd;
+  const int xcd = blockIdx.x % n_xcd, slot = blockIdx.x / n_xcd;
+  const int lo = (int)((long long)n_tiles * xcd / n_xcd), hi = (int)((long long)n_tiles * (xcd + 1) / n_xcd);
+  const int R = hi - lo, rounds = R / per_xcd, rem = R - rounds * per_xcd;
+  const bool split = rem > 0 && 2 * rem <= per_xcd;
+  const int n_full = split ? rounds : (R > slot ? (R - slot + per_xcd - 1) / per_xcd : 0);
+  const int n_mine = n_full + ((split && slot < 2 * rem) ? 1 : 0);
+  const int total = n_mine * nk, total_a = n_mine * nka;
+  if (total == 0) return;
+
+  auto decode = [&](int n) __attribute__((always_inline)) {
+    const bool half = n >= n_full;
+    const int L = half ? lo + rounds * per_xcd + (slot >> 1) : lo + slot + n * per_xcd;
+    const int rt = L / CT, ct = L - rt * CT;
+    const int e = __popcll(__ballot(v_tbeg <= rt)) - 1;
+    PauliTileInfo t;
+    t.e = e;
+    t.row0 = __builtin_amdgcn_readlane(v_off, e) + (rt - __builtin_amdgcn_readlane(v_tbeg, e)) * T;
+    t.row_end = __builtin_amdgcn_readlane(v_end, e);
+    t.col0 = ct * BN;
+    t.half = half ? (slot & 1) : -1;
+    return t;
+  };
+
+  const int wt = wave % BWT, wj = wave / BWT;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int IP = d_in >> 1;  // input pairs (d_in even)
+  constexpr uint32_t kOff = 0x80000000u;  // past every range: reads zero
+
+  const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0,
+                                                                          x_bytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(gather), (short)0, gather ? (uint32_t)n_rows * 4 : 0u, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(bias), (short)0, bias ? (uint32_t)E * d_out * 32 : 0u, kBufferFlags);
+  __amdgpu_buffer_rsrc_t w_rsrc = x_rsrc;
+
+  // this lane's pieces: A loads 4 w .. 4 w + 3 (half-rows 8 q .. 8 q + 7, one
+  // 128-byte line each), W loads 2 w and 2 w + 1 (columns 8 q .. 8 q + 7)
+  int a_lim[4], w_lim[2];  // a piece is inside the K range while its chunk's first pair is below these
+  uint32_t a_pc[4], w_pc[2];  // the piece's byte offset inside its row or column chunk
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int r = 8 * (4 * wave + u) + (lane >> 3);
+    const int c = (lane & 7) ^ swz8(r);  // input pair of the chunk
+    a_lim[u] = IP - c;
+    a_pc[u] = c * 16;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int c = (lane & 7) ^ swz8(8 * (2 * wave + u) + (lane >> 3));  // piece (pair, a) of the chunk
+    w_lim[u] = IP - (c >> 1);
+    w_pc[u] = c * 16;
+  }
+  uint32_t a_cur[4], w_cur[2];  // offsets of those pieces in the next chunk to issue
+
+  // next A chunk: chunk iak of tile iam, slot ias; next W chunk: chunk iwk of
+  // tile iwm, slot iws (value selects throughout: a branch that increments one
+  // of two counters becomes an address select that keeps them in scratch)
+  int ia = 0, iam = 0, iak = 0, ias = 0;
+  int iw = 0, iwm = 0, iwk = 0, iws = 0;
+  // issue the next A chunk (4 loads per wave); at a tile's first A chunk also the
+  // next tile's gather indices (wave 3, before the chunk)
+  auto issue_a = [&]() __attribute__((always_inline)) {
+    if (iak == 0) {
+      const PauliTileInfo t = decode(iam);
+      const int* gs = reinterpret_cast<const int*>(smem + C::G_OFF + (iam & 1) * T * 4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int r = 8 * (4 * wave + u) + (lane >> 3);  // half-row (token r / 2, b = r % 2)
+        const int src = gather ? gs[r >> 1] : min(t.row0 + (r >> 1), t.row_end - 1);
+        a_cur[u] = (uint32_t)(2 * src + (r & 1)) * d_in * 8 + a_pc[u];
+      }
+      if (gather != nullptr && wave == 3 && iam + 1 < n_mine) {
+        const PauliTileInfo tn = decode(iam + 1);
+        dma_to_lds<4>(g_rsrc, smem + C::G_OFF + ((iam + 1) & 1) * T * 4,
+                      (uint32_t)min(tn.row0 + lane, tn.row_end - 1) * 4);
+      }
+    }
+    const int p0 = iak * KC;  // first input pair of the chunk (16 multivectors)
+    unsigned char* st = smem + ias * C::A_SLOT + 4 * wave * 1024;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      dma_to_lds<16>(x_rsrc, st + u * 1024, p0 < a_lim[u] ? a_cur[u] : kOff);
+      a_cur[u] += KC * 16;
+    }
+    ++ia;
+    ias = ias == C::NA - 1 ? 0 : ias + 1;
+    const bool last = iak == nka - 1;
+    iam += last ? 1 : 0;
+    iak = last ? 0 : iak + 1;
+  };
+  // issue the next W chunk (2 loads per wave); at a tile's first W chunk also
+  // the tile's bias (waves 0 and 1, before the chunk)
+  auto issue_w = [&]() __attribute__((always_inline)) {
+    if (iwk == 0) {
+      const PauliTileInfo t = decode(iwm);
+      w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(Wp) + (size_t)t.e * d_out * IP * 16, (short)0,
+                                                 (uint32_t)d_out * IP * 32, kBufferFlags);
+      if (wave < 2) {  // bias: 64 columns x 32 B, two loads of 32 columns
+        const int j = t.col0 + 32 * wave + (lane >> 1);
+        dma_to_lds<16>(b_rsrc, smem + C::B_OFF + (iwm & 1) * BN * 32 + wave * 1024,
+                       j < d_out ? (uint32_t)(t.e * d_out + j) * 32 + (lane & 1) * 16 : kOff);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int j = t.col0 + 8 * (2 * wave + u) + (lane >> 3);  // past d_out: past the expert's range, reads zero
+        w_cur[u] = (uint32_t)j * IP * 32 + w_pc[u];
+      }
+    }
+    const int p0 = iwk * (KC / 2);  // first input pair of the chunk (8 multivectors)
+    unsigned char* st = smem + C::W_OFF + iws * C::W_SLOT + 2 * wave * 1024;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma_to_lds<16>(w_rsrc, st + u * 1024, p0 < w_lim[u] ? w_cur[u] : kOff);
+      w_cur[u] += KC / 2 * 32;
+    }
+    ++iw;
+    iws = iws == C::NW - 1 ? 0 : iws + 1;
+    const bool last = iwk == nk - 1;
+    iwm += last ? 1 : 0;
+    iwk = last ? 0 : iwk + 1;
+  };
+
+  // MFMA operand reads: half-row (wt WR + rb) 32 + l32 at pair 4 (step parity)
+  // + 2 s + g of the A chunk, and column (wj WC + cb) 32 + l32 at piece
+  // 2 (2 s + g) + a of the W chunk, through the swizzles.  The odd step's pair
+  // differs in bit 2, i.e. bit 6 of the byte offset: offset ^ 64.  (Selecting
+  // between two offset arrays instead would turn into an address select that
+  // keeps the arrays in scratch memory.)
+  uint32_t a_rd[2][2], w_rd[WC][2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = (wt * WR + rb) * 32 + l32;
+      a_rd[s][rb] = (uint32_t)row * 128 + ((2 * s + g) ^ swz8(row)) * 16;
+    }
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int cb = 0; cb < WC; ++cb) {
+      const int col = (wj * WC + cb) * 32 + l32;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) w_rd[cb][s][a] = col * 128 + (((2 * (2 * s + g) + a) ^ swz8(col)) * 16);
+    }
+
+  pf32x16_t acc[WR][WC][2][2];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < WR; ++a)
+#pragma unroll
+      for (int b = 0; b < WC; ++b)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[a][b][c][d][v] = 0.f;
+  };
+  // a step's operands: A chunk half `par` in slot as, W chunk in slot ws; NR row
+  // blocks from rb0 (a half tile computes one block, rb0, with its offsets by
+  // arithmetic: no dynamic register index)
+  uint4 av[2][WR], wv[2][WC][2];
+  auto read_operands = [&](int as, int ws, int par, auto nr_tag, int rb0) __attribute__((always_inline)) {
+    constexpr int NR = decltype(nr_tag)::value;
+    const unsigned char* As = smem + as * C::A_SLOT;
+    const unsigned char* Ws = smem + C::W_OFF + ws * C::W_SLOT;
+#pragma unroll
+    for (int s = 0; s < KC / 4; ++s) {
+      if constexpr (NR == WR) {
+#pragma unroll
+        for (int rb = 0; rb < NR; ++rb) av[s][rb] = *reinterpret_cast<const uint4*>(As + (a_rd[s][rb] ^ (par << 6)));
+      } else {
+        const int row = (wt * WR + rb0) * 32 + l32;
+        av[s][0] = *reinterpret_cast<const uint4*>(As + row * 128 + ((4 * par + 2 * s + g) ^ swz8(row)) * 16);
+      }
+#pragma unroll
+      for (int cb = 0; cb < WC; ++cb)
+#pragma unroll
+        for (int a = 0; a < 2; ++a) wv[s][cb][a] = *reinterpret_cast<const uint4*>(Ws + w_rd[cb][s][a]);
+    }
+  };
+  auto mfmas = [&](auto nr_tag) __attribute__((always_inline)) {
+    constexpr int NR = decltype(nr_tag)::value;
+#pragma unroll
+    for (int s = 0; s < KC / 4; ++s)
+#pragma unroll
+      for (int rb = 0; rb < NR; ++rb) {
+        const uint4 x = av[s][rb];
+        const uint4 ap = make_uint4(rot_conj(x.x), rot_conj(x.y), rot_conj(x.z), rot_conj(x.w));
+        const pbf16x8_t A0 = __builtin_bit_cast(pbf16x8_t, x);
+        const pbf16x8_t A1 = __builtin_bit_cast(pbf16x8_t, ap);
+#pragma unroll
+        for (int cb = 0; cb < WC; ++cb)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            const pbf16x8_t B = __builtin_bit_cast(pbf16x8_t, wv[s][cb][a]);
+            acc[rb][cb][a][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A0, B, acc[rb][cb][a][0], 0, 0, 0);
+            acc[rb][cb][a][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, B, acc[rb][cb][a][1], 0, 0, 0);
+          }
+      }
+  };
+
+  float bvs[WC][8];
+  auto epilogue = [&](const PauliTileInfo& ti, int m) __attribute__((always_inline)) {
+    const unsigned char* bs = smem + C::B_OFF + (m & 1) * BN * 32;
+#pragma unroll
+    for (int cb = 0; cb < WC; ++cb) {
+      const int jl = (wj * WC + cb) * 32 + l32;
+      const uint4 lo4 = *reinterpret_cast<const uint4*>(bs + jl * 32);
+      const uint4 hi4 = *reinterpret_cast<const uint4*>(bs + jl * 32 + 16);
+      const uint32_t mk[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};  // mask order
+#pragma unroll
+      for (int c = 0; c < 8; ++c) bvs[cb][c] = __builtin_bit_cast(float, mk[blade_to_mask(c)]);
+    }
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT>(acc, bvs, ti, wave, g, l32, d_out, Y);
+  };
+
+  // prologue: the first tile's gather indices; then what steps -4 .. -1 would
+  // issue: A chunks 0 and 1, W chunk 0, and W chunk 1 last
+  if (gather != nullptr && wave == 3) {
+    const PauliTileInfo t = decode(0);
+    dma_to_lds<4>(g_rsrc, smem + C::G_OFF, (uint32_t)min(t.row0 + lane, t.row_end - 1) * 4);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();
+  issue_a();
+  issue_a();  // every tile has at least two A chunks
+  issue_w();
+  issue_w();
+  zero_acc();
+
+  // Steps come in pairs (a tile has an even number): the even step issues the
+  // A chunk two pairs ahead and the W chunk two steps ahead, the odd step the
+  // W chunk.  The newest chunk a step reads is the W chunk issued two steps
+  // before, so the loads of the previous step may stay outstanding: 2 after
+  // an odd step, 6 after an even one (a tile's bias or gather indices, issued
+  // before those, only make the wait stricter); near the end, none.
+  PauliTileInfo cur = {0, 0, 1, 0, -1};
+  int fm = 0, fkc = 0;   // tile and K chunk of the step computed
+  int fas = 0, fws = 0;  // its A and W slots
+  auto step = [&](int f, auto nr_tag) __attribute__((always_inline)) {
+    constexpr int NR = decltype(nr_tag)::value;
+    const bool odd = (f & 1) != 0;
+    if (f + 3 < total) {
+      if (odd) wait_vmcnt<6>();
+      else wait_vmcnt<2>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    if (fkc == 0) cur = decode(fm);
+    read_operands(fas, fws, odd ? 1 : 0, nr_tag, cur.half < 0 ? 0 : cur.half);
+    if (!odd && ia < total_a) issue_a();
+    if (iw < total) issue_w();
+    mfmas(nr_tag);
+    const bool last = fkc == nk - 1;
+    if (last) {
+      epilogue(cur, fm);
+      zero_acc();
+    }
+    fm += last ? 1 : 0;
+    fkc = last ? 0 : fkc + 1;
+    fas = odd ? (fas == C::NA - 1 ? 0 : fas + 1) : fas;
+    fws = fws == C::NW - 1 ? 0 : fws + 1;
+    (void)NR;
+  };
+  int f = 0;
+  for (; f < n_full * nk; f += 2) {
+    step(f, std::integral_constant<int, WR>{});
+    step(f + 1, std::integral_constant<int, WR>{});
+  }
+  for (; f < total; f += 2) {
+    step(f, std::integral_constant<int, 1>{});
+    step(f + 1, std::integral_constant<int, 1>{});
+  }
+  wait_vmcnt<0>();
 }
 
 // ---------------------------------------------------------------------------
@@ -484,8 +885,12 @@ int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int3
     grid = (int)max_tiles;
     xcds = 1;
   }
-  pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
-      <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
+  if (IN == kInPauliRows && d_in > 2 * PauliDmaTile::KC)  // at least two A chunks per tile
+    pauli_gemm_dma_kernel<ACT, OUT, ODT>
+        <<<grid, PauliDmaTile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
+  else
+    pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
+        <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
   return check_launch("pauli_gemm");
 }
 
@@ -548,7 +953,9 @@ YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, int x_rows, co
   // staging uses 32-bit buffer offsets: every operand stays below 2 GiB (x's
   // rows, blade or Pauli half-row pairs, are 16 d_in bytes either way)
   const size_t lim = (size_t)1 << 31;
-  YGG_CHECK_ARG((size_t)d_out * d_in * 16 < lim && (size_t)E * d_out * 32 < lim && (size_t)x_rows * d_in * 16 < lim,
+  // (a column tile may reach 64 columns past d_out: their offsets must not wrap either)
+  YGG_CHECK_ARG((size_t)(d_out + 64) * d_in * 16 < lim && (size_t)E * d_out * 32 < lim &&
+                    (size_t)x_rows * d_in * 16 < lim,
                 "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (x rows=%d d_in=%d d_out=%d)",
                 x_rows, d_in, d_out);
   if (P_max == 0) return 0;
