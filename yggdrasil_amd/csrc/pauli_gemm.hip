@@ -93,17 +93,27 @@ struct PauliTileInfo {
 // activation and the output layout, all in the lane that holds the 8 reals of
 // an output multivector.  acc[rb][cb][a][re/im] is wave row block rb (of WR,
 // each 16 tokens x b = 0, 1), column block cb (of WC, 32 output multivectors);
-// bv[cb] is the bias of this lane's column in blade order.
-template <int ACT, int OUT, int OUT_DT, int WR, int WC, int BWT>
+// bv[cb] is the bias of this lane's column in blade order, added here unless
+// BIAS_IN_ACC (the accumulators started from it).  The output is written by
+// buffer stores: y_rsrc spans the output's true size, the row-dependent part of
+// each offset is a scalar, the lane's part a fixed per-lane offset.
+template <int ACT, int OUT, int OUT_DT, int WR, int WC, int BWT, bool BIAS_IN_ACC>
 __device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][WC][2][2], const float (&bvs)[WC][8],
                                                     const PauliTileInfo& ti, int wave, int g, int l32, int d_out,
-                                                    void* __restrict__ Y) {
+                                                    __amdgpu_buffer_rsrc_t y_rsrc) {
+  typedef unsigned int pu32x2_t __attribute__((ext_vector_type(2)));
+  typedef unsigned int pu32x4_t __attribute__((ext_vector_type(4)));
   const int wt = wave % BWT, wj = wave / BWT;
+  // bytes per output row (Pauli half-row pair, bf16 blade or fp32 blade row)
+  constexpr int MV_BYTES = (OUT == kOutPauliRows || OUT_DT == kBF16) ? 16 : 32;
 #pragma unroll
   for (int cb = 0; cb < WC; ++cb) {
     const int j = ti.col0 + (wj * WC + cb) * 32 + l32;
     if (j >= d_out) continue;
     const float* bv = bvs[cb];
+    // lane part of the offset: token 2 g of the group of four, column j
+    const uint32_t v_off = OUT == kOutPauliRows ? (uint32_t)((4 * g) * d_out + j) * 8
+                                                : (uint32_t)((2 * g) * d_out + j) * MV_BYTES;
 #pragma unroll
     for (int rb = 0; rb < WR; ++rb) {
       if (ti.half >= 0 && rb > 0) break;  // a half tile: the first accumulators hold block `half`
@@ -112,39 +122,63 @@ __device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][W
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int t = (wt * WR + rbr) * 16 + 4 * q + 2 * g + h;
-          const int row = ti.row0 + t;
-          if (row >= ti.row_end) continue;
+          const int rs = ti.row0 + (wt * WR + rbr) * 16 + 4 * q + h;  // row of lanes with g = 0
+          if (rs + 2 * g >= ti.row_end) continue;
+          const uint32_t s_off = (uint32_t)rs * d_out * MV_BYTES;
           const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
           float y[8];
           pauli_to_blade(acc[rb][cb][0][0][v0], acc[rb][cb][0][1][v0], acc[rb][cb][0][0][v0 + 1],
                          acc[rb][cb][0][1][v0 + 1], acc[rb][cb][1][0][v0], acc[rb][cb][1][1][v0],
                          acc[rb][cb][1][0][v0 + 1], acc[rb][cb][1][1][v0 + 1], y);
+          if constexpr (!BIAS_IN_ACC) {
 #pragma unroll
-          for (int c = 0; c < 8; ++c) y[c] += bv[c];
+            for (int c = 0; c < 8; ++c) y[c] += bv[c];
+          }
           activate_blade<ACT>(y);
           if constexpr (OUT == kOutPauliRows) {
             float c0[4], c1[4];
             blade_to_pauli(y, c0, c1);
-            uint16_t* Yh = static_cast<uint16_t*>(Y);
-            *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row) * d_out + j) * 4) =
-                make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
-            *reinterpret_cast<uint2*>(Yh + ((size_t)(2 * row + 1) * d_out + j) * 4) =
-                make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+            const pu32x2_t h0 = {pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3])};
+            const pu32x2_t h1 = {pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3])};
+            __builtin_amdgcn_raw_buffer_store_b64(h0, y_rsrc, v_off, s_off, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(h1, y_rsrc, v_off + (uint32_t)d_out * 8, s_off, 0);
           } else if constexpr (OUT_DT == kBF16) {
-            uint4 o;
-            o.x = pack2_bf16(y[0], y[1]);
-            o.y = pack2_bf16(y[2], y[3]);
-            o.z = pack2_bf16(y[4], y[5]);
-            o.w = pack2_bf16(y[6], y[7]);
-            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(Y) + ((size_t)row * d_out + j) * 8) = o;
+            const pu32x4_t o = {pack2_bf16(y[0], y[1]), pack2_bf16(y[2], y[3]), pack2_bf16(y[4], y[5]),
+                                pack2_bf16(y[6], y[7])};
+            __builtin_amdgcn_raw_buffer_store_b128(o, y_rsrc, v_off, s_off, 0);
           } else {
-            float4* p = reinterpret_cast<float4*>(static_cast<float*>(Y) + ((size_t)row * d_out + j) * 8);
-            p[0] = make_float4(y[0], y[1], y[2], y[3]);
-            p[1] = make_float4(y[4], y[5], y[6], y[7]);
+            const pu32x4_t lo = {__builtin_bit_cast(unsigned, y[0]), __builtin_bit_cast(unsigned, y[1]),
+                                 __builtin_bit_cast(unsigned, y[2]), __builtin_bit_cast(unsigned, y[3])};
+            const pu32x4_t hi = {__builtin_bit_cast(unsigned, y[4]), __builtin_bit_cast(unsigned, y[5]),
+                                 __builtin_bit_cast(unsigned, y[6]), __builtin_bit_cast(unsigned, y[7])};
+            __builtin_amdgcn_raw_buffer_store_b128(lo, y_rsrc, v_off, s_off, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(hi, y_rsrc, v_off + 16, s_off, 0);
           }
         }
     }
+  }
+}
+
+// The accumulators of a tile started from the bias: entry (a, b) of the halved
+// Pauli matrix of the lane's column bias, re and im (the weights hold W / 2, so
+// the products are half the Pauli matrices and pauli_to_blade needs no scale).
+template <int WR, int WC>
+__device__ __forceinline__ void pauli_acc_from_bias(pf32x16_t (&acc)[WR][WC][2][2], const float (&bvs)[WC][8]) {
+#pragma unroll
+  for (int cb = 0; cb < WC; ++cb) {
+    float c0[4], c1[4];
+    blade_to_pauli(bvs[cb], c0, c1);  // c0 = (M00, M10), c1 = (M01, M11)
+    // [a][re/im][b]
+    const float e[2][2][2] = {{{0.5f * c0[0], 0.5f * c1[0]}, {0.5f * c0[1], 0.5f * c1[1]}},
+                              {{0.5f * c0[2], 0.5f * c1[2]}, {0.5f * c0[3], 0.5f * c1[3]}}};
+#pragma unroll
+    for (int rb = 0; rb < WR; ++rb)
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int ri = 0; ri < 2; ++ri)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[rb][cb][a][ri][v] = e[a][ri][v & 1];
   }
 }
 
@@ -152,7 +186,7 @@ template <int ACT, int IN, int OUT, int OUT_DT, class TL>
 __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_kernel(
     const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
-    void* __restrict__ Y, int n_xcd, uint32_t x_bytes) {
+    void* __restrict__ Y, int n_xcd, uint32_t x_bytes, uint32_t y_bytes) {
   constexpr int NT = TL::NT, T = TL::T, BN = TL::BN, KC = TL::KC, WR = TL::WR, WC = TL::WC, BWT = TL::BWT;
   constexpr int A_PER = TL::A_PER, W_PER = TL::W_PER;
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * TL::STAGE];
@@ -369,8 +403,9 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
     }
   };
 
+  const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, y_bytes, kBufferFlags);
   auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
-    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT>(acc, bvs, ti, wave, g, l32, d_out, Y);
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, false>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc);
   };
 
   // ---- the stream of (tile, chunk) steps ------------------------------------
@@ -481,7 +516,7 @@ template <int ACT, int OUT, int OUT_DT>
 __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_dma_kernel(
     const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
-    void* __restrict__ Y, int n_xcd, uint32_t x_bytes) {
+    void* __restrict__ Y, int n_xcd, uint32_t x_bytes, uint32_t y_bytes) {
   using C = PauliDmaTile;
   constexpr int NT = C::NT, T = C::T, BN = C::BN, KC = C::KC, WR = C::WR, WC = C::WC, BWT = C::BWT;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
@@ -663,18 +698,6 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     }
 
   pf32x16_t acc[WR][WC][2][2];
-  auto zero_acc = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int a = 0; a < WR; ++a)
-#pragma unroll
-      for (int b = 0; b < WC; ++b)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int d = 0; d < 2; ++d)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[a][b][c][d][v] = 0.f;
-  };
   // a step's operands: A chunk half `par` in slot as, W chunk in slot ws; NR row
   // blocks from rb0 (a half tile computes one block, rb0, with its offsets by
   // arithmetic: no dynamic register index)
@@ -719,8 +742,9 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
       }
   };
 
+  // a tile's accumulators start from its bias (slot m % 2, complete by the tile's first step)
   float bvs[WC][8];
-  auto epilogue = [&](const PauliTileInfo& ti, int m) __attribute__((always_inline)) {
+  auto acc_from_bias = [&](int m) __attribute__((always_inline)) {
     const unsigned char* bs = smem + C::B_OFF + (m & 1) * BN * 32;
 #pragma unroll
     for (int cb = 0; cb < WC; ++cb) {
@@ -731,7 +755,11 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
 #pragma unroll
       for (int c = 0; c < 8; ++c) bvs[cb][c] = __builtin_bit_cast(float, mk[blade_to_mask(c)]);
     }
-    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT>(acc, bvs, ti, wave, g, l32, d_out, Y);
+    pauli_acc_from_bias<WR, WC>(acc, bvs);
+  };
+  const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, y_bytes, kBufferFlags);
+  auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, true>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc);
   };
 
   // prologue: the first tile's gather indices; then what steps -4 .. -1 would
@@ -746,7 +774,6 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   issue_a();  // every tile has at least two A chunks
   issue_w();
   issue_w();
-  zero_acc();
 
   // Steps come in pairs (a tile has an even number): the even step issues the
   // A chunk two pairs ahead and the W chunk two steps ahead, the odd step the
@@ -767,16 +794,16 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
       wait_vmcnt<0>();
     }
     lds_barrier();
-    if (fkc == 0) cur = decode(fm);
+    if (fkc == 0) {
+      cur = decode(fm);
+      acc_from_bias(fm);
+    }
     read_operands(fas, fws, odd ? 1 : 0, nr_tag, cur.half < 0 ? 0 : cur.half);
     if (!odd && ia < total_a) issue_a();
     if (iw < total) issue_w();
     mfmas(nr_tag);
     const bool last = fkc == nk - 1;
-    if (last) {
-      epilogue(cur, fm);
-      zero_acc();
-    }
+    if (last) epilogue(cur);
     fm += last ? 1 : 0;
     fkc = last ? 0 : fkc + 1;
     fas = odd ? (fas == C::NA - 1 ? 0 : fas + 1) : fas;
@@ -876,6 +903,8 @@ template <int ACT, int IN, int OUT, int ODT>
 int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int32_t* gather, const uint16_t* Wp,
                  const float* bias, const int32_t* offsets, int E, int P_max, int d_in, int d_out, void* Y) {
   const DeviceShape ds = device_shape();
+  // the output's size (rows past P_max, from offsets beyond it, are not written)
+  const uint32_t y_bytes = (uint32_t)((size_t)P_max * d_out * ((OUT == kOutPauliRows || ODT == kBF16) ? 16 : 32));
   // never more workgroups than tiles can exist
   const long long max_tiles =
       ((long long)(P_max + Tile::T - 1) / Tile::T + E) * ((d_out + Tile::BN - 1) / Tile::BN);
@@ -887,10 +916,10 @@ int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int3
   }
   if (IN == kInPauliRows && d_in > 2 * PauliDmaTile::KC)  // at least two A chunks per tile
     pauli_gemm_dma_kernel<ACT, OUT, ODT>
-        <<<grid, PauliDmaTile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
+        <<<grid, PauliDmaTile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes, y_bytes);
   else
     pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
-        <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes);
+        <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes, y_bytes);
   return check_launch("pauli_gemm");
 }
 
@@ -955,9 +984,10 @@ YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, int x_rows, co
   const size_t lim = (size_t)1 << 31;
   // (a column tile may reach 64 columns past d_out: their offsets must not wrap either)
   YGG_CHECK_ARG((size_t)(d_out + 64) * d_in * 16 < lim && (size_t)E * d_out * 32 < lim &&
-                    (size_t)x_rows * d_in * 16 < lim,
-                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (x rows=%d d_in=%d d_out=%d)",
-                x_rows, d_in, d_out);
+                    (size_t)x_rows * d_in * 16 < lim && (size_t)P_max * d_out * 32 < lim,
+                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (x rows=%d d_in=%d d_out=%d "
+                "output rows=%d)",
+                x_rows, d_in, d_out, P_max);
   if (P_max == 0) return 0;
   YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear: null pointer");
   const uint32_t x_bytes = (uint32_t)((size_t)x_rows * d_in * 16);
