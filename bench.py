@@ -97,7 +97,7 @@ def parse():
     # shapes the C3 Pauli products issue: the practical reference for the MFMA roofline
     ap.add_argument("--calibrate", action="store_true")
     # record counter figures measured by rocprofv3 for the current build of a kernel, e.g.
-    # --pin '{"key": "pauli_gemm_kernel_c3", "sources": ["yggdrasil_amd/csrc/pauli_gemm.hip"],
+    # --pin '{"key": "pauli_gemm_dma_kernel_c3", "sources": ["yggdrasil_amd/csrc/pauli_gemm.hip"],
     #         "traffic_bytes_per_launch": 4.1e8, "mfma_busy": 0.36, "profile": "profiles/....md"}'
     ap.add_argument("--pin", default=None)
     return ap.parse_args()
@@ -792,7 +792,7 @@ def main():
         ach = head["_flops_per_launch"] / (head["_ms_per_launch"] * 1e-3)
         peak = PEAK_F32 if CONFIGS[head_name]["dtype"] == "f32" else PEAK_BF16
         pauli = CONFIGS[head_name]["fmt"] == "pauli"
-        kern = "pauli_gemm_kernel" if pauli else "grouped_cl_mfma"
+        kern = "pauli_gemm_dma_kernel" if pauli else "grouped_cl_mfma"
         roof = dict(bound="mfma", kernel=f"{kern} (mean of the up and down expert products)",
                     achieved=ach / 1e12, peak=peak / 1e12, unit="TFLOP/s", frac=ach / peak, traffic=None)
         if pauli:

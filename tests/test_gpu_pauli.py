@@ -178,6 +178,32 @@ def test_pauli_small_integer_product_is_exact(E, d_in, d_out, P, N, x_layout, bi
         assert np.array_equal(y[rows], ref), e
 
 
+@pytest.mark.parametrize("E,d_in,d_out,P,N", [(2, 512, 512, 3000, 1000), (3, 128, 512, 6000, 2000)])
+def test_pauli_integer_product_exact_at_full_load(E, d_in, d_out, P, N):
+    """Exact integer products with every CU busy (hundreds of tiles): staged chunks that a
+    wait let through before they landed would show as whole wrong tiles.  The reference is
+    the dense L(W) product in float64 (``oracle.dense.linear``)."""
+    from oracle import dense
+    ops = _ops()
+    g = np.random.default_rng(d_in + P)
+    W = g.integers(-2, 3, size=(E, d_out, d_in, 8)).astype(np.float32)
+    x = g.integers(-2, 3, size=(N, d_in, 8)).astype(np.float32)
+    b = g.integers(-3, 4, size=(E, d_out, 8)).astype(np.float32)
+    gather = g.integers(0, N, P).astype(np.int32)
+    offsets = _offsets(g, E, P, empty_first=False)
+    say(f"pauli integer product at full load E={E} d_in={d_in} d_out={d_out} P={P}")
+    xt = ops.pauli_rows_from_blade(torch.from_numpy(x).cuda().bfloat16())
+    y = ops.pauli_grouped_linear(xt, ops.prepare_weights(torch.from_numpy(W).cuda(), "pauli"),
+                                 torch.from_numpy(offsets).cuda(), ops.prepare_bias(torch.from_numpy(b).cuda()),
+                                 "none", x_layout="pauli", gather=torch.from_numpy(gather).cuda(),
+                                 y_layout="blade", out_dtype=torch.float32).cpu().numpy()
+    for e in range(E):
+        rows = slice(offsets[e], offsets[e + 1])
+        ref = dense.linear(x[gather[rows]], W[e], b[e])
+        bad = np.nonzero(np.any(y[rows] != ref, axis=-1))
+        assert bad[0].size == 0, (e, bad[0][:8], bad[1][:8])
+
+
 def test_pauli_rejects_bad_arguments():
     ops = _ops()
     with pytest.raises(ValueError):
