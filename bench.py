@@ -173,9 +173,19 @@ def make_inputs(torch, c, seed=0):
 # ---------------------------------------------------------------------------
 
 
+# Warm-up runs at least this long as well as at least W steps: a config that starts on an idle GPU
+# otherwise times its first steps before the clocks have settled (5 steps of config 3 take 2 ms)
+WARMUP_MIN_S = 0.3
+
+
 def time_fn(torch, fn, steps, warmup):
-    for _ in range(warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < WARMUP_MIN_S:
         fn()
+        n += 1
+        if n >= warmup and n % 8 == 0:
+            torch.cuda.synchronize()  # so the wall clock follows the device
     torch.cuda.synchronize()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
@@ -820,6 +830,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_min_s": WARMUP_MIN_S,
         "ms_per_step": head.get("ms_per_step"),
         "higher_is_better": True,
         "scaling": "weak",

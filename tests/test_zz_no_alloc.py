@@ -60,6 +60,8 @@ def _call(ops, noalloc, x, k, pu, pd, bu, bd, act, logits, rw, rb, residual):
 CASES = [
     # (name, dtype, fmt, N first, N second, d, F, E, k, router, residual)
     ("int8 decode, routed in the up product", torch.bfloat16, "int8", 64, 16, 128, 512, 32, 2, "logits", False),
+    ("int8 Pauli decode layer", torch.bfloat16, "int8_pauli", 64, 16, 128, 512, 32, 2, "logits", False),
+    ("int8 Pauli decode, grade-energy router", torch.bfloat16, "int8_pauli", 48, 20, 64, 128, 8, 2, "energy", True),
     ("bf16 Pauli", torch.bfloat16, "pauli", 512, 96, 32, 64, 8, 2, "logits", True),
     ("fp32 Pauli, grade-energy router", torch.float32, "pauli_f32", 300, 33, 16, 32, 6, 2, "energy", False),
     ("bf16 L(w) blocks", torch.bfloat16, "bf16", 200, 40, 16, 32, 4, 3, "logits", False),
