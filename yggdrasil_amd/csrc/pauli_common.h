@@ -112,7 +112,14 @@ __device__ inline uint32_t pack2_bf16(float lo, float hi) {
 __device__ inline float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
-// (re, im) -> (im, -re) on each bf16 pair of a dword
-__device__ inline uint32_t rot_conj(uint32_t w) { return __builtin_amdgcn_alignbit(w, w, 16) ^ 0x80000000u; }
+// (re, im) -> (im, -re) on each bf16 pair of a dword, in one packed 16-bit add:
+// op_sel swaps the halves of w, and adding 0x8000 to the new high half flips its
+// sign bit (no carry reaches the other half).  The compiler builds it from two
+// instructions (a shift and an add), and this runs twice per MFMA.
+__device__ inline uint32_t rot_conj(uint32_t w) {
+  uint32_t r;
+  asm("v_pk_add_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[0,1]" : "=v"(r) : "v"(w), "s"(0x80000000u));
+  return r;
+}
 
 }  // namespace ygg
