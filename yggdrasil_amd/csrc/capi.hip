@@ -177,20 +177,31 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     return combine_planes(static_cast<const float*>(ys), decode_layer_planes(F), (int)P, N, k, d, topk_idx, topk_w,
                           slot_pos, residual, out, dtype, stream);
   }
+  // the Pauli formats' conversion of x to Pauli rows (into the x_sorted region: N <= P
+  // rows) runs as extra workgroups of the routing's first launch
+  ygg::RowConvert cv;
+  if (w_format == kWPauli || w_format == kWPauliF32) {
+    cv.x = x;
+    cv.out = xs;
+    cv.n = (long long)N * d;
+    cv.d = d;
+    cv.kind = w_format == kWPauli ? ygg::kConvBf16Pauli : ygg::kConvF32Pauli;
+  }
   if (fused_route) {
     // routed below
   } else if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
-    if (ygg_route_energy(x, dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos,
-                         lg, rws, rws_bytes, stream))
+    if (ygg::route_energy_convert(x, dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm,
+                                  slot_pos, lg, rws, rws_bytes, cv, stream))
       return -1;
-  } else if (ygg_route(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) {
+  } else if (ygg::route_convert(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, rws, rws_bytes,
+                                cv, stream)) {
     return -1;
   }
   if (w_format == kWPauliF32) {
-    // fp32 Pauli: x -> split rows once (x_sorted region), up gathers them through
-    // perm, down in K splits whose partial planes the combine adds in split order
+    // fp32 Pauli: x's Pauli rows (converted with the routing) are gathered through perm
+    // by the up product; the down product runs in K splits whose partial planes the
+    // combine adds in split order
     const int splits = pauli_f32_splits((int)P, E, F, d);
-    if (ygg_pauli_rows_from_blade_f32(static_cast<const float*>(x), N, d, static_cast<float*>(xs), stream)) return -1;
     if (pauli_f32_linear_save_pre(static_cast<const float*>(xs), perm, (int)P, static_cast<const float*>(w_up), b_up,
                                   offsets, E, d, F, act, static_cast<float*>(h), h_pre_out, stream))
       return -1;
@@ -201,10 +212,9 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
                           residual, out, dtype, stream);
   }
   if (w_format == kWPauli) {
-    // x -> Pauli half-rows once (in the x_sorted region: N <= P rows); up: gather those
-    // rows through perm inside the product -> h in Pauli half-rows; down: h -> y_sorted
-    // in blade order.  No expert-grouped copy of x is made.
-    if (ygg_pauli_rows_from_blade(x, N, d, xs, stream)) return -1;
+    // x's Pauli half-rows (converted with the routing); up: gather those rows through
+    // perm inside the product -> h in Pauli half-rows; down: h -> y_sorted in blade
+    // order.  No expert-grouped copy of x is made.
     if (ygg_pauli_grouped_linear(xs, /*Pauli rows*/ 1, N, perm, (int)P, w_up, b_up, offsets, E, d, F, act, h,
                                  /*Pauli rows*/ 0, kBF16, stream))
       return -1;
@@ -453,18 +463,27 @@ YGG_API int ygg_moe_backward(const float* x, int N, int d, int F, int E, int k, 
   float* dp = static_cast<float*>(take());  // Pauli rows of dy
   void* wg = take();                        // weight-gradient partial sums
 
-  if (logits) {
-    if (ygg_route(logits, N, E, k, idx, tw, counts, offsets, perm, slot_pos, rws, rws_bytes, stream)) return -1;
-  } else if (ygg_route_energy(x, kF32, N, d, router_w, router_b, E, k, idx, tw, counts, offsets, perm, slot_pos, lg,
-                              rws, rws_bytes, stream)) {
-    return -1;
-  }
   // forward recompute: h_pre (unless the forward kept it), h (Pauli rows), y (blade, for dtopk_w)
   const float* hp_in = h_pre_saved;
   // the MFMA weight gradient pays off with enough rows per expert; below that the
   // vector-ALU kernel, which spreads a tile's pairs over more waves, is faster
   const bool wg_mfma = P >= (size_t)kWgradMfmaRowsPerExpert * E;
-  if ((!hp_in || wg_mfma) && ygg_pauli_rows_from_blade_f32(x, N, d, xp, stream)) return -1;
+  // x's Pauli rows, when needed, are converted by extra workgroups of the routing launch
+  ygg::RowConvert cv;
+  if (!hp_in || wg_mfma) {
+    cv.x = x;
+    cv.out = xp;
+    cv.n = (long long)N * d;
+    cv.d = d;
+    cv.kind = ygg::kConvF32Pauli;
+  }
+  if (logits) {
+    if (ygg::route_convert(logits, N, E, k, idx, tw, counts, offsets, perm, slot_pos, rws, rws_bytes, cv, stream))
+      return -1;
+  } else if (ygg::route_energy_convert(x, kF32, N, d, router_w, router_b, E, k, idx, tw, counts, offsets, perm,
+                                       slot_pos, lg, rws, rws_bytes, cv, stream)) {
+    return -1;
+  }
   if (!hp_in) {
     if (ygg_pauli_grouped_linear_f32(xp, perm, (int)P, w_up, b_up, offsets, E, d, F, kActNone, h_pre, 1, stream))
       return -1;

@@ -112,6 +112,55 @@ __device__ inline uint32_t pack2_bf16(float lo, float hi) {
 __device__ inline float bf_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
 __device__ inline float bf_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
 
+// Multivector n = m d + i of blade-order bf16 rows (rows, d, 8) -> its two Pauli
+// half-rows (bf16, rounded to nearest even): (M00, M10) at half-row 2 m, (M01, M11)
+// at 2 m + 1, (re, im) each.
+__device__ inline void pauli_rows_bf16_one(const uint16_t* __restrict__ x, int d, size_t n,
+                                           uint16_t* __restrict__ out) {
+  const size_t m = n / d;
+  const int i = (int)(n - m * d);
+  const uint4 q = *reinterpret_cast<const uint4*>(x + n * 8);
+  const float v[8] = {bf_lo(q.x), bf_hi(q.x), bf_lo(q.y), bf_hi(q.y), bf_lo(q.z), bf_hi(q.z), bf_lo(q.w), bf_hi(q.w)};
+  float c0[4], c1[4];
+  blade_to_pauli(v, c0, c1);
+  *reinterpret_cast<uint2*>(out + ((2 * m) * d + i) * 4) = make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+  *reinterpret_cast<uint2*>(out + ((2 * m + 1) * d + i) * 4) =
+      make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+}
+
+// Multivector n of blade-order fp32 rows -> its fp32 Pauli row record: eight floats
+// [b][k][c] (column b, re / im k, row c) at out + 8 n.
+__device__ inline void pauli_rows_f32_one(const float* __restrict__ x, size_t n, float* __restrict__ out) {
+  const float4 p0 = reinterpret_cast<const float4*>(x + n * 8)[0];
+  const float4 p1 = reinterpret_cast<const float4*>(x + n * 8)[1];
+  const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+  float c0[4], c1[4];
+  blade_to_pauli(v, c0, c1);
+  float4* q = reinterpret_cast<float4*>(out + n * 8);
+  q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+  q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+}
+
+// Workgroup b's share of a RowConvert riding on another launch: THREADS x U
+// multivectors, U per thread at a stride of THREADS (coalesced).
+template <int THREADS, int U>
+__device__ inline void convert_rows_block(const RowConvert& cv, int b) {
+  const long long base = (long long)b * THREADS * U + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const long long n = base + (long long)u * THREADS;
+    if (n >= cv.n) break;
+    if (cv.kind == kConvBf16Pauli)
+      pauli_rows_bf16_one(static_cast<const uint16_t*>(cv.x), cv.d, (size_t)n, static_cast<uint16_t*>(cv.out));
+    else
+      pauli_rows_f32_one(static_cast<const float*>(cv.x), (size_t)n, static_cast<float*>(cv.out));
+  }
+}
+template <int THREADS, int U>
+inline int convert_rows_blocks(const RowConvert& cv) {
+  return cv.kind == kConvNone ? 0 : (int)((cv.n + (long long)THREADS * U - 1) / ((long long)THREADS * U));
+}
+
 // (re, im) -> (im, -re) on each bf16 pair of a dword, in one packed 16-bit add:
 // op_sel swaps the halves of w, and adding 0x8000 to the new high half flips its
 // sign bit (no carry reaches the other half).  The compiler builds it from two

@@ -316,14 +316,7 @@ __global__ __launch_bounds__(256) void blade_to_pauli_f32_rows_kernel(const floa
                                                                       float* __restrict__ out) {
   const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= (size_t)rows * d) return;
-  const float4 p0 = reinterpret_cast<const float4*>(x + n * 8)[0];
-  const float4 p1 = reinterpret_cast<const float4*>(x + n * 8)[1];
-  const float v[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-  float c0[4], c1[4];
-  blade_to_pauli(v, c0, c1);
-  float4* q = reinterpret_cast<float4*>(out + n * 8);  // [b][k][c]
-  q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
-  q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+  pauli_rows_f32_one(x, n, out);
 }
 
 // b (K, N, 8) fp32 blade -> Pauli rows of its transpose (N, K): row n holds b[:, n].

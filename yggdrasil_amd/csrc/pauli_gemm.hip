@@ -855,15 +855,7 @@ __global__ __launch_bounds__(256) void blade_to_pauli_rows_kernel(const uint16_t
                                                                   uint16_t* __restrict__ out) {
   const size_t n = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= (size_t)rows * d) return;
-  const size_t m = n / d;
-  const int i = (int)(n % d);
-  const uint4 q = *reinterpret_cast<const uint4*>(x + n * 8);
-  const float v[8] = {bf_lo(q.x), bf_hi(q.x), bf_lo(q.y), bf_hi(q.y), bf_lo(q.z), bf_hi(q.z), bf_lo(q.w), bf_hi(q.w)};
-  float c0[4], c1[4];
-  blade_to_pauli(v, c0, c1);
-  *reinterpret_cast<uint2*>(out + ((2 * m) * d + i) * 4) = make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
-  *reinterpret_cast<uint2*>(out + ((2 * m + 1) * d + i) * 4) =
-      make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+  pauli_rows_bf16_one(x, d, n, out);
 }
 
 }  // namespace ygg

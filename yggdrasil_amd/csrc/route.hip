@@ -31,6 +31,7 @@
 // Within an expert the rows are in ascending token order, the reference's
 // dispatch order (hlm_block.py:172-178).
 
+#include "pauli_common.h"
 #include "route_select.h"
 #include "ygg_common.h"
 
@@ -38,14 +39,20 @@ namespace ygg {
 
 constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
+constexpr int kSelConvPerThread = 4;                  // multivectors per thread of a conversion workgroup
 
 template <int Q>  // Q = ceil(E / 8) logits per lane
 __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
                                                           int32_t* __restrict__ topk_idx,
                                                           float* __restrict__ topk_w,
                                                           int32_t* __restrict__ slot_rank,
-                                                          int32_t* __restrict__ block_hist) {
+                                                          int32_t* __restrict__ block_hist, int n_sel,
+                                                          RowConvert cv) {
   __shared__ int32_t wave_cnt[kSelBlock / 64][kMaxExperts];
+  if ((int)blockIdx.x >= n_sel) {  // a conversion workgroup
+    convert_rows_block<kSelBlock, kSelConvPerThread>(cv, (int)blockIdx.x - n_sel);
+    return;
+  }
   const int tid = threadIdx.x;
   const int j = tid & (kSelLanes - 1);
   const int t = blockIdx.x * kSelTokens + tid / kSelLanes;
@@ -77,7 +84,7 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
     int c = 0;
 #pragma unroll
     for (int w = 0; w < kSelBlock / 64; ++w) c += wave_cnt[w][tid];
-    block_hist[(size_t)tid * gridDim.x + blockIdx.x] = c;  // expert-major: [E][blocks]
+    block_hist[(size_t)tid * n_sel + blockIdx.x] = c;  // expert-major: [E][blocks]
   }
 }
 
@@ -193,10 +200,14 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
                                                              int32_t* __restrict__ counts,
                                                              int32_t* __restrict__ offsets,
                                                              int32_t* __restrict__ perm,
-                                                             int32_t* __restrict__ slot_pos) {
+                                                             int32_t* __restrict__ slot_pos, RowConvert cv) {
   __shared__ int32_t cnt[kMaxExperts][kSmallGroups];  // slots per (expert, group), then their base
   __shared__ int32_t tot[kMaxExperts];
   __shared__ int32_t eoff[kMaxExperts];
+  if (blockIdx.x > 0) {  // a conversion workgroup
+    convert_rows_block<kSmallThreads, 1>(cv, (int)blockIdx.x - 1);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = tid & (kSelLanes - 1);
   const int ngroups = (N + 7) / 8;
@@ -329,12 +340,13 @@ namespace {
 template <bool FROM_X>
 int launch_route_small(const float* logits, const void* x, int x_dtype, int d, const float* rw, const float* rb, int N,
                        int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
-                       int32_t* perm, int32_t* slot_pos, hipStream_t stream) {
+                       int32_t* perm, int32_t* slot_pos, const RowConvert& cv, hipStream_t stream) {
+  const unsigned grid = 1u + (unsigned)convert_rows_blocks<kSmallThreads, 1>(cv);
   switch ((E + 7) / 8) {
 #define YGG_SMALL(Q)                                                                                              \
   case Q:                                                                                                         \
-    route_small<Q, FROM_X><<<1, kSmallThreads, 0, stream>>>(logits, x, x_dtype, d, rw, rb, N, E, k, topk_idx,     \
-                                                            topk_w, counts, offsets, perm, slot_pos);            \
+    route_small<Q, FROM_X><<<grid, kSmallThreads, 0, stream>>>(logits, x, x_dtype, d, rw, rb, N, E, k, topk_idx,  \
+                                                               topk_w, counts, offsets, perm, slot_pos, cv);      \
     break;
     YGG_SMALL(1) YGG_SMALL(2) YGG_SMALL(3) YGG_SMALL(4) YGG_SMALL(5) YGG_SMALL(6) YGG_SMALL(7) YGG_SMALL(8)
 #undef YGG_SMALL
@@ -352,6 +364,15 @@ YGG_API size_t ygg_route_workspace_bytes(int N, int E, int k) {
 YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
                       int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
                       hipStream_t stream) {
+  return ygg::route_convert(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, workspace,
+                            workspace_bytes, RowConvert{}, stream);
+}
+
+// The conversion's workgroups follow the routing's own in its first launch: they
+// do not depend on it, and the short routing kernels leave most of the chip idle.
+int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                       int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
+                       const RowConvert& cv, hipStream_t stream) {
   YGG_CHECK_ARG(N >= 0, "ygg_route: N=%d must be >= 0", N);
   YGG_CHECK_ARG(E >= 1 && E <= kMaxExperts, "ygg_route: E=%d out of range [1, %d]", E, kMaxExperts);
   YGG_CHECK_ARG(k >= 1 && k <= kMaxTopK && k <= E, "ygg_route: k=%d out of range [1, min(%d, E=%d)]", k, kMaxTopK, E);
@@ -362,15 +383,17 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
   YGG_CHECK_ARG(counts && offsets, "ygg_route: null counts/offsets");
   if (N > 0 && N <= kSmallMaxN)
     return launch_route_small<false>(logits, nullptr, 0, 0, nullptr, nullptr, N, E, k, topk_idx, topk_w, counts,
-                                     offsets, perm, slot_pos, stream);
+                                     offsets, perm, slot_pos, cv, stream);
   const int nb = (N + kSelTokens - 1) / kSelTokens;
   int32_t* block_hist = static_cast<int32_t*>(workspace);
-  if (nb > 0) {
+  const int conv_blocks = convert_rows_blocks<kSelBlock, kSelConvPerThread>(cv);
+  if (nb + conv_blocks > 0) {
     // slot ranks go to slot_pos; route_scan_place turns them into rows
     switch ((E + 7) / 8) {
-#define YGG_SEL(Q)                                                                                            \
-  case Q:                                                                                                     \
-    route_select<Q><<<nb, kSelBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_pos, block_hist); \
+#define YGG_SEL(Q)                                                                                          \
+  case Q:                                                                                                   \
+    route_select<Q><<<nb + conv_blocks, kSelBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_pos, \
+                                                                block_hist, nb, cv);                        \
     break;
       YGG_SEL(1) YGG_SEL(2) YGG_SEL(3) YGG_SEL(4) YGG_SEL(5) YGG_SEL(6) YGG_SEL(7) YGG_SEL(8)
 #undef YGG_SEL
@@ -490,6 +513,14 @@ YGG_API int ygg_route_energy(const void* x, int x_dtype, int N, int d, const flo
                              int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
                              int32_t* perm, int32_t* slot_pos, float* logits_scratch, void* workspace,
                              size_t workspace_bytes, hipStream_t stream) {
+  return ygg::route_energy_convert(x, x_dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm,
+                                   slot_pos, logits_scratch, workspace, workspace_bytes, RowConvert{}, stream);
+}
+
+int ygg::route_energy_convert(const void* x, int x_dtype, int N, int d, const float* router_w, const float* router_b,
+                              int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets,
+                              int32_t* perm, int32_t* slot_pos, float* logits_scratch, void* workspace,
+                              size_t workspace_bytes, const RowConvert& cv, hipStream_t stream) {
   YGG_CHECK_ARG(x_dtype == kF32 || x_dtype == kBF16, "ygg_route_energy: x dtype %d unsupported", x_dtype);
   YGG_CHECK_ARG(N >= 0 && d >= 1, "ygg_route_energy: bad sizes N=%d d=%d", N, d);
   YGG_CHECK_ARG(E >= 1 && E <= kMaxExperts, "ygg_route_energy: E=%d out of range [1, %d]", E, kMaxExperts);
@@ -500,11 +531,11 @@ YGG_API int ygg_route_energy(const void* x, int x_dtype, int N, int d, const flo
     YGG_CHECK_ARG(x && router_w && router_b && topk_idx && topk_w && perm && slot_pos,
                   "ygg_route_energy: null pointer argument");
     return launch_route_small<true>(nullptr, x, x_dtype, d, router_w, router_b, N, E, k, topk_idx, topk_w, counts,
-                                    offsets, perm, slot_pos, stream);
+                                    offsets, perm, slot_pos, cv, stream);
   }
   YGG_CHECK_ARG(N == 0 || logits_scratch, "ygg_route_energy: %d tokens need logits_scratch (N x E fp32)", N);
   if (N > 0 && ygg_router_energy_logits(x, x_dtype, N, d, router_w, router_b, E, logits_scratch, nullptr, stream))
     return -1;
-  return ygg_route(logits_scratch, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, workspace,
-                   workspace_bytes, stream);
+  return ygg::route_convert(logits_scratch, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, workspace,
+                            workspace_bytes, cv, stream);
 }

@@ -109,6 +109,28 @@ enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3, kWPauliF32 = 
 // bf16 Pauli weight layout (pauli_gemm.hip)
 int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
 
+// Blade rows -> Pauli rows carried by the workgroups of another launch (the routing
+// kernels append them to their own): n multivectors of x, rows of d, bf16 -> bf16
+// Pauli half-rows (ygg_pauli_rows_from_blade) or fp32 -> fp32 Pauli rows
+// (ygg_pauli_rows_from_blade_f32), with the same results as those calls.
+enum RowConvertKind : int { kConvNone = 0, kConvBf16Pauli = 1, kConvF32Pauli = 2 };
+struct RowConvert {
+  const void* x = nullptr;
+  void* out = nullptr;
+  long long n = 0;  // multivectors (rows x d)
+  int d = 0;
+  int kind = kConvNone;
+};
+// ygg_route that also runs `cv` in the same launch as its first kernel
+int route_convert(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
+                  int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
+                  const RowConvert& cv, hipStream_t stream);
+// ygg_route_energy likewise
+int route_energy_convert(const void* x, int x_dtype, int N, int d, const float* router_w, const float* router_b, int E,
+                         int k, int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                         int32_t* slot_pos, float* logits_scratch, void* workspace, size_t workspace_bytes,
+                         const RowConvert& cv, hipStream_t stream);
+
 // fp32 Pauli products (pauli_f32.hip): weight preparation (format 4), the
 // number of K splits the layer uses for a down product, and that K-split
 // product writing fp32 partial planes (splits, P_max, d_out, 8), blade order,
