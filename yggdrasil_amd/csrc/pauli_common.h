@@ -28,11 +28,18 @@ typedef float pf32x16_t __attribute__((ext_vector_type(16)));
 __device__ inline float fsigmoid(float z) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));
 }
-__device__ inline float gelu_gate(float v) {  // gelu(v) / v
-  const float k2 = 2.0f * 0.7978845608028654f;
-  return fsigmoid(k2 * (v + 0.044715f * v * v * v));
+// gelu(v) / v = sigma(k2 (v + 0.044715 v^3)) with k2 = 2 sqrt(2/pi), i.e.
+// 1 / (1 + 2^(v (a + b v^2))): a = -log2(e) k2, b = 0.044715 a folded into one
+// multiply-add (three VALU operations before the exponential instead of five).
+__device__ inline float gelu_gate(float v) {
+  constexpr float a = -1.4426950408889634f * 2.0f * 0.7978845608028654f;
+  constexpr float b = a * 0.044715f;
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * __builtin_fmaf(b, v * v, a)));
 }
-__device__ inline float ftanh(float t) { return 2.0f * fsigmoid(2.0f * t) - 1.0f; }
+// tanh(t) = 2 sigma(2 t) - 1, with -2 log2(e) folded
+__device__ inline float ftanh(float t) {
+  return __builtin_fmaf(2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-2.8853900817779268f * t)), -1.0f);
+}
 
 // y: blade order 1,e1,e2,e3,e12,e13,e23,e123
 template <int ACT>
@@ -40,8 +47,11 @@ __device__ inline void activate_blade(float* y) {
   if constexpr (ACT == kActNone) {
     return;
   } else {
-    const float m1 = __builtin_amdgcn_sqrtf(y[1] * y[1] + y[2] * y[2] + y[3] * y[3] + 1e-12f);
-    const float m2 = __builtin_amdgcn_sqrtf(y[4] * y[4] + y[5] * y[5] + y[6] * y[6] + 1e-12f);
+    // grade norms, sqrt(1e-12 + sum of squares) as three multiply-adds
+    const float m1 =
+        __builtin_amdgcn_sqrtf(__builtin_fmaf(y[3], y[3], __builtin_fmaf(y[2], y[2], __builtin_fmaf(y[1], y[1], 1e-12f))));
+    const float m2 =
+        __builtin_amdgcn_sqrtf(__builtin_fmaf(y[6], y[6], __builtin_fmaf(y[5], y[5], __builtin_fmaf(y[4], y[4], 1e-12f))));
     float f0, f1, f2;
     if constexpr (ACT == kActGelu) {
       f0 = gelu_gate(y[0]);
