@@ -502,6 +502,15 @@ __device__ __forceinline__ void dma_to_lds(__amdgpu_buffer_rsrc_t r, unsigned ch
   else
     asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(m0), "s"(r) : "m0");
 }
+// the same 16-byte load with a wave-uniform byte offset `soff` added in a scalar
+// register: a chunk's advance along K costs no vector instruction
+__device__ __forceinline__ void dma_to_lds_s(__amdgpu_buffer_rsrc_t r, unsigned char* lds, uint32_t off,
+                                             uint32_t soff) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds);
+  const uint32_t so = __builtin_amdgcn_readfirstlane(soff);
+  asm volatile("s_mov_b32 m0, %1\n\tbuffer_load_dwordx4 %0, %2, %3 offen lds" ::"v"(off), "s"(m0), "s"(r), "s"(so)
+               : "m0");
+}
 // wait until at most N vector memory operations of this wave are outstanding
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -604,7 +613,8 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     w_lim[u] = IP - (c >> 1);
     w_pc[u] = c * 16;
   }
-  uint32_t a_cur[4], w_cur[2];  // offsets of those pieces in the next chunk to issue
+  uint32_t a_cur[4], w_cur[2];  // offsets of those pieces in the tile's first chunk (the chunk's own
+                                // advance along K is a scalar offset)
 
   // next A chunk: chunk iak of tile iam, slot ias; next W chunk: chunk iwk of
   // tile iwm, slot iws (value selects throughout: a branch that increments one
@@ -631,10 +641,13 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     }
     const int p0 = iak * KC;  // first input pair of the chunk (16 multivectors)
     unsigned char* st = smem + ias * C::A_SLOT + 4 * wave * 1024;
+    const uint32_t so = (uint32_t)p0 * 16;
+    if (p0 + KC <= IP) {  // uniform: the whole chunk lies inside the K range
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      dma_to_lds<16>(x_rsrc, st + u * 1024, p0 < a_lim[u] ? a_cur[u] : kOff);
-      a_cur[u] += KC * 16;
+      for (int u = 0; u < 4; ++u) dma_to_lds_s(x_rsrc, st + u * 1024, a_cur[u], so);
+    } else {  // the K tail: pieces past it read zero
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dma_to_lds_s(x_rsrc, st + u * 1024, p0 < a_lim[u] ? a_cur[u] : kOff, so);
     }
     ++ia;
     ias = ias == C::NA - 1 ? 0 : ias + 1;
@@ -662,10 +675,13 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     }
     const int p0 = iwk * (KC / 2);  // first input pair of the chunk (8 multivectors)
     unsigned char* st = smem + C::W_OFF + iws * C::W_SLOT + 2 * wave * 1024;
+    const uint32_t so = (uint32_t)p0 * 32;
+    if (p0 + KC / 2 <= IP) {  // uniform: the whole chunk lies inside the K range
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      dma_to_lds<16>(w_rsrc, st + u * 1024, p0 < w_lim[u] ? w_cur[u] : kOff);
-      w_cur[u] += KC / 2 * 32;
+      for (int u = 0; u < 2; ++u) dma_to_lds_s(w_rsrc, st + u * 1024, w_cur[u], so);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) dma_to_lds_s(w_rsrc, st + u * 1024, p0 < w_lim[u] ? w_cur[u] : kOff, so);
     }
     ++iw;
     iws = iws == C::NW - 1 ? 0 : iws + 1;
