@@ -161,7 +161,7 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
                            stream))
       return -1;
     return combine_planes(static_cast<const float*>(ys), decode_pauli_planes(F), (int)P, N, k, d, topk_idx, topk_w,
-                          slot_pos, residual, out, dtype, stream);
+                          slot_pos, residual, out, dtype, stream, /*slot rows*/ true);
   }
   // decode layers given logits route inside their up product (no routing launch)
   const bool decode = decode_shape((int)P, E, w_format);

@@ -202,6 +202,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
   __shared__ float s_xmax[kDpBatch][2], s_xinv[kDpBatch], s_hinv[kDpBatch];
   __shared__ float s_hmax[kDpRb][kDpWaves][4];
   __shared__ int32_t rows_tok[kDpMaxTokens];           // this expert's tokens, ascending
+  __shared__ int32_t rows_slot[kDpMaxTokens];          // their slots t k + s: the partial planes' rows
   __shared__ int32_t s_cnt[kMaxExperts], s_wv[kDpSelPasses * kDpWaves];
   __shared__ int32_t s_sel[kDpMaxTokens * kMaxTopK];  // the selection: expert and weight of every slot
   __shared__ float s_w[kDpMaxTokens * kMaxTopK];
@@ -374,6 +375,12 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
     return;
   }
   __syncthreads();  // rows_tok is complete
+  for (int r = tid; r < n_e; r += kDpThreads) {  // (read after the conversion's barrier)
+    const int t = rows_tok[r];
+    int q = 0;
+    while (s_sel[t * k + q] != e) ++q;
+    rows_slot[r] = t * k + q;
+  }
 
   // ---- 3. the input rows of the first batch (load l: token 4 l + tid / 128, input
   // tid % 128), then the down weights: wave w takes output column blocks 2 w and
@@ -573,7 +580,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
         const float4 ys = a ? yhi : ylo, bs = a ? bhi : blo;
         const float4 o4 = make_float4(ys.x * sc + bs.x, ys.y * sc + bs.y, ys.z * sc + bs.z, ys.w * sc + bs.w);
         if (tk < nb && o < d)
-          *reinterpret_cast<float4*>(planes + (((size_t)c * P_max + row_beg + b0 + tk) * d + o) * 8 + 4 * a) = o4;
+          *reinterpret_cast<float4*>(planes + (((size_t)c * P_max + rows_slot[b0 + tk]) * d + o) * 8 + 4 * a) = o4;
       }
     }
   }

@@ -197,7 +197,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 // together: a thread waits for memory twice (routing, then rows).
 constexpr int kPlaneBatch = 4;
 
-template <int OT, bool RESID>
+// SLOT_ROWS: the planes hold slot (t, s) at row t k + s (the int8 Pauli decode layer
+// writes them so) instead of at slot_pos[t k + s]
+template <int OT, bool RESID, bool SLOT_ROWS>
 __global__ __launch_bounds__(256) void combine_planes_kernel(const float* __restrict__ ys, int N, int k, int d,
                                                              const int32_t* __restrict__ topk_idx,
                                                              const float* __restrict__ topk_w,
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(256) void combine_planes_kernel(const float* __rest
 #pragma unroll
   for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
     const size_t f = (size_t)t * k + min(s, k - 1);
-    const int e = topk_idx[f], rw = slot_pos[f];
+    const int e = topk_idx[f], rw = SLOT_ROWS ? (int)f : slot_pos[f];
     const float ws = topk_w[f];
     const bool on = s < k;
     ex[s] = on ? e : 0x7fffffff;
@@ -287,7 +289,7 @@ __global__ __launch_bounds__(256) void combine_planes_kernel(const float* __rest
 // and the loads of two slots x all planes issued together -- one wait for the
 // routing, one for the rows.  Same additions in the same order as above, so the
 // result is identical.
-template <int OT, bool RESID, int PL>
+template <int OT, bool RESID, int PL, bool SLOT_ROWS>
 __global__ __launch_bounds__(256) void combine_planes_half_kernel(const float* __restrict__ ys, int N, int k, int d,
                                                                   const int32_t* __restrict__ topk_idx,
                                                                   const float* __restrict__ topk_w,
@@ -300,18 +302,6 @@ __global__ __launch_bounds__(256) void combine_planes_half_kernel(const float* _
   const size_t mv = n >> 1;
   const int half = (int)(n & 1);
   const int t = (int)(mv / d), i = (int)(mv % d);
-  int ex[8], row[8];
-  float w[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
-    const size_t f = (size_t)t * k + min(s, k - 1);
-    const int e = topk_idx[f], rw = slot_pos[f];
-    const float ws = topk_w[f];
-    const bool on = s < k;
-    ex[s] = on ? e : 0x7fffffff;
-    row[s] = on ? rw : 0;
-    w[s] = on ? ws : 0.f;
-  }
   float r[4] = {0.f, 0.f, 0.f, 0.f};
   if constexpr (RESID) {
     if constexpr (OT == kF32) {
@@ -322,6 +312,56 @@ __global__ __launch_bounds__(256) void combine_planes_half_kernel(const float* _
       r[0] = bf16_bits_to_f32((uint16_t)(q.x & 0xffffu)); r[1] = bf16_bits_to_f32((uint16_t)(q.x >> 16));
       r[2] = bf16_bits_to_f32((uint16_t)(q.y & 0xffffu)); r[3] = bf16_bits_to_f32((uint16_t)(q.y >> 16));
     }
+  }
+  auto store = [&](const float (&acc)[4]) __attribute__((always_inline)) {
+    if constexpr (OT == kF32) {
+      reinterpret_cast<float4*>(out)[n] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    } else {
+      reinterpret_cast<uint2*>(out)[n] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+    }
+  };
+  if constexpr (SLOT_ROWS) {
+    if (k == 2) {  // uniform.  The rows do not depend on the routing arrays, so every load goes
+      // out at once; and with two slots the ascending-expert order needs no sort:
+      // (0 + a) + b == (0 + b) + a exactly
+      const size_t f0 = (size_t)t * 2;
+      float4 v[2][PL];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int p = 0; p < PL; ++p)
+          v[u][p] = reinterpret_cast<const float4*>(ys + p * plane_stride + ((f0 + u) * d + i) * 8)[half];
+      const float w2[2] = {topk_w[f0], topk_w[f0 + 1]};
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float y[4] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w};
+#pragma unroll
+        for (int p = 1; p < PL; ++p) {
+          y[0] = y[0] + v[u][p].x; y[1] = y[1] + v[u][p].y; y[2] = y[2] + v[u][p].z; y[3] = y[3] + v[u][p].w;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = acc[c] + w2[u] * y[c];
+      }
+      if constexpr (RESID) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = r[c] + acc[c];
+      }
+      store(acc);
+      return;
+    }
+  }
+  int ex[8], row[8];
+  float w[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
+    const size_t f = (size_t)t * k + min(s, k - 1);
+    const int e = topk_idx[f], rw = SLOT_ROWS ? (int)f : slot_pos[f];
+    const float ws = topk_w[f];
+    const bool on = s < k;
+    ex[s] = on ? e : 0x7fffffff;
+    row[s] = on ? rw : 0;
+    w[s] = on ? ws : 0.f;
   }
 #pragma unroll
   for (int a = 1; a < 8; ++a)
@@ -366,11 +406,7 @@ __global__ __launch_bounds__(256) void combine_planes_half_kernel(const float* _
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = r[c] + acc[c];
   }
-  if constexpr (OT == kF32) {
-    reinterpret_cast<float4*>(out)[n] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  } else {
-    reinterpret_cast<uint2*>(out)[n] = make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
-  }
+  store(acc);
 }
 
 }  // namespace ygg
@@ -408,15 +444,17 @@ static void launch_combine(int grid, hipStream_t st, const void* ys, int N, int 
 #undef YGG_C
 }
 
-int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
-                        const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
-                        hipStream_t stream) {
+template <bool SR>
+static int combine_planes_t(const float* y_planes, int planes, int P_max, int N, int k, int d,
+                            const int32_t* topk_idx, const float* topk_w, const int32_t* slot_pos, const void* residual,
+                            void* out, int out_dtype, hipStream_t stream) {
   if (N == 0) return 0;
   const size_t stride = (size_t)P_max * d;
   if (planes == 4 || planes == 8) {  // the decode layer's partial planes: the half-multivector kernel
     const unsigned hgrid = (unsigned)(((size_t)N * d * 2 + 255) / 256);
 #define YGG_CH(OT, RS, PL)                                                                                          \
-  combine_planes_half_kernel<OT, RS, PL><<<hgrid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos, \
+  combine_planes_half_kernel<OT, RS, PL, SR><<<hgrid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w,        \
+                                                                         slot_pos, \
                                                                      residual, out, stride * 8)
 #define YGG_CH2(PL)                                                                        \
   if (out_dtype == kF32) { if (residual) YGG_CH(kF32, true, PL); else YGG_CH(kF32, false, PL); } \
@@ -428,12 +466,22 @@ int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int
   }
   const unsigned grid = (unsigned)(((size_t)N * d + 255) / 256);
 #define YGG_CP(OT, RS)                                                                                            \
-  combine_planes_kernel<OT, RS><<<grid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos, residual, \
+  combine_planes_kernel<OT, RS, SR><<<grid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w, slot_pos,        \
+                                                              residual, \
                                                           out, planes, stride)
   if (out_dtype == kF32) { if (residual) YGG_CP(kF32, true); else YGG_CP(kF32, false); }
   else { if (residual) YGG_CP(kBF16, true); else YGG_CP(kBF16, false); }
 #undef YGG_CP
   return check_launch("combine (partial planes)");
+}
+
+int ygg::combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
+                        const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
+                        hipStream_t stream, bool slot_rows) {
+  return slot_rows ? combine_planes_t<true>(y_planes, planes, P_max, N, k, d, topk_idx, topk_w, slot_pos, residual, out,
+                                            out_dtype, stream)
+                   : combine_planes_t<false>(y_planes, planes, P_max, N, k, d, topk_idx, topk_w, slot_pos, residual,
+                                             out, out_dtype, stream);
 }
 
 YGG_API int ygg_combine(const void* y_sorted, int y_dtype, int y_mask_order, int N, int k, int d,

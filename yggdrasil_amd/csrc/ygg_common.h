@@ -195,9 +195,10 @@ int decode_pauli_layer(const uint16_t* x, const float* logits, int N, int E, int
 
 // combine of fp32 blade-order partial planes (dispatch.hip): the planes of a
 // row are added in plane order, then weighted and combined as ygg_combine does.
+// slot_rows: the planes hold slot (t, s) at row t k + s, not at slot_pos[t k + s]
 int combine_planes(const float* y_planes, int planes, int P_max, int N, int k, int d, const int32_t* topk_idx,
                    const float* topk_w, const int32_t* slot_pos, const void* residual, void* out, int out_dtype,
-                   hipStream_t stream);
+                   hipStream_t stream, bool slot_rows = false);
 
 // backward pieces (backward.hip), all fp32 blade order: the grouped weight
 // gradient dW[e, j, i] = sum_rows dy[r, j] ~a[src(r), i] (src through gather
