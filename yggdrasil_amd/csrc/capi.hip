@@ -90,6 +90,7 @@ YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dt
   b += align256(P * d * 8 * es);          // x_sorted (Pauli half-rows of x for format 3)
   b += align256(P * F * 8 * es);          // h
   b += align256(ys_bytes(P, E, d, F, dtype, w_format));  // y_sorted
+  if (w_format == kWPauliF32) b += align256(P * 4);       // row_slot: each row's slot, for the partial planes
   return b;
 }
 
@@ -187,6 +188,14 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     cv.d = d;
     cv.kind = w_format == kWPauli ? ygg::kConvBf16Pauli : ygg::kConvF32Pauli;
   }
+  // fp32 Pauli: the routing also writes each row's slot, and the down product its
+  // partial planes at slot rows t k + s (the combine's plane loads then need no
+  // routing array)
+  int32_t* row_slot = nullptr;
+  if (w_format == kWPauliF32) {
+    row_slot = reinterpret_cast<int32_t*>(static_cast<char*>(ys) + align256(ys_bytes(P, E, d, F, dtype, w_format)));
+    cv.row_slot = row_slot;
+  }
   if (fused_route) {
     // routed below
   } else if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
@@ -206,10 +215,10 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
                                   offsets, E, d, F, act, static_cast<float*>(h), h_pre_out, stream))
       return -1;
     if (pauli_f32_linear_partial(static_cast<const float*>(h), (int)P, static_cast<const float*>(w_down), b_down,
-                                 offsets, E, F, d, splits, static_cast<float*>(ys), stream))
+                                 offsets, E, F, d, splits, static_cast<float*>(ys), stream, row_slot))
       return -1;
     return combine_planes(static_cast<const float*>(ys), splits, (int)P, N, k, d, topk_idx, topk_w, slot_pos,
-                          residual, out, dtype, stream);
+                          residual, out, dtype, stream, /*slot rows*/ true);
   }
   if (w_format == kWPauli) {
     // x's Pauli half-rows (converted with the routing); up: gather those rows through

@@ -154,7 +154,8 @@ __device__ inline void f32_kloop(f32x16v_t (&acc)[WR][2][2], const float* const 
 template <int ACT, int OUT>
 __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y01i, float y10r, float y10i, float y11r,
                                     float y11i, const float* __restrict__ bias, int e, int row, int j, int d_out,
-                                    int split, int P_max, float* __restrict__ Y, float* __restrict__ Ypre) {
+                                    int split, int P_max, float* __restrict__ Y, float* __restrict__ Ypre,
+                                    const int32_t* __restrict__ row_map) {
   float y[8];
   pauli_to_blade(y00r, y00i, y01r, y01i, y10r, y10i, y11r, y11i, y);
   if (bias != nullptr && (OUT != kF32OutPartial || split == 0)) {
@@ -175,7 +176,8 @@ __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y0
     q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
   } else {
     size_t mv = OUT == kF32OutBladeT ? (size_t)j * P_max + row : (size_t)row * d_out + j;
-    if constexpr (OUT == kF32OutPartial) mv += (size_t)split * P_max * d_out;
+    if constexpr (OUT == kF32OutPartial)  // partial planes: at row_map[row] when given (slot rows)
+      mv = (size_t)split * P_max * d_out + (size_t)(row_map != nullptr ? row_map[row] : row) * d_out + j;
     else activate_blade<ACT>(y);
     float4* p = reinterpret_cast<float4*>(Y + mv * 8);
     p[0] = make_float4(y[0], y[1], y[2], y[3]);
@@ -187,7 +189,7 @@ template <int ACT, int OUT, int WR>  // WR row blocks of 16 tokens per wave
 __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(2))) void pauli_f32_kernel(
     const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
-    float* __restrict__ Y, float* __restrict__ Ypre, int n_xcd) {
+    float* __restrict__ Y, float* __restrict__ Ypre, const int32_t* __restrict__ row_map, int n_xcd) {
   constexpr int TOK = kF32Tok * WR;  // tokens per tile
   // the waves' partial sums: one round for WR = 1; for WR = 2 waves 2, 3 hand theirs
   // to waves 0, 1 first, so the buffer holds two waves' tiles
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
     }
     // Y[a][b]: a = 0 -> (x, y), a = 1 -> (z, w); b from the row
     f32_store_mv<ACT, OUT>(s0.x, s0.y, s1.x, s1.y, s0.z, s0.w, s1.z, s1.w, bias, e, row, j, d_out, split, P_max, Y,
-                           Ypre);
+                           Ypre, row_map);
   }
 }
 
@@ -391,7 +393,7 @@ dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd, int tok) {
 template <int OUT>
 int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const int32_t* gather, const float* W,
                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
-                   float* Ypre = nullptr) {
+                   float* Ypre = nullptr, const int32_t* row_map = nullptr) {
   const int n_xcd = f32_xcds();
   const dim3 g1 = f32_grid(P_max, E, d_out, splits, n_xcd, kF32Tok);
   const dim3 g2 = f32_grid(P_max, E, d_out, splits, n_xcd, 2 * kF32Tok);
@@ -404,10 +406,10 @@ int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const in
 #define YGG_F(A)                                                                                              \
   if (two)                                                                                                    \
     pauli_f32_kernel<A, OUT, 2><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
-                                                                 P_max, Y, Ypre, n_xcd);                      \
+                                                                 P_max, Y, Ypre, row_map, n_xcd);             \
   else                                                                                                        \
     pauli_f32_kernel<A, OUT, 1><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
-                                                                 P_max, Y, Ypre, n_xcd)
+                                                                 P_max, Y, Ypre, row_map, n_xcd)
   switch (act) {
     case kActNone: YGG_F(kActNone); break;
     case kActGelu: YGG_F(kActGelu); break;
@@ -435,10 +437,10 @@ int ygg::pauli_f32_splits(int P_max, int E, int d_in, int d_out) {
 
 int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias,
                                   const int32_t* offsets, int E, int d_in, int d_out, int splits, float* y_planes,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const int32_t* row_map) {
   if (P_max == 0) return 0;
   return launch_f32_act<kF32OutPartial>(kActNone, splits, stream, x, nullptr, w, bias, offsets, E, d_in, d_out, P_max,
-                                        y_planes);
+                                        y_planes, nullptr, row_map);
 }
 
 int ygg::pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, const float* w,

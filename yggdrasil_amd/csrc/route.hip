@@ -101,7 +101,8 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
                                                                 int E, int k, int32_t* __restrict__ perm,
                                                                 int32_t* __restrict__ slot_pos,
                                                                 int32_t* __restrict__ counts,
-                                                                int32_t* __restrict__ offsets) {
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ row_slot) {
   __shared__ int32_t s_tot[kMaxExperts];
   __shared__ int32_t s_off[kMaxExperts];
   __shared__ int32_t s_base[kMaxExperts][kPlaceMaxSel];
@@ -174,6 +175,7 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
     const int pos = s_off[my_e] + s_base[my_e][t / kSelTokens - sb0] + my_rank;
     slot_pos[f] = pos;
     perm[pos] = t;
+    if (row_slot != nullptr) row_slot[pos] = (int32_t)f;
   }
 }
 
@@ -283,6 +285,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
       const int pos = eoff[e] + cnt[e][grp] + slot_pos[f];
       slot_pos[f] = pos;
       perm[pos] = t;
+      if (cv.row_slot != nullptr) cv.row_slot[pos] = (int32_t)f;
     }
   }
 }
@@ -403,7 +406,7 @@ int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_i
   const size_t slots = (size_t)N * k;
   const unsigned place_blocks = slots ? (unsigned)((slots + kPlaceSlots - 1) / kPlaceSlots) : 1u;  // N = 0: counts 0
   route_scan_place<<<place_blocks, kPlaceSlots, 0, stream>>>(topk_idx, block_hist, N, nb, E, k, perm, slot_pos, counts,
-                                                             offsets);
+                                                             offsets, cv.row_slot);
   return check_launch("route_scan_place");
 }
 

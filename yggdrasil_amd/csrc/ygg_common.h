@@ -120,6 +120,9 @@ struct RowConvert {
   long long n = 0;  // multivectors (rows x d)
   int d = 0;
   int kind = kConvNone;
+  // when set, the routing also writes each expert-grouped row's slot:
+  // row_slot[slot_pos[f]] = f (the K-split products then write slot rows)
+  int32_t* row_slot = nullptr;
 };
 // ygg_route that also runs `cv` in the same launch as its first kernel
 int route_convert(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
@@ -143,7 +146,8 @@ int pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, 
                               const int32_t* offsets, int E, int d_in, int d_out, int act, float* y_pauli,
                               float* y_pre, hipStream_t stream);
 int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias, const int32_t* offsets,
-                             int E, int d_in, int d_out, int splits, float* y_planes, hipStream_t stream);
+                             int E, int d_in, int d_out, int splits, float* y_planes, hipStream_t stream,
+                             const int32_t* row_map = nullptr);  // row_map: the planes' row of each product row
 
 // decode-shape int8 products (clifford_gemm.hip): whether (P_max rows, E
 // experts, format) takes the weight-streaming kernel, its number of K splits
