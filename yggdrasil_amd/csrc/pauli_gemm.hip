@@ -739,6 +739,9 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   };
   auto mfmas = [&](auto nr_tag) __attribute__((always_inline)) {
     constexpr int NR = decltype(nr_tag)::value;
+    // raised issue priority while this wave feeds the MFMA pipe: the co-resident
+    // workgroup's wave on the SIMD then fills the gaps with its epilogue or loads
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int s = 0; s < KC / 4; ++s)
 #pragma unroll
@@ -756,6 +759,7 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
             acc[rb][cb][a][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, B, acc[rb][cb][a][1], 0, 0, 0);
           }
       }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   // a tile's accumulators start from its bias (slot m % 2, complete by the tile's first step)
