@@ -127,12 +127,16 @@ def test_layer_pauli_f32_against_reference_golden(name):
     _run_layer_case(name, fmt_override="pauli_f32")
 
 
-def test_layer_pauli_f32_large_down_splits():
-    """F = 1024 over few rows: the down product splits its contraction over several partial planes."""
+@pytest.mark.parametrize("N,k", [(96, 2), (96, 1), (96, 3), (180, 3)])
+def test_layer_pauli_f32_large_down_splits(N, k):
+    """F = 1024 over few rows: the down product splits its contraction over several partial planes,
+    written at slot rows t k + s.  (96, 2): 8 planes, the two-slot combine; (96, 1), (96, 3): 13 and 6
+    planes, the general plane combine; (180, 3): 4 planes, the half-multivector combine sorting three
+    slots by expert."""
     import yggdrasil_amd
 
-    g = np.random.default_rng(77)
-    N, d, F, E, k = 96, 64, 1024, 4, 2
+    g = np.random.default_rng(77 + N + k)
+    d, F, E = 64, 1024, 4
     x = g.standard_normal((1, N, d, 8), dtype=np.float32)
     wu = (g.standard_normal((E, F, d, 8), dtype=np.float32) / np.sqrt(8 * d)).astype(np.float32)
     wd = (g.standard_normal((E, d, F, 8), dtype=np.float32) / np.sqrt(8 * F)).astype(np.float32)
