@@ -164,6 +164,63 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         int tr = row[b]; row[b] = row[b - 1]; row[b - 1] = tr;
         float tw = w[b]; w[b] = w[b - 1]; w[b - 1] = tw;
       }
+  // k <= 4: the rows of KM slots loaded raw and unconditionally (a slot past k repeats
+  // the last row: a cache hit), all in flight before the first is used -- a load
+  // inside `if (s < k)` is waited for inside its branch, one round trip per slot.
+  // Same products and adds, in the same order, as the loop below.
+  auto rows_raw = [&](auto km_tag) __attribute__((always_inline)) {
+    constexpr int KM = decltype(km_tag)::value;
+    int rs[KM];
+#pragma unroll
+    for (int s = 0; s < KM; ++s) rs[s] = row[s < k ? s : k - 1];
+    for (int i = lane; i < d; i += 64) {
+      RawMV<YT> y[KM];
+#pragma unroll
+      for (int s = 0; s < KM; ++s) y[s] = load_raw<YT, false>(ys, (size_t)rs[s] * d + i);
+      MV acc;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
+#pragma unroll
+      for (int s = 0; s < KM; ++s) {
+        float v[8];
+        if constexpr (YT == kF32) {
+          const uint32_t u[8] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w, y[s].b.x, y[s].b.y, y[s].b.z, y[s].b.w};
+#pragma unroll
+          for (int c = 0; c < 8; ++c) v[c] = __uint_as_float(u[c]);
+        } else {
+          const uint32_t u[4] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v[2 * c] = bf16_bits_to_f32((uint16_t)(u[c] & 0xffff));
+            v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(u[c] >> 16));
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc.v[c] = s < k ? acc.v[c] + w[s] * v[c] : acc.v[c];
+      }
+      if constexpr (Y_MASK) {  // back to blade order
+        const float t3 = acc.v[3];
+        acc.v[3] = acc.v[4];
+        acc.v[4] = t3;
+      }
+      if constexpr (RESID) {
+        const MV r = load_mv<OT>(resid, (size_t)t * d + i);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc.v[c] = r.v[c] + acc.v[c];
+      }
+      store_mv<OT>(out, (size_t)t * d + i, acc);
+    }
+  };
+  if constexpr (YT == kBF16) {  // (fp32 rows: measured no faster, the loop below serves them)
+    if (k <= 2) {
+      rows_raw(std::integral_constant<int, 2>{});
+      return;
+    }
+    if (k <= 4) {
+      rows_raw(std::integral_constant<int, 4>{});
+      return;
+    }
+  }
   for (int i = lane; i < d; i += 64) {
     MV acc;
 #pragma unroll
