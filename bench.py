@@ -14,10 +14,13 @@ backward, fp32) at the config 1 and 3 shapes.
 
 One JSON line is printed.  ``roofline`` covers the dominant kernel, the
 grouped CliffordLinear MFMA kernel (both expert products), from HIP events
-around its launches on the stream it runs on; its ``frac`` counts algorithmic
-FLOPs (64 multiply-adds per multivector pair), ``mfma_issued_frac`` the ones
-the Pauli form issues, and HBM traffic / MFMA-busy counters appear only when
-``profiles/pins.json`` holds them for the current sources of the kernel.
+around its launches on the stream it runs on.  Its ``achieved`` and ``frac`` count
+the MFMA work the kernel issues (for the Pauli form 32 multiply-adds per
+multivector pair), so ``frac`` is a fraction of the hardware peak;
+``dense_equiv_tflops`` is the rate in the reference's arithmetic (64 multiply-adds
+per pair, the dense 8x8 L(w) block), an effective rate and no fraction of any peak.
+HBM traffic / MFMA-busy counters appear only when ``profiles/pins.json`` holds them
+for the current sources of the kernel.
 ``cpu_baseline`` (per BASELINE config under "configs", the headline's at the
 top) times the reference's own compiled CPU geometric matmul (``oracle/_ref``,
 built from the reference sources) -- or the C restatement if that is absent --
@@ -378,7 +381,9 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     out_t = torch.empty_like(x)
     ms_comb = time_fn(torch, lambda: ops.combine(ys, r, out=out_t), steps, warmup)
 
-    flops_proj = 128.0 * d * F * P  # per projection (algorithmic: 64 multiply-adds per multivector pair)
+    flops_proj = 128.0 * d * F * P  # per projection in the reference's arithmetic (64 multiply-adds per pair)
+    # what the MFMA units execute: the Pauli (complex 2x2) form issues 32 of the 64 multiply-adds
+    issued_proj = flops_proj / 2 if c["fmt"] in ("pauli", "pauli_f32") else flops_proj
     peak = PEAK_F32 if c["dtype"] == "f32" else PEAK_BF16
     # bytes each timed kernel moves itself.  route: logits in; top-k indices and weights,
     # slot positions, the permutation and the counts / offsets out.  The pass over x before
@@ -391,17 +396,15 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     b_comb = P * R + 12 * P + N * R
     res.update(
         kernels_ms=dict(route=ms_route, dispatch=ms_disp, expert_up=ms_up, expert_down=ms_down, combine=ms_comb),
-        expert_tflops=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
-        expert_mfma_frac=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / peak,
+        expert_tflops=2 * issued_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
+        expert_mfma_frac=2 * issued_proj / ((ms_up + ms_down) * 1e-3) / peak,
+        expert_dense_equiv_tflops=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
         kernel_bytes=dict(route=b_route, dispatch=b_pass, combine=b_comb),
         kernel_hbm_frac=dict(route=b_route / (ms_route * 1e-3) / PEAK_HBM, dispatch=b_pass / (ms_disp * 1e-3) / PEAK_HBM,
                              combine=b_comb / (ms_comb * 1e-3) / PEAK_HBM),
         route_dispatch_combine_hbm_frac=(b_route + b_pass + b_comb) / ((ms_route + ms_disp + ms_comb) * 1e-3) / PEAK_HBM)
-    if c["fmt"] in ("pauli", "pauli_f32"):
-        # the Pauli (complex 2x2) form issues 32 of the 64 multiply-adds: the MFMA pipes run at half
-        # the algorithmic rate
-        res["expert_mfma_issued_frac"] = res["expert_mfma_frac"] / 2
-    res["_flops_per_launch"] = flops_proj
+    res["_flops_per_launch"] = issued_proj
+    res["_dense_flops_per_launch"] = flops_proj
     res["_ms_per_launch"] = (ms_up + ms_down) / 2
     return res
 
@@ -437,11 +440,13 @@ def run_ep_config(torch, ops, name, c, steps, warmup):
                                               per, F, d, 0, y.data_ptr(), 1, dt, st))
 
     ms = time_fn(torch, step, steps, warmup)
-    flops = 2 * 128.0 * d * F * P
+    flops = 2 * 128.0 * d * F * P  # both products, the reference's 64 multiply-adds per pair
+    issued = flops / 2  # the Pauli form's 32
     return dict(workload=name, gpus_modelled=G, experts_here=list(range(e0, e0 + per)), rows_here=P,
                 rows_per_gpu=rows, straggler_ratio=P / (N * k / G), ms_per_step=ms,
-                rows_per_s=P / (ms * 1e-3), expert_tflops=flops / (ms * 1e-3) / 1e12,
-                expert_mfma_frac=flops / (ms * 1e-3) / PEAK_BF16)
+                rows_per_s=P / (ms * 1e-3), expert_tflops=issued / (ms * 1e-3) / 1e12,
+                expert_mfma_frac=issued / (ms * 1e-3) / PEAK_BF16,
+                expert_dense_equiv_tflops=flops / (ms * 1e-3) / 1e12)
 
 
 def run_block_config(torch, ops, name, c, steps, warmup):
@@ -534,12 +539,11 @@ def run_train_config(torch, ops, name, c, steps, warmup):
                 ms_per_step=ms, tokens_per_s=N / (ms * 1e-3), weight_grad_kernel=wg_kind,
                 kernels_ms=dict(weight_grad_up=ms_wg_up, weight_grad_down=ms_wg_down),
                 step_tflops=6 * flops_proj / (ms * 1e-3) / 1e12,
-                weight_grad_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,
-                # algorithmic: 64 multiply-adds per multivector pair; the Pauli form issues 32, so this
-                # rate can reach 2x the fp32 peak -- the issued fraction is the MFMA utilisation
-                weight_grad_algorithmic_frac_f32=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32,
-                weight_grad_issued_frac_f32=(flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32
-                                             if wg_kind == "mfma" else None))
+                # the reference's arithmetic (64 multiply-adds per multivector pair): an effective rate
+                weight_grad_dense_equiv_tflops=2 * flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / 1e12,
+                # the MFMA work issued (the Pauli form's 32 multiply-adds per pair) against the fp32 peak
+                weight_grad_mfma_frac_f32=(flops_proj / ((ms_wg_up + ms_wg_down) * 1e-3) / PEAK_F32
+                                           if wg_kind == "mfma" else None))
 
 
 def run_gm(torch, ops, name, c, steps, warmup):
@@ -549,19 +553,18 @@ def run_gm(torch, ops, name, c, steps, warmup):
     N, d, F = c["N"], c["d"], c["F"]
     res = dict(workload=name, dtype="f32", kernels=["pauli_f32_prep_kernel", "pauli_f32_rows_t_kernel",
                                                     "pauli_f32_kernel"],
-               # algorithmic: 64 multiply-adds per multivector pair; the Pauli form issues 32, so the
-               # algorithmic fraction can exceed 1 -- the issued fraction is the MFMA utilisation
-               frac_basis="algorithmic FLOPs against the fp32 MFMA peak; issued = algorithmic / 2")
+               frac_basis="MFMA work issued (the Pauli form's 32 multiply-adds per multivector pair) against "
+                          "the fp32 MFMA peak; dense_equiv_tflops counts the reference's 64 (an effective rate)")
     for tag, M, K in (("up", F, d), ("down", d, F)):
         a = torch.randn(M, K, 8, generator=g, device="cuda") / (8.0 * K) ** 0.5
         b = torch.randn(K, N, 8, generator=g, device="cuda")
         ws = torch.empty(ops.geom_matmul_workspace_bytes(M, K, N), device="cuda", dtype=torch.uint8)
         out = torch.empty((M, N, 8), device="cuda")
         ms = time_fn(torch, lambda: ops.geom_matmul(a, b, workspace=ws, out=out), steps, warmup)
-        flops = 128.0 * M * K * N  # algorithmic: 64 multiply-adds per multivector pair
-        res[tag] = dict(M=M, K=K, N=N, ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
-                        algorithmic_frac_f32=flops / (ms * 1e-3) / PEAK_F32,
-                        issued_frac_f32=flops / 2 / (ms * 1e-3) / PEAK_F32)
+        flops = 128.0 * M * K * N  # the reference's arithmetic: 64 multiply-adds per multivector pair
+        res[tag] = dict(M=M, K=K, N=N, ms=ms, tflops=flops / 2 / (ms * 1e-3) / 1e12,
+                        mfma_frac_f32=flops / 2 / (ms * 1e-3) / PEAK_F32,
+                        dense_equiv_tflops=flops / (ms * 1e-3) / 1e12)
         del a, b, ws, out
     return res
 
@@ -805,11 +808,14 @@ def main():
         kern = "pauli_gemm_dma_kernel" if pauli else "grouped_cl_mfma"
         roof = dict(bound="mfma", kernel=f"{kern} (mean of the up and down expert products)",
                     achieved=ach / 1e12, peak=peak / 1e12, unit="TFLOP/s", frac=ach / peak, traffic=None)
+        dense = head["_dense_flops_per_launch"] / (head["_ms_per_launch"] * 1e-3)
         if pauli:
-            # achieved counts the algorithmic 64 multiply-adds per multivector pair; the complex
-            # (Pauli) form issues 32, so frac can reach 2 and the MFMA pipes run at half of it
-            roof["frac_basis"] = "algorithmic FLOPs (64 multiply-adds per multivector pair); issued = frac / 2"
-            roof["mfma_issued_frac"] = ach / 2 / peak
+            # achieved and frac count the MFMA work issued: the complex (Pauli) form's 32
+            # multiply-adds per multivector pair; the reference's arithmetic (64, the dense L(w)
+            # block) is reported as an effective rate beside it
+            roof["frac_basis"] = ("MFMA work issued: 32 multiply-adds per multivector pair (Pauli form), "
+                                  "against the dense bf16 peak")
+        roof["dense_equiv_tflops"] = dense / 1e12
         pin = pinned(f"{kern}_{head_name}")
         if pin is not None:
             # HBM bytes per launch (mean of the two products, rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by
@@ -821,6 +827,7 @@ def main():
             roof["counters_from"] = pin["profile"]
     for r in results.values():
         r.pop("_flops_per_launch", None)
+        r.pop("_dense_flops_per_launch", None)
         r.pop("_ms_per_launch", None)
     c = CONFIGS[head_name]
     line = {

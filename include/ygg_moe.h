@@ -4,9 +4,16 @@
  * Library: yggdrasil_amd/lib/libygg_moe.so (hipcc, gfx950 code objects).
  *
  * Conventions (every entry point):
- *  - plain C types only; every pointer is a DEVICE pointer owned by the caller
- *    (the library allocates nothing and keeps no state between calls, except
- *    the per-GPU scratch array of ygg_moe_forward_noalloc);
+ *  - plain C types only; every pointer is a DEVICE pointer owned by the caller.
+ *    The library keeps no state between calls, except the per-GPU scratch array
+ *    of ygg_moe_forward_noalloc, and allocates nothing, with one exception:
+ *    ygg_geom_matmul_f32, which keeps the reference launcher's signature (no
+ *    workspace argument), takes its scratch from the stream-ordered pool
+ *    (hipMallocAsync / hipFreeAsync on `stream`); callers that cannot allocate
+ *    use ygg_geom_matmul_f32_ws with their own workspace;
+ *  - expert row ranges (`offsets`, E + 1 ascending values from 0 to the rows
+ *    the call names) are read on the device and trusted: the caller keeps them
+ *    ascending and within the rows (the Python wrappers clamp them so);
  *  - the work is enqueued on `stream` (a hipStream_t; pass the caller's
  *    current stream, e.g. torch.cuda.current_stream().cuda_stream);
  *  - the return value is 0 on success and -1 on a rejected argument or a
