@@ -163,3 +163,51 @@ def test_decode_pauli_energy_router_and_residual():
     err = normwise_err(y, ref)
     say(f"decode pauli energy router normwise error {err:.3e}")
     assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("fmt", ["int8_pauli", "int8"])
+def test_decode_tiny_and_nonfinite_tokens(fmt):
+    """Both int8 decode layers scale each token's row (and hidden row) by a power of two
+    before the integer or fp16 products.  Rows whose largest entry lies far below 2^-112
+    take the largest normal shift and quantize to (nearly) zero codes, so their outputs
+    stay the oracle's (the biases' image) instead of overflowing the scale; an all-zero
+    token gives the biases' image too.  A token holding a NaN or an Inf gives a non-finite
+    output row, as the reference's arithmetic does, and leaves every other token exact to
+    the int8 bound."""
+    yggdrasil_amd, ops = _mods()
+    g = np.random.default_rng(4242)
+    N, d, F, E, k = 32, 64, 128, 8, 2
+    x = _inputs.bf16_round(g.standard_normal((N, d, 8), dtype=np.float32))
+    x[0:4] *= np.float32(2.0 ** -120)   # near zero, representable in bf16 (2^-133 and up)
+    x[4] *= np.float32(2.0 ** -130)     # subnormal in bf16 and fp32
+    x[5] = 0.0
+    x[6, 3, 2] = np.nan
+    x[7, 10, 5] = np.inf
+    x = _inputs.bf16_round(x)
+    wu, bu, wd, bd = _inputs.expert_weights(g, E, d, F, bias_std=0.2)
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    cfg = yggdrasil_amd.MoEHLMConfig(d_model=d, d_ff=F, n_experts=E, top_k=k, dtype=torch.bfloat16,
+                                     weight_format=fmt, router="logits")
+    layer = yggdrasil_amd.CliffordMoELayer(cfg, device="cuda")
+    layer.load_reference_weights(w_up=wu, b_up=bu, w_down=wd, b_down=bd)
+    say(f"decode {fmt} tiny and non-finite tokens N={N} d={d} F={F} E={E} k={k}")
+    y = layer.moe_forward(torch.from_numpy(x).cuda().bfloat16().reshape(1, N, d, 8),
+                          logits=torch.from_numpy(logits).cuda()).float().cpu().numpy().reshape(N, d, 8)
+    idx, w = moe.route_topk(moe.softmax(logits), k)
+    assert np.array_equal(layer.last_routing["topk_idx"].cpu().numpy(), idx)
+    if fmt == "int8_pauli":
+        wu_q = moe.dequantize_int8_pauli(*moe.quantize_int8_pauli(wu))
+        wd_q = moe.dequantize_int8_pauli(*moe.quantize_int8_pauli(wd))
+    else:
+        wu_q, wd_q = moe.dequantize_int8(*moe.quantize_int8(wu)), moe.dequantize_int8(*moe.quantize_int8(wd))
+    bad = [6, 7]
+    good = [t for t in range(N) if t not in bad]
+    ref = _layer_ref(x[good], idx[good], w[good], wu_q, bu, wd_q, bd, "gelu")
+    assert np.isfinite(y[good]).all()
+    err = normwise_err(y[good], ref)
+    # the near-zero and zero tokens on their own: their outputs are the biases' image
+    err_tiny = normwise_err(y[:6], ref[:6])
+    say(f"decode {fmt} finite tokens normwise error {err:.3e}, near-zero tokens {err_tiny:.3e}")
+    assert err < TOL_BF16 and err_tiny < TOL_BF16
+    for t in bad:
+        assert not np.isfinite(y[t]).any(), f"token {t}: a non-finite input gave finite outputs"

@@ -56,12 +56,26 @@ __device__ inline int dc_wave_sum(int v) {
          (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
-// exponent shift that brings a row's largest magnitude m into [2^13, 2^14)
+// exponent shift that brings a row's largest magnitude m into [2^13, 2^14).  The
+// shift stops at 126 (2^126 and 2^-126 are normal floats), so a row whose largest
+// magnitude is below 2^-112 is scaled to below 2^14 and its tiniest entries round to
+// zero codes: its error stays below 2^-127 in absolute terms.  Zero and non-finite
+// maxima give 0 (a non-finite row's inverse scale is NaN, dc_inv_scale).
 __device__ inline int dc_shift(float m) {
   if (!(m > 0.f) || !(m < INFINITY)) return 0;
   int ex;
   frexpf(m, &ex);  // m = f 2^ex, f in [0.5, 1)
-  return 14 - ex;
+  return min(14 - ex, 126);
 }
+// |v| for a row maximum, with NaN counted as infinite: a row holding NaN or Inf has a
+// non-finite maximum (fmaxf would drop a NaN operand)
+__device__ inline float dc_mag(float v) {
+  const float a = fabsf(v);
+  return a == a ? a : INFINITY;
+}
+// the factor that undoes the shift sh of a row with maximum m: NaN for a non-finite
+// row, so that its outputs are NaN as the reference's arithmetic makes them (integer
+// codes cannot carry a NaN)
+__device__ inline float dc_inv_scale(float m, int sh) { return m < INFINITY ? ldexpf(1.0f, -sh) : __builtin_nanf(""); }
 
 }  // namespace ygg

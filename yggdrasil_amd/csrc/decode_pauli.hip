@@ -156,9 +156,12 @@ __global__ __launch_bounds__(256) void dp_prep_kernel(const float* __restrict__ 
   out[u] = make_uint4(word[0], word[1], word[2], word[3]);
 }
 
-// 16-bit fixed point value -> (hi, lo) int8 planes with v = 256 hi + lo, |v| <= 2^14
+// 16-bit fixed point value -> (hi, lo) int8 planes with v = 256 hi + lo, |v| <= 2^14.
+// x scale lies in [-2^14, 2^14] for every finite row; the clamp (NaN to 0) keeps the
+// conversion defined for a non-finite row, whose inverse scale makes its outputs NaN.
 __device__ inline void dp_split(float x, float scale, int& hi, int& lo) {
-  const int v = (int)rintf(x * scale);
+  const float t = x * scale;
+  const int v = (int)rintf(t == t ? fminf(fmaxf(t, -16384.f), 16384.f) : 0.f);
   hi = (v + 128) >> 8;
   lo = v - (hi << 8);
 }
@@ -443,7 +446,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       blade_to_pauli(b, &pv[l][0], &pv[l][4]);  // column 0 (M00, M10), column 1 (M01, M11)
       float m = 0.f;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(pv[l][q]));
+      for (int q = 0; q < 8; ++q) m = fmaxf(m, dc_mag(pv[l][q]));
       m = dc_wave_max(m);
       if (lane == 0) s_xmax[4 * l + xt][wave & 1] = m;
     }
@@ -453,9 +456,10 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
     for (int l = 0; l < kDpRb; ++l) {
       if (4 * l >= nb) break;
       const int tk = 4 * l + xt;
-      const int sh = dc_shift(fmaxf(s_xmax[tk][0], s_xmax[tk][1]));
+      const float mt = fmaxf(s_xmax[tk][0], s_xmax[tk][1]);
+      const int sh = dc_shift(mt);
       const float sc = ldexpf(1.0f, sh);
-      if (xi == 0) s_xinv[tk] = ldexpf(1.0f, -sh);
+      if (xi == 0) s_xinv[tk] = dc_inv_scale(mt, sh);
 #pragma unroll
       for (int v = 0; v < 4; ++v) {  // row (b, p) = (v / 2, v % 2): entries X[0][b].p, X[1][b].p
         const int b = v >> 1, p = v & 1;
@@ -515,7 +519,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       for (int q = 0; q < 4; ++q) {
         hc0[q] = ok ? hc0[q] : 0.f;
         hc1[q] = ok ? hc1[q] : 0.f;
-        m = fmaxf(m, fmaxf(fabsf(hc0[q]), fabsf(hc1[q])));
+        m = fmaxf(m, fmaxf(dc_mag(hc0[q]), dc_mag(hc1[q])));
       }
       m = dc_row_max(m);  // over the token's 8 channels x 2 rows in this wave
       if (n == 0) s_hmax[rb][wave][g] = m;
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       for (int w = 0; w < kDpWaves; ++w) mx = fmaxf(mx, s_hmax[rb][w][g]);
       const int sh = dc_shift(mx);
       const float hs = ldexpf(1.0f, sh);
-      if (wave == 0 && n == 0) s_hinv[tk] = ldexpf(1.0f, -sh);
+      if (wave == 0 && n == 0) s_hinv[tk] = dc_inv_scale(mx, sh);
       // lane (jj, a) writes the rows of column b = a: entries (H[0][a].p, H[1][a].p) at
       // K position hidden channel 8 wave + jj (K step wave / 4, lane group wave % 4)
 #pragma unroll
