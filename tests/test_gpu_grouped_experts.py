@@ -95,3 +95,34 @@ def test_layer_experts_flat_rows_and_range_check():
     bad[-1] += 1  # the last range runs past the rows
     with pytest.raises(ValueError):
         ops.grouped_experts(xt, off_t, bad, prep["w_up"], prep["w_down"], validate=True)
+
+
+@pytest.mark.parametrize("fmt", ["pauli", "pauli_f32", "bf16"])
+def test_grouped_experts_unvalidated_ranges_are_clamped(fmt):
+    """Without validation the ranges are clamped on the device into ascending bounds within
+    the rows: counts that sum past P (the last range running 50 rows past the end), or an
+    offset beyond P, reach the products as ranges inside [0, P].  The first gives exactly
+    the valid call's rows; in the second every expert from the bad offset on is empty and
+    the rows before it are the valid call's."""
+    from yggdrasil_amd import ops
+
+    E, d, F, P = 5, 32, 64, 240
+    x, (wu, bu, wd, bd), _, offsets, counts = _case(fmt, E, d, F, P, seed=77)
+    dt = torch.float32 if fmt == "pauli_f32" else torch.bfloat16
+    dev = "cuda"
+    xt = torch.from_numpy(x).to(dev, dt)
+    pu, pd = (ops.prepare_weights(torch.from_numpy(w).to(dev), fmt) for w in (wu, wd))
+    bup, bdn = ops.prepare_bias(torch.from_numpy(bu).to(dev)), ops.prepare_bias(torch.from_numpy(bd).to(dev))
+    off_t, cnt_t = torch.from_numpy(offsets).to(dev), torch.from_numpy(counts).to(dev)
+    say(f"grouped experts clamped ranges fmt={fmt} E={E} d={d} F={F} P={P}")
+    y = ops.grouped_experts(xt, off_t, cnt_t, pu, pd, bup, bdn, "gelu", validate=True)
+    long_last = cnt_t.clone()
+    long_last[-1] += 50
+    y_long = ops.grouped_experts(xt, off_t, long_last, pu, pd, bup, bdn, "gelu")
+    assert torch.equal(y_long, y)
+    far = off_t.clone()
+    far[3] = P + 100  # experts 3 and 4 become empty; expert 2's range runs to P
+    y_far = ops.grouped_experts(xt, far, cnt_t, pu, pd, bup, bdn, "gelu")
+    torch.cuda.synchronize()
+    assert torch.equal(y_far[:offsets[2]], y[:offsets[2]])
+    assert bool(torch.isfinite(y_far.float()).all())

@@ -429,7 +429,9 @@ def grouped_experts(x_sorted: torch.Tensor, expert_offsets: torch.Tensor, expert
     contiguous and ascending from row 0 (as a sort by expert leaves them).  Weights
     and biases are prepared (:func:`prepare_weights`, :func:`prepare_bias`); the
     weight format picks the products (bf16 / fp32 Pauli, or the L(w) blocks).
-    ``validate`` checks the ranges on the host (one synchronisation).
+    ``validate`` checks the ranges on the host (one synchronisation).  Without it the
+    ranges are clamped on the device (no synchronisation) into ascending bounds within
+    ``[0, P]``, so malformed ranges give wrong rows, never accesses past x_sorted or y.
     Returns y_sorted in x_sorted's shape and dtype.
     """
     dev = _dev(x_sorted, expert_offsets, expert_counts, b_up, b_down)
@@ -451,6 +453,8 @@ def grouped_experts(x_sorted: torch.Tensor, expert_offsets: torch.Tensor, expert
             raise ValueError("expert ranges must be contiguous, ascending and cover the rows from 0")
     if P == 0:
         return x_sorted.clone()
+    # the products take every range from these bounds: ascending and inside the rows
+    offs = torch.cummax(offs.clamp(0, P), 0).values.to(torch.int32).contiguous()
     fmt = w_up.fmt
     if fmt == "int8_pauli":
         raise ValueError("int8_pauli weights run inside the decode layer (moe_forward), which routes its own "
