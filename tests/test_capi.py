@@ -137,6 +137,35 @@ def test_layer_rejects_bad_routing_sizes():
     assert b"does not match" in L.ygg_last_error()
 
 
+def test_layer_refuses_unaddressable_sizes_before_any_launch():
+    """The bf16 Pauli layer takes any number of tokens whose x fits the gathered rows' 2 GiB
+    range (N = 73728 at the config 3 shape is accepted as far as the workspace check); beyond
+    that, and beyond 2^31 - 1 token-expert rows, it refuses before the routing launches (dummy
+    non-null pointers: nothing is dereferenced)."""
+    from yggdrasil_amd import _native
+
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("library not built")
+    L = _native.lib()
+
+    def fwd(N, d, F, E, k, ws_bytes):  # bf16, Pauli weights, given logits
+        return L.ygg_moe_forward(1, 1, N, d, F, E, k, 1, 1, None, None, 1, None, None, 1, None, None, 3, None, 1,
+                                 1, 1, 1, 1, 1, ws_bytes, None)
+
+    # C3 shape beyond 32768 tokens: the sizes pass, the short workspace is what is refused
+    assert fwd(73728, 128, 512, 32, 4, 0) == -1 and b"workspace" in L.ygg_last_error()
+    assert L.ygg_moe_workspace_bytes(73728, 128, 512, 32, 4, 1, 3) > (1 << 31)
+    # x's Pauli rows (N x 16 d bytes, gathered by token) past 2 GiB: refused with the reason
+    assert fwd(1 << 20, 128, 512, 32, 2, 1 << 62) == -1
+    assert b"gathered x rows" in L.ygg_last_error()
+    # more token-expert rows than an int holds
+    assert fwd(1 << 29, 8, 16, 16, 8, 1 << 62) == -1 and b"2^31 - 1" in L.ygg_last_error()
+    # the block entry refuses the same sizes before its norm launches
+    assert L.ygg_moe_block_ffn(1, 1, 1 << 20, 128, 512, 32, 2, 1, 1, 1, 1e-6, 1, None, None, 1, None, None, 1,
+                               None, None, 3, 2, 1, 1, 1, 1, 1, 1 << 62, None) == -1
+    assert b"gathered x rows" in L.ygg_last_error()
+
+
 def test_backward_workspace_holds_either_weight_gradient():
     """The weight-gradient region is shared by the up (d -> F) and down (F -> d) products, so
     its size does not shrink below the down product's needs when d_model > d_ff."""

@@ -108,6 +108,43 @@ def test_c3_every_token(c3_case, fmt):
     assert err.max() < TOL_BF16, (int(err.argmax()), float(err.max()))
 
 
+@pytest.mark.parametrize("N", [40960, 73728])
+def test_c3_shape_prefill_beyond_32k_tokens(N):
+    """Prefill at the config 3 shape with more tokens than a 32-bit offset over whole operands allows:
+    at N = 73728 the hidden rows h (P = 294912 rows of 8 KiB) span 2.4 GB, so the down product reads,
+    and the up product writes, rows past 2 GiB.  Routing indices and expert counts are bit-exact; the
+    outputs of a sample of tokens -- 512 random ones and every token of the last two experts in row
+    order, whose rows sit at the end of h -- are within the bf16 bound of the float64 oracle per
+    token; and the layer is token-permutation equivariant bit for bit (reversed order, every token)."""
+    d, E, k, F = 128, 32, 4, 512
+    ops = _ops()
+    g = np.random.default_rng(3090 + N)
+    logits = _inputs.normal(g, (N, E), 1.0)
+    logits[:, :4] += 1.5  # a skewed load, the first four experts heaviest
+    x = _bf16(g.standard_normal((N, d, 8), dtype=np.float32))
+    dev, host = _device_weights(3091, E, d, F, torch.bfloat16)
+    P = _layer(ops, dev, "pauli")
+    del dev
+    xt = torch.from_numpy(x).cuda().bfloat16()
+    lt = torch.from_numpy(logits).cuda()
+    say(f"c3-shape prefill N={N} (P={N * k} rows, h {N * k * F * 16 / 2**30:.2f} GiB)")
+    out, rt = ops.moe_forward(xt, k, P["w_up"], P["w_down"], P["b_up"], P["b_down"], "gelu", logits=lt)
+    idx, w = _check_routing(rt, logits, k)
+    got = out.float().cpu().numpy()
+    last = np.flatnonzero((idx >= E - 2).any(axis=1))
+    sample = np.union1d(g.choice(N, size=512, replace=False), last)
+    say(f"c3-shape prefill N={N}: float64 oracle on {sample.size} tokens")
+    ref = dense.moe_layer(x[sample], idx[sample], w[sample], host["w_up"], host["b_up"], host["w_down"],
+                          host["b_down"], "gelu")
+    err = _per_token_err(got[sample], ref)
+    say(f"c3-shape prefill N={N}: worst token error {err.max():.3e}, median {np.median(err):.3e}")
+    assert err.max() < TOL_BF16, (int(sample[err.argmax()]), float(err.max()))
+    say(f"c3-shape prefill N={N}: reversed token order")
+    out_r, _ = ops.moe_forward(torch.flip(xt, [0]).contiguous(), k, P["w_up"], P["w_down"], P["b_up"],
+                               P["b_down"], "gelu", logits=torch.flip(lt, [0]).contiguous())
+    assert torch.equal(torch.flip(out_r, [0]), out)
+
+
 @pytest.mark.parametrize("fmt", ["int8", "int8_pauli"])
 def test_c4_decode_every_token(fmt):
     """BASELINE config 4 (N=64, d=128, F=512, E=32, k=2, int8 weights) against the float64 layer on the

@@ -94,6 +94,25 @@ YGG_API size_t ygg_moe_workspace_bytes(int N, int d, int F, int E, int k, int dt
   return b;
 }
 
+// Sizes the layer's kernels cannot address, refused before the first launch: more
+// than 2^31 - 1 token-expert rows, and the bf16 Pauli products' 32-bit limits (the
+// up product gathers x's Pauli rows, N of them, into P rows of h; the down product
+// reads h in place into P blade rows).
+static int layer_size_check(const char* who, int N, int d, int F, int E, int k, int w_format) {
+  YGG_CHECK_ARG((long long)N * k <= 0x7fffffffLL, "%s: N k = %lld token-expert rows exceed 2^31 - 1", who,
+                (long long)N * k);
+  if (w_format == kWPauli && N > 0) {
+    const int P = N * k;
+    const char* why = ygg::pauli_size_limit(/*Pauli rows*/ 1, N, /*gathered*/ true, P, E, d, F, /*Pauli rows*/ 0, kBF16);
+    if (!why) why = ygg::pauli_size_limit(1, P, false, P, E, F, d, /*blade*/ 1, kBF16);
+    if (why) {
+      set_error("%s: %s (N=%d d=%d F=%d E=%d k=%d)", who, why, N, d, F, E, k);
+      return -1;
+    }
+  }
+  return 0;
+}
+
 static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E, int k, int act,
                             const float* logits, const float* router_w, const float* router_b, const void* w_up,
                             const float* s_up, const float* b_up, const void* w_down, const float* s_down,
@@ -122,6 +141,7 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
                 N, d);
   YGG_CHECK_ARG(w_format != kWPauli || (d % 2 == 0 && F % 2 == 0),
                 "ygg_moe_forward: the Pauli weight format needs even d and F (d=%d F=%d)", d, F);
+  if (layer_size_check("ygg_moe_forward", N, d, F, E, k, w_format)) return -1;
   YGG_CHECK_ARG(workspace_bytes >= ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format),
                 "ygg_moe_forward: workspace of %zu bytes, need %zu", workspace_bytes,
                 ygg_moe_workspace_bytes(N, d, F, E, k, dtype, w_format));
@@ -375,6 +395,7 @@ YGG_API int ygg_moe_block_ffn(const void* x, int dtype, int N, int d, int F, int
   const size_t need = ygg_moe_block_ffn_workspace_bytes(N, d, F, E, k, dtype, w_format);
   YGG_CHECK_ARG(workspace_bytes >= need, "ygg_moe_block_ffn: workspace of %zu bytes, need %zu", workspace_bytes, need);
   YGG_CHECK_ARG(N == 0 || out != x, "ygg_moe_block_ffn: out must not alias x");
+  if (N > 0 && layer_size_check("ygg_moe_block_ffn", N, d, F, E, k, w_format)) return -1;
   // x_norm = ffn_norm(x) at the front of the workspace; the MoE layer gets the
   // rest, and adds x back in its combine
   const size_t xn_bytes = align256((size_t)N * d * 8 * ((dtype == kF32) ? 4 : 2));

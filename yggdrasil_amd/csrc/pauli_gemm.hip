@@ -95,12 +95,13 @@ struct PauliTileInfo {
 // each 16 tokens x b = 0, 1), column block cb (of WC, 32 output multivectors);
 // bv[cb] is the bias of this lane's column in blade order, added here unless
 // BIAS_IN_ACC (the accumulators started from it).  The output is written by
-// buffer stores: y_rsrc spans the output's true size, the row-dependent part of
-// each offset is a scalar, the lane's part a fixed per-lane offset.
+// buffer stores: y_rsrc starts at output row `row_base` and ends at the output's
+// true end, the row-dependent part of each offset is a scalar, the lane's part a
+// fixed per-lane offset.
 template <int ACT, int OUT, int OUT_DT, int WR, int WC, int BWT, bool BIAS_IN_ACC>
 __device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][WC][2][2], const float (&bvs)[WC][8],
                                                     const PauliTileInfo& ti, int wave, int g, int l32, int d_out,
-                                                    __amdgpu_buffer_rsrc_t y_rsrc) {
+                                                    __amdgpu_buffer_rsrc_t y_rsrc, int row_base) {
   typedef unsigned int pu32x2_t __attribute__((ext_vector_type(2)));
   typedef unsigned int pu32x4_t __attribute__((ext_vector_type(4)));
   const int wt = wave % BWT, wj = wave / BWT;
@@ -124,7 +125,7 @@ __device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][W
         for (int h = 0; h < 2; ++h) {
           const int rs = ti.row0 + (wt * WR + rbr) * 16 + 4 * q + h;  // row of lanes with g = 0
           if (rs + 2 * g >= ti.row_end) continue;
-          const uint32_t s_off = (uint32_t)rs * d_out * MV_BYTES;
+          const uint32_t s_off = (uint32_t)(rs - row_base) * d_out * MV_BYTES;
           const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
           float y[8];
           pauli_to_blade(acc[rb][cb][0][0][v0], acc[rb][cb][0][1][v0], acc[rb][cb][0][0][v0 + 1],
@@ -405,7 +406,7 @@ __global__ __launch_bounds__(TL::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
 
   const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, y_bytes, kBufferFlags);
   auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
-    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, false>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc);
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, false>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc, 0);
   };
 
   // ---- the stream of (tile, chunk) steps ------------------------------------
@@ -521,11 +522,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the staged LDS contents ready are the explicit ones above
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Sizes: x_bytes and y_bytes are the operands' whole sizes (64-bit).  Gathered rows
+// (token ids through `gather`) index the whole of x, which the host keeps below
+// 2 GiB; rows taken in place, and the output, are addressed from buffer resources
+// whose 64-bit base is the tile's first row, so only one tile's span needs 32-bit
+// offsets and the number of rows is not limited by them.
 template <int ACT, int OUT, int OUT_DT>
 __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_eu(2))) void pauli_gemm_dma_kernel(
     const uint16_t* __restrict__ X, const int32_t* __restrict__ gather, const uint16_t* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out,
-    void* __restrict__ Y, int n_xcd, uint32_t x_bytes, uint32_t y_bytes) {
+    void* __restrict__ Y, int n_xcd, uint64_t x_bytes, uint64_t y_bytes) {
   using C = PauliDmaTile;
   constexpr int NT = C::NT, T = C::T, BN = C::BN, KC = C::KC, WR = C::WR, WC = C::WC, BWT = C::BWT;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
@@ -588,8 +594,17 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   const int IP = d_in >> 1;  // input pairs (d_in even)
   constexpr uint32_t kOff = 0x80000000u;  // past every range: reads zero
 
-  const __amdgpu_buffer_rsrc_t x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(X), (short)0,
-                                                                          x_bytes, kBufferFlags);
+  // a buffer resource over `bytes` bytes from `base`, offset `off` bytes into it
+  // (64-bit), its range clamped to what lies past `off` and below 2 GiB
+  auto rsrc_from = [](const void* base, uint64_t bytes, uint64_t off) __attribute__((always_inline)) {
+    const uint64_t left = bytes > off ? bytes - off : 0;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(base)) + off, (short)0,
+                                             (uint32_t)(left < 0x7fffffffull ? left : 0x7fffffffull), kBufferFlags);
+  };
+  // gathered rows index the whole of x (below 2 GiB); in place, the resource is
+  // re-based at each tile's first row when its first A chunk is issued
+  __amdgpu_buffer_rsrc_t x_rsrc = rsrc_from(X, gather ? x_bytes : 0, 0);
+  const uint64_t x_row_bytes = (uint64_t)d_in * 16;  // a row: two Pauli half-rows of d_in x 8 bytes
   const __amdgpu_buffer_rsrc_t g_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int32_t*>(gather), (short)0, gather ? (uint32_t)n_rows * 4 : 0u, kBufferFlags);
   const __amdgpu_buffer_rsrc_t b_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -627,10 +642,12 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     if (iak == 0) {
       const PauliTileInfo t = decode(iam);
       const int* gs = reinterpret_cast<const int*>(smem + C::G_OFF + (iam & 1) * T * 4);
+      if (gather == nullptr) x_rsrc = rsrc_from(X, x_bytes, (uint64_t)t.row0 * x_row_bytes);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int r = 8 * (4 * wave + u) + (lane >> 3);  // half-row (token r / 2, b = r % 2)
-        const int src = gather ? gs[r >> 1] : min(t.row0 + (r >> 1), t.row_end - 1);
+        // the gathered token, or the row relative to the tile's first
+        const int src = gather ? gs[r >> 1] : min(r >> 1, t.row_end - 1 - t.row0);
         a_cur[u] = (uint32_t)(2 * src + (r & 1)) * d_in * 8 + a_pc[u];
       }
       if (gather != nullptr && wave == 3 && iam + 1 < n_mine) {
@@ -777,9 +794,11 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     }
     pauli_acc_from_bias<WR, WC>(acc, bvs);
   };
-  const __amdgpu_buffer_rsrc_t y_rsrc = __builtin_amdgcn_make_buffer_rsrc(Y, (short)0, y_bytes, kBufferFlags);
+  // the output from the tile's first row on (64-bit base)
+  constexpr uint64_t Y_MV_BYTES = (OUT == kOutPauliRows || OUT_DT == kBF16) ? 16 : 32;
   auto epilogue = [&](const PauliTileInfo& ti) __attribute__((always_inline)) {
-    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, true>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc);
+    const __amdgpu_buffer_rsrc_t y_rsrc = rsrc_from(Y, y_bytes, (uint64_t)ti.row0 * d_out * Y_MV_BYTES);
+    pauli_tile_epilogue<ACT, OUT, OUT_DT, WR, WC, BWT, true>(acc, bvs, ti, wave, g, l32, d_out, y_rsrc, ti.row0);
   };
 
   // prologue: the first tile's gather indices; then what steps -4 .. -1 would
@@ -878,6 +897,33 @@ __global__ __launch_bounds__(256) void blade_to_pauli_rows_kernel(const uint16_t
   pauli_rows_bf16_one(x, d, n, out);
 }
 
+// Which kernel runs a product: the direct-to-LDS kernel for Pauli half-row input
+// with at least two A chunks per tile, else the register-staged one.
+bool pauli_uses_dma(int x_layout, int d_in) { return x_layout == kInPauliRows && d_in > 2 * PauliDmaTile::KC; }
+
+// The 32-bit buffer offsets of the products: nullptr if the call fits, else why not.
+// Both kernels address one expert's weights (a column tile may reach 64 columns
+// past d_out) and the biases as whole buffers.  The direct-to-LDS kernel addresses
+// gathered x rows over the whole of x, and rows in place and the output from each
+// tile's first row (64-bit bases: any number of rows); the register-staged kernel
+// addresses x and the output as whole buffers.  (x rows, blade or Pauli half-row
+// pairs, are 16 d_in bytes either way.)
+const char* pauli_size_limit(int x_layout, int x_rows, bool gathered, int P_max, int E, int d_in, int d_out,
+                             int y_layout, int y_dtype) {
+  const uint64_t lim = (uint64_t)1 << 31;
+  const uint64_t y_mv = (y_layout == kOutPauliRows || y_dtype == kBF16) ? 16 : 32;
+  if ((uint64_t)(d_out + 64) * d_in * 16 >= lim) return "one expert's weights reach 2 GiB";
+  if ((uint64_t)E * d_out * 32 >= lim) return "the biases reach 2 GiB";
+  if (pauli_uses_dma(x_layout, d_in)) {
+    if (gathered && (uint64_t)x_rows * d_in * 16 >= lim) return "gathered x rows span 2 GiB or more";
+    if ((uint64_t)PauliDmaTile::T * d_out * y_mv >= lim || (uint64_t)PauliDmaTile::T * d_in * 16 >= lim)
+      return "one tile's rows span 2 GiB";
+  } else if ((uint64_t)x_rows * d_in * 16 >= lim || (uint64_t)P_max * d_out * y_mv >= lim) {
+    return "operands of 2 GiB or more need Pauli half-row input with d_in > 16";
+  }
+  return nullptr;
+}
+
 }  // namespace ygg
 
 using namespace ygg;
@@ -912,11 +958,11 @@ DeviceShape device_shape() {
 }
 
 template <int ACT, int IN, int OUT, int ODT>
-int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int32_t* gather, const uint16_t* Wp,
+int launch_pauli(hipStream_t st, const uint16_t* X, uint64_t x_bytes, const int32_t* gather, const uint16_t* Wp,
                  const float* bias, const int32_t* offsets, int E, int P_max, int d_in, int d_out, void* Y) {
   const DeviceShape ds = device_shape();
   // the output's size (rows past P_max, from offsets beyond it, are not written)
-  const uint32_t y_bytes = (uint32_t)((size_t)P_max * d_out * ((OUT == kOutPauliRows || ODT == kBF16) ? 16 : 32));
+  const uint64_t y_bytes = (uint64_t)P_max * d_out * ((OUT == kOutPauliRows || ODT == kBF16) ? 16 : 32);
   // never more workgroups than tiles can exist
   const long long max_tiles =
       ((long long)(P_max + Tile::T - 1) / Tile::T + E) * ((d_out + Tile::BN - 1) / Tile::BN);
@@ -926,17 +972,17 @@ int launch_pauli(hipStream_t st, const uint16_t* X, uint32_t x_bytes, const int3
     grid = (int)max_tiles;
     xcds = 1;
   }
-  if (IN == kInPauliRows && d_in > 2 * PauliDmaTile::KC)  // at least two A chunks per tile
+  if (pauli_uses_dma(IN, d_in))
     pauli_gemm_dma_kernel<ACT, OUT, ODT>
         <<<grid, PauliDmaTile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes, y_bytes);
-  else
-    pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile>
-        <<<grid, Tile::NT, 0, st>>>(X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, x_bytes, y_bytes);
+  else  // the register-staged kernel: whole operands below 2 GiB (checked by the caller)
+    pauli_gemm_kernel<ACT, IN, OUT, ODT, Tile><<<grid, Tile::NT, 0, st>>>(
+        X, gather, Wp, bias, offsets, E, d_in, d_out, Y, xcds, (uint32_t)x_bytes, (uint32_t)y_bytes);
   return check_launch("pauli_gemm");
 }
 
 template <int ACT>
-int launch_pauli_act(hipStream_t st, int in_layout, int out_layout, int y_dtype, const uint16_t* X, uint32_t x_bytes,
+int launch_pauli_act(hipStream_t st, int in_layout, int out_layout, int y_dtype, const uint16_t* X, uint64_t x_bytes,
                      const int32_t* gather, const uint16_t* Wp, const float* bias, const int32_t* offsets, int E,
                      int P_max, int d_in, int d_out, void* Y) {
 #define YGG_PL(IN, OUT, ODT) \
@@ -991,18 +1037,15 @@ YGG_API int ygg_pauli_grouped_linear(const void* x, int x_layout, int x_rows, co
                 E, P_max, d_in, d_out, kPauliMaxExperts);
   YGG_CHECK_ARG(x_rows >= 0 && (gather != nullptr || x_rows >= P_max),
                 "ygg_pauli_grouped_linear: x has %d rows, the product reads %d without a gather", x_rows, P_max);
-  // staging uses 32-bit buffer offsets: every operand stays below 2 GiB (x's
-  // rows, blade or Pauli half-row pairs, are 16 d_in bytes either way)
-  const size_t lim = (size_t)1 << 31;
-  // (a column tile may reach 64 columns past d_out: their offsets must not wrap either)
-  YGG_CHECK_ARG((size_t)(d_out + 64) * d_in * 16 < lim && (size_t)E * d_out * 32 < lim &&
-                    (size_t)x_rows * d_in * 16 < lim && (size_t)P_max * d_out * 32 < lim,
-                "ygg_pauli_grouped_linear: operands of 2 GiB or more are not supported (x rows=%d d_in=%d d_out=%d "
-                "output rows=%d)",
-                x_rows, d_in, d_out, P_max);
+  if (const char* why = ygg::pauli_size_limit(x_layout, x_rows, gather != nullptr, P_max, E, d_in, d_out, y_layout,
+                                              y_dtype)) {
+    ygg::set_error("ygg_pauli_grouped_linear: %s (x rows=%d d_in=%d d_out=%d output rows=%d)", why, x_rows, d_in,
+                   d_out, P_max);
+    return -1;
+  }
   if (P_max == 0) return 0;
   YGG_CHECK_ARG(x && w && offsets && y, "ygg_pauli_grouped_linear: null pointer");
-  const uint32_t x_bytes = (uint32_t)((size_t)x_rows * d_in * 16);
+  const uint64_t x_bytes = (uint64_t)x_rows * d_in * 16;
   const uint16_t* X = static_cast<const uint16_t*>(x);
   const uint16_t* Wp = static_cast<const uint16_t*>(w);
   switch (act) {

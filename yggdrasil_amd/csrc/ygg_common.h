@@ -108,6 +108,13 @@ enum WFormat : int { kWF32 = 0, kWBF16 = 1, kWI8 = 2, kWPauli = 3, kWPauliF32 = 
 
 // bf16 Pauli weight layout (pauli_gemm.hip)
 int pauli_prepare_weights(const float* W, int E, int d_out, int d_in, void* out, hipStream_t stream);
+// bf16 Pauli products: the kernel a call takes, and whether its sizes fit that
+// kernel's 32-bit buffer offsets (nullptr) or why not; x_layout / y_layout as
+// ygg_pauli_grouped_linear's (0: blade rows gathered / Pauli rows out; 1: Pauli rows
+// in / blade rows out)
+bool pauli_uses_dma(int x_layout, int d_in);
+const char* pauli_size_limit(int x_layout, int x_rows, bool gathered, int P_max, int E, int d_in, int d_out,
+                             int y_layout, int y_dtype);
 
 // Blade rows -> Pauli rows carried by the workgroups of another launch (the routing
 // kernels append them to their own): n multivectors of x, rows of d, bf16 -> bf16
