@@ -20,7 +20,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_LIB = os.path.join(HERE, "_build", "libcl3_oracle.so")
+# YGG_ORACLE_LIB names another build of the C restatement (e.g. one with sanitizers)
+ORACLE_LIB = os.environ.get("YGG_ORACLE_LIB") or os.path.join(HERE, "_build", "libcl3_oracle.so")
 REF_LIB = os.path.join(HERE, "_ref", "libmjolnir_cpu.so")
 
 _F = ctypes.POINTER(ctypes.c_float)
@@ -80,6 +81,18 @@ def c_geom_matmul(a, b, threads: int = 1):
         lib.oracle_geom_matmul_omp(_p(a), _p(b), _p(out), M, K, N, threads)
     else:
         lib.oracle_geom_matmul(_p(a), _p(b), _p(out), M, K, N)
+    return out
+
+
+def c_geom_prod(a, b):
+    """C restatement of the element-wise geometric product over rows of 8."""
+    lib = oracle_lib()
+    if lib is None:
+        raise FileNotFoundError(ORACLE_LIB)
+    a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1, 8)
+    b = np.ascontiguousarray(b, dtype=np.float32).reshape(-1, 8)
+    out = np.empty_like(a)
+    lib.oracle_geom_prod(_p(a), _p(b), _p(out), a.shape[0])
     return out
 
 

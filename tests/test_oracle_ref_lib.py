@@ -47,12 +47,18 @@ def test_reference_known_answer_programs_pass(prog):
 
 
 @needs_c
-def test_c_restatement_tables_and_bits():
+@pytest.mark.parametrize("shape", [(12, 30, 17), (1, 1, 1), (5, 0, 3), (7, 3, 1), (1, 64, 9)])
+def test_c_restatement_tables_and_bits(shape):
+    """The C restatement (tables, serial and OpenMP matmul, element-wise product) bit for bit
+    against the NumPy restatement, on ragged shapes and an empty contraction (zeros)."""
+    M, K, N = shape
     idx, sign = native.c_tables()
     assert np.array_equal(idx, cl3.PRODUCT_IDX) and np.array_equal(sign, cl3.PRODUCT_SIGN)
-    r = np.random.default_rng(4)
-    a = r.standard_normal((12, 30, 8), dtype=np.float32)
-    b = r.standard_normal((30, 17, 8), dtype=np.float32)
-    ref = moe.geom_matmul(a, b)
+    r = np.random.default_rng(4 + M + K + N)
+    a = r.standard_normal((M, K, 8), dtype=np.float32)
+    b = r.standard_normal((K, N, 8), dtype=np.float32)
+    ref = moe.geom_matmul(a, b) if K > 0 else np.zeros((M, N, 8), np.float32)
     assert np.array_equal(native.c_geom_matmul(a, b), ref)
     assert np.array_equal(native.c_geom_matmul(a, b, threads=4), ref)
+    x, y = r.standard_normal((2, 3 * M + 1, 8), dtype=np.float32)
+    assert np.array_equal(native.c_geom_prod(x, y), cl3.geom_prod(x, y))

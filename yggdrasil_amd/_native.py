@@ -13,7 +13,9 @@ import os
 
 import torch  # noqa: F401  (must precede loading the library)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libygg_moe.so")
+# YGG_MOE_LIB names another build of the same library (e.g. one with host-side sanitizers)
+LIB_PATH = os.environ.get("YGG_MOE_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib",
+                                                         "libygg_moe.so")
 
 _c_int, _c_size, _vp, _c_double = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_double
 
