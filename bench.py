@@ -380,6 +380,14 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
         ms_disp = time_fn(torch, lambda: ops.dispatch(x, r, mask_order=True, out=xs_t), steps, warmup)
     out_t = torch.empty_like(x)
     ms_comb = time_fn(torch, lambda: ops.combine(ys, r, out=out_t), steps, warmup)
+    ms_route_conv = None
+    if c["fmt"] in ("pauli", "pauli_f32") and logits is not None:
+        # what the layer runs first: the routing with the conversion of x to Pauli rows in the
+        # same launches (ygg_route_pauli_rows), buffers reused
+        r_rc, xp_rc = ops.route_pauli_rows(logits, k, x)
+        ws_rc = torch.empty((max(L.ygg_route_workspace_bytes(N, E, k), 1),), device="cuda", dtype=torch.uint8)
+        ms_route_conv = time_fn(torch, lambda: ops.route_pauli_rows(logits, k, x, out=r_rc, x_pauli=xp_rc,
+                                                                    workspace=ws_rc), steps, warmup)
 
     flops_proj = 128.0 * d * F * P  # per projection in the reference's arithmetic (64 multiply-adds per pair)
     # what the MFMA units execute: the Pauli (complex 2x2) form issues 32 of the 64 multiply-adds
@@ -394,15 +402,20 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     b_route = 4 * N * E + 12 * P + 4 * P + 8 * E
     b_pass = 2 * N * R if c["fmt"] in ("pauli", "pauli_f32") else P * R + P * R + 4 * P
     b_comb = P * R + 12 * P + N * R
+    # the layer's route / dispatch / combine time: for the Pauli formats the routing launches that
+    # also convert x (as the layer runs them), else the routing and the dispatch copy
+    ms_rdc = (ms_route_conv if ms_route_conv is not None else ms_route + ms_disp) + ms_comb
     res.update(
-        kernels_ms=dict(route=ms_route, dispatch=ms_disp, expert_up=ms_up, expert_down=ms_down, combine=ms_comb),
+        kernels_ms=dict(route=ms_route, dispatch=ms_disp, expert_up=ms_up, expert_down=ms_down, combine=ms_comb,
+                        **({} if ms_route_conv is None else {"route_with_conversion": ms_route_conv})),
         expert_tflops=2 * issued_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
         expert_mfma_frac=2 * issued_proj / ((ms_up + ms_down) * 1e-3) / peak,
         expert_dense_equiv_tflops=2 * flops_proj / ((ms_up + ms_down) * 1e-3) / 1e12,
         kernel_bytes=dict(route=b_route, dispatch=b_pass, combine=b_comb),
         kernel_hbm_frac=dict(route=b_route / (ms_route * 1e-3) / PEAK_HBM, dispatch=b_pass / (ms_disp * 1e-3) / PEAK_HBM,
                              combine=b_comb / (ms_comb * 1e-3) / PEAK_HBM),
-        route_dispatch_combine_hbm_frac=(b_route + b_pass + b_comb) / ((ms_route + ms_disp + ms_comb) * 1e-3) / PEAK_HBM)
+        route_dispatch_combine_ms=ms_rdc,
+        route_dispatch_combine_hbm_frac=(b_route + b_pass + b_comb) / (ms_rdc * 1e-3) / PEAK_HBM)
     res["_flops_per_launch"] = issued_proj
     res["_dense_flops_per_launch"] = flops_proj
     res["_ms_per_launch"] = (ms_up + ms_down) / 2

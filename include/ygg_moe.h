@@ -85,7 +85,7 @@ int ygg_router_head_logits(const void* x, int x_dtype, int N, int d, const float
 int ygg_router_energy_logits(const void* x, int x_dtype, int N, int d, const float* router_w,
                              const float* router_b, int E, float* logits, float* energy, ygg_stream_t stream);
 
-/* Workspace bytes needed by ygg_route. */
+/* Workspace bytes needed by ygg_route (and ygg_route_energy, ygg_route_pauli_rows). */
 size_t ygg_route_workspace_bytes(int N, int E, int k);
 
 /* Softmax, top-k and the expert counting sort.
@@ -101,6 +101,18 @@ size_t ygg_route_workspace_bytes(int N, int E, int k);
 int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
               int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
               ygg_stream_t stream);
+
+/* ygg_route and, in the same launches, the conversion of x (N, d, 8) to Pauli rows
+ * (x_dtype 1: bf16 blade rows -> bf16 Pauli half-rows as ygg_pauli_rows_from_blade
+ * writes them, d even; 0: fp32 -> fp32 Pauli rows as ygg_pauli_rows_from_blade_f32):
+ * the first launches of ygg_moe_forward for weight formats 3 and 4, with their
+ * outputs.  Replaces clifford_router.py:18-21,93-104 and hlm_block.py:165-177 as
+ * ygg_route does; the conversion has no counterpart in the reference (its
+ * CliffordLinear reads blade rows, clifford_linear.py:101-123). */
+int ygg_route_pauli_rows(const float* logits, int N, int E, int k, const void* x, int x_dtype, int d,
+                         int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                         int32_t* slot_pos, void* x_pauli, void* workspace, size_t workspace_bytes,
+                         ygg_stream_t stream);
 
 /* CliffordRouter.forward end to end (holograph/layers/clifford_router.py:54-104)
  * plus the slot grouping of hlm_block.py:165-177: the grade-energy logits of

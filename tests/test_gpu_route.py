@@ -237,3 +237,27 @@ def test_router_head_logits_bit_exact(N, d, E, dtype):
     say(f"router head logits N={N} d={d} E={E} {dtype}")
     got = ops.router_head_logits(xt, torch.from_numpy(W).cuda()).cpu().numpy()
     assert np.array_equal(got, moe.clifford_linear(x, W, None)[..., 0])
+
+
+@pytest.mark.parametrize("N,d,E,k,dtype", [(8192, 128, 32, 4, torch.bfloat16), (4096, 256, 64, 2, torch.bfloat16),
+                                           (1500, 40, 16, 2, torch.float32), (700, 64, 8, 2, torch.bfloat16),
+                                           (1030, 6, 5, 3, torch.float32)])
+def test_route_pauli_rows_equals_route_and_conversion(N, d, E, k, dtype):
+    """The layer's first launches -- the routing with the conversion of x to Pauli rows split over
+    both of its launches (one launch up to 1024 tokens) -- give ygg_route's routing and
+    ygg_pauli_rows_from_blade(_f32)'s rows bit for bit, and the routing matches the oracle."""
+    ops = _ops()
+    g = np.random.default_rng(N + d + E)
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    x = torch.from_numpy(g.standard_normal((N, d, 8), dtype=np.float32)).cuda().to(dtype)
+    lt = torch.from_numpy(logits).cuda()
+    say(f"route_pauli_rows N={N} d={d} E={E} k={k} {dtype}")
+    r, xp = ops.route_pauli_rows(lt, k, x)
+    r0 = ops.route(lt, k)
+    want = ops.pauli_rows_from_blade(x) if dtype == torch.bfloat16 else ops.pauli_rows_from_blade_f32(x)
+    torch.cuda.synchronize()
+    for key in ("topk_idx", "topk_w", "counts", "offsets", "perm", "slot_pos"):
+        assert torch.equal(getattr(r, key), getattr(r0, key)), key
+    assert torch.equal(xp.reshape(-1), want.reshape(-1))
+    idx_o, _ = moe.route_topk(moe.softmax(logits), k)
+    assert np.array_equal(r.topk_idx.cpu().numpy(), idx_o)

@@ -30,6 +30,8 @@ SIGNATURES = {
     "ygg_router_energy_logits": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "ygg_route_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int]),
     "ygg_route": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "ygg_route_pauli_rows": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _vp, _vp, _c_size, _vp]),
     "ygg_route_energy": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _vp, _vp, _c_size, _vp]),
     "ygg_dispatch": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _vp]),

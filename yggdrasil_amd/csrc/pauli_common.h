@@ -152,18 +152,58 @@ __device__ inline void pauli_rows_f32_one(const float* __restrict__ x, size_t n,
 }
 
 // Workgroup b's share of a RowConvert riding on another launch: THREADS x U
-// multivectors, U per thread at a stride of THREADS (coalesced).
+// multivectors, U per thread at a stride of THREADS (coalesced).  Every load of the
+// thread is issued before the first conversion (an index past the end repeats the
+// last multivector and is not stored), so a thread waits for memory once.
 template <int THREADS, int U>
 __device__ inline void convert_rows_block(const RowConvert& cv, int b) {
   const long long base = (long long)b * THREADS * U + threadIdx.x;
+  if (base >= cv.n) return;
+  size_t n[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const long long n = base + (long long)u * THREADS;
-    if (n >= cv.n) break;
-    if (cv.kind == kConvBf16Pauli)
-      pauli_rows_bf16_one(static_cast<const uint16_t*>(cv.x), cv.d, (size_t)n, static_cast<uint16_t*>(cv.out));
-    else
-      pauli_rows_f32_one(static_cast<const float*>(cv.x), (size_t)n, static_cast<float*>(cv.out));
+    const long long v = base + (long long)u * THREADS;
+    n[u] = (size_t)(v < cv.n ? v : cv.n - 1);
+  }
+  if (cv.kind == kConvBf16Pauli) {
+    const uint16_t* x = static_cast<const uint16_t*>(cv.x);
+    uint16_t* out = static_cast<uint16_t*>(cv.out);
+    uint4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = *reinterpret_cast<const uint4*>(x + n[u] * 8);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + (long long)u * THREADS >= cv.n) break;
+      const size_t m = n[u] / cv.d;
+      const int i = (int)(n[u] - m * cv.d);
+      const float v[8] = {bf_lo(q[u].x), bf_hi(q[u].x), bf_lo(q[u].y), bf_hi(q[u].y),
+                          bf_lo(q[u].z), bf_hi(q[u].z), bf_lo(q[u].w), bf_hi(q[u].w)};
+      float c0[4], c1[4];
+      blade_to_pauli(v, c0, c1);
+      *reinterpret_cast<uint2*>(out + ((2 * m) * cv.d + i) * 4) =
+          make_uint2(pack2_bf16(c0[0], c0[1]), pack2_bf16(c0[2], c0[3]));
+      *reinterpret_cast<uint2*>(out + ((2 * m + 1) * cv.d + i) * 4) =
+          make_uint2(pack2_bf16(c1[0], c1[1]), pack2_bf16(c1[2], c1[3]));
+    }
+  } else {
+    const float* x = static_cast<const float*>(cv.x);
+    float* out = static_cast<float*>(cv.out);
+    float4 p0[U], p1[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      p0[u] = reinterpret_cast<const float4*>(x + n[u] * 8)[0];
+      p1[u] = reinterpret_cast<const float4*>(x + n[u] * 8)[1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + (long long)u * THREADS >= cv.n) break;
+      const float v[8] = {p0[u].x, p0[u].y, p0[u].z, p0[u].w, p1[u].x, p1[u].y, p1[u].z, p1[u].w};
+      float c0[4], c1[4];
+      blade_to_pauli(v, c0, c1);
+      float4* q = reinterpret_cast<float4*>(out + n[u] * 8);
+      q[0] = make_float4(c0[0], c0[2], c0[1], c0[3]);
+      q[1] = make_float4(c1[0], c1[2], c1[1], c1[3]);
+    }
   }
 }
 template <int THREADS, int U>

@@ -40,6 +40,7 @@ namespace ygg {
 constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
 constexpr int kSelConvPerThread = 4;                  // multivectors per thread of a conversion workgroup
+constexpr int kConvFirstShare = 6;                    // eighths of the conversion's rows in the first launch
 
 template <int Q>  // Q = ceil(E / 8) logits per lane
 __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restrict__ logits, int N, int E, int k,
@@ -102,10 +103,15 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
                                                                 int32_t* __restrict__ slot_pos,
                                                                 int32_t* __restrict__ counts,
                                                                 int32_t* __restrict__ offsets,
-                                                                int32_t* __restrict__ row_slot) {
+                                                                int32_t* __restrict__ row_slot, int n_place,
+                                                                RowConvert cv) {
   __shared__ int32_t s_tot[kMaxExperts];
   __shared__ int32_t s_off[kMaxExperts];
   __shared__ int32_t s_base[kMaxExperts][kPlaceMaxSel];
+  if ((int)blockIdx.x >= n_place) {  // a conversion workgroup (the second part of the rows)
+    convert_rows_block<kPlaceSlots, kSelConvPerThread>(cv, (int)blockIdx.x - n_place);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const long long slots = (long long)N * k;
   const long long f0 = (long long)blockIdx.x * kPlaceSlots;
@@ -371,8 +377,29 @@ YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_id
                             workspace_bytes, RowConvert{}, stream);
 }
 
-// The conversion's workgroups follow the routing's own in its first launch: they
+YGG_API int ygg_route_pauli_rows(const float* logits, int N, int E, int k, const void* x, int x_dtype, int d,
+                                 int32_t* topk_idx, float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                                 int32_t* slot_pos, void* x_pauli, void* workspace, size_t workspace_bytes,
+                                 hipStream_t stream) {
+  YGG_CHECK_ARG(x_dtype == kF32 || x_dtype == kBF16, "ygg_route_pauli_rows: x dtype %d unsupported", x_dtype);
+  YGG_CHECK_ARG(d >= 1 && (x_dtype == kF32 || d % 2 == 0), "ygg_route_pauli_rows: d=%d (even for bf16 rows)", d);
+  YGG_CHECK_ARG(N == 0 || (x && x_pauli), "ygg_route_pauli_rows: null x or x_pauli");
+  ygg::RowConvert cv;
+  if (N > 0) {
+    cv.x = x;
+    cv.out = x_pauli;
+    cv.n = (long long)N * d;
+    cv.d = d;
+    cv.kind = x_dtype == kBF16 ? ygg::kConvBf16Pauli : ygg::kConvF32Pauli;
+  }
+  return ygg::route_convert(logits, N, E, k, topk_idx, topk_w, counts, offsets, perm, slot_pos, workspace,
+                            workspace_bytes, cv, stream);
+}
+
+// The conversion's workgroups follow the routing's own in both of its launches: they
 // do not depend on it, and the short routing kernels leave most of the chip idle.
+// The rows are split between the launches in proportion to what each launch's
+// routing part is worth in conversion time, so the two end together.
 int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
                        int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
                        const RowConvert& cv, hipStream_t stream) {
@@ -389,14 +416,18 @@ int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_i
                                      offsets, perm, slot_pos, cv, stream);
   const int nb = (N + kSelTokens - 1) / kSelTokens;
   int32_t* block_hist = static_cast<int32_t*>(workspace);
-  const int conv_blocks = convert_rows_blocks<kSelBlock, kSelConvPerThread>(cv);
+  // the first launch converts rows [0, r_split), the second the rest
+  const long long conv_rows = cv.kind == kConvNone || cv.d <= 0 ? 0 : cv.n / cv.d;
+  const long long r_split = conv_rows * kConvFirstShare / 8;
+  const RowConvert cv1 = row_convert_part(cv, 0, r_split), cv2 = row_convert_part(cv, r_split, conv_rows);
+  const int conv_blocks = convert_rows_blocks<kSelBlock, kSelConvPerThread>(cv1);
   if (nb + conv_blocks > 0) {
     // slot ranks go to slot_pos; route_scan_place turns them into rows
     switch ((E + 7) / 8) {
 #define YGG_SEL(Q)                                                                                          \
   case Q:                                                                                                   \
     route_select<Q><<<nb + conv_blocks, kSelBlock, 0, stream>>>(logits, N, E, k, topk_idx, topk_w, slot_pos, \
-                                                                block_hist, nb, cv);                        \
+                                                                block_hist, nb, cv1);                       \
     break;
       YGG_SEL(1) YGG_SEL(2) YGG_SEL(3) YGG_SEL(4) YGG_SEL(5) YGG_SEL(6) YGG_SEL(7) YGG_SEL(8)
 #undef YGG_SEL
@@ -405,8 +436,9 @@ int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_i
   }
   const size_t slots = (size_t)N * k;
   const unsigned place_blocks = slots ? (unsigned)((slots + kPlaceSlots - 1) / kPlaceSlots) : 1u;  // N = 0: counts 0
-  route_scan_place<<<place_blocks, kPlaceSlots, 0, stream>>>(topk_idx, block_hist, N, nb, E, k, perm, slot_pos, counts,
-                                                             offsets, cv.row_slot);
+  const unsigned conv2_blocks = (unsigned)convert_rows_blocks<kPlaceSlots, kSelConvPerThread>(cv2);
+  route_scan_place<<<place_blocks + conv2_blocks, kPlaceSlots, 0, stream>>>(
+      topk_idx, block_hist, N, nb, E, k, perm, slot_pos, counts, offsets, cv.row_slot, (int)place_blocks, cv2);
   return check_launch("route_scan_place");
 }
 

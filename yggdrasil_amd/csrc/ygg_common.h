@@ -131,7 +131,20 @@ struct RowConvert {
   // row_slot[slot_pos[f]] = f (the K-split products then write slot rows)
   int32_t* row_slot = nullptr;
 };
-// ygg_route that also runs `cv` in the same launch as its first kernel
+// The rows [r0, r1) of a conversion (the rows of d multivectors of x), as a
+// conversion of its own: x and out advanced to row r0 (x: 8 values per
+// multivector of bf16 or fp32; out: bf16 Pauli half-row pairs or fp32 Pauli rows,
+// 8 values per multivector either way), the same results as the whole one.
+inline RowConvert row_convert_part(const RowConvert& cv, long long r0, long long r1) {
+  RowConvert p = cv;
+  if (cv.kind == kConvNone || cv.d <= 0) return p;
+  const size_t es = cv.kind == kConvBf16Pauli ? 2 : 4;
+  p.x = static_cast<const char*>(cv.x) + (size_t)r0 * cv.d * 8 * es;
+  p.out = static_cast<char*>(cv.out) + (size_t)r0 * cv.d * 8 * es;
+  p.n = (r1 - r0) * cv.d;
+  return p;
+}
+// ygg_route that also runs `cv` in the same launches
 int route_convert(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
                   int32_t* offsets, int32_t* perm, int32_t* slot_pos, void* workspace, size_t workspace_bytes,
                   const RowConvert& cv, hipStream_t stream);

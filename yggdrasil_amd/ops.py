@@ -190,6 +190,43 @@ def route(logits: torch.Tensor, k: int, out: Routing | None = None, workspace: t
     return r
 
 
+def route_pauli_rows(logits: torch.Tensor, k: int, x: torch.Tensor, out: Routing | None = None,
+                     x_pauli: torch.Tensor | None = None, workspace: torch.Tensor | None = None):
+    """:func:`route` and, in the same launches, x (N, d, 8) -> its Pauli rows (bf16: the half-rows of
+    :func:`pauli_rows_from_blade`; fp32: those of :func:`pauli_rows_from_blade_f32`) -- the first launches
+    of the layer for the Pauli weight formats.  Returns ``(Routing, x_pauli)``; ``out``, ``x_pauli`` and
+    ``workspace`` are reused when given."""
+    dev = _dev(logits, x)
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise ValueError("logits must be (N, E) float32")
+    Nt, E = logits.shape
+    if x.dim() != 3 or x.shape[0] != Nt or x.shape[2] != 8:
+        raise ValueError(f"x must be ({Nt}, d, 8), got {tuple(x.shape)}")
+    d = x.shape[1]
+    shape = (Nt, 2, d, 4) if x.dtype == torch.bfloat16 else (Nt, d, 2, 2, 2)
+    if x_pauli is None:
+        x_pauli = torch.empty(shape, device=dev, dtype=x.dtype)
+    elif tuple(x_pauli.shape) != shape or x_pauli.dtype != x.dtype or not x_pauli.is_contiguous():
+        raise ValueError(f"x_pauli must be a contiguous {x.dtype} {shape} tensor")
+    L = lib()
+    ws_bytes = L.ygg_route_workspace_bytes(Nt, E, k)
+    r = out if out is not None else Routing(
+        topk_idx=torch.empty((Nt, k), device=dev, dtype=torch.int32),
+        topk_w=torch.empty((Nt, k), device=dev, dtype=torch.float32),
+        counts=torch.empty((E,), device=dev, dtype=torch.int32),
+        offsets=torch.empty((E + 1,), device=dev, dtype=torch.int32),
+        perm=torch.empty((Nt * k,), device=dev, dtype=torch.int32),
+        slot_pos=torch.empty((Nt, k), device=dev, dtype=torch.int32))
+    if tuple(r.topk_idx.shape) != (Nt, k) or r.counts.numel() != E:
+        raise ValueError("out routing buffers do not match (N, E, k)")
+    ws = workspace if workspace is not None and workspace.numel() >= ws_bytes else \
+        torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    check(L.ygg_route_pauli_rows(ptr(logits), Nt, E, k, ptr(x), _dtype_code(x), d, ptr(r.topk_idx), ptr(r.topk_w),
+                                 ptr(r.counts), ptr(r.offsets), ptr(r.perm), ptr(r.slot_pos), ptr(x_pauli), ptr(ws),
+                                 ws_bytes, stream_handle(dev)), "route_pauli_rows")
+    return r, x_pauli
+
+
 def route_energy(x: torch.Tensor, router_weight: torch.Tensor, router_bias: torch.Tensor, k: int) -> Routing:
     """CliffordRouter.forward (``clifford_router.py:54-104``) and the counting sort in one call.
 
