@@ -37,6 +37,28 @@
 
 namespace ygg {
 
+// Rank of each lane's slot among the wave's slots of the same expert (lower lanes
+// first, i.e. token order), and the wave's count of every expert e in cnt[e stride]
+// (E <= 64).  One ballot per expert the wave holds, not per expert of the layer.
+__device__ inline int rank_in_wave(int my_e, int E, int lane, int32_t* __restrict__ cnt, int stride = 1) {
+  if (lane < E) cnt[lane * stride] = 0;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int rank = 0;
+  uint64_t todo = __ballot(my_e >= 0);
+  while (todo) {
+    const int e = __builtin_amdgcn_readlane(my_e, (int)__builtin_ctzll(todo));
+    const uint64_t bal = __ballot(my_e == e);
+    if (my_e == e) rank = __popcll(bal & lt_mask);
+    if (lane == 0) cnt[e * stride] = __popcll(bal);
+    todo &= ~bal;
+  }
+  return rank;
+}
+
+// Block histograms, expert-major: row e holds expert e's count in every selection
+// block, rows padded to a multiple of 4 blocks so they are read in 16-byte pieces.
+__host__ __device__ inline int hist_stride(int nb) { return (nb + 3) & ~3; }
+
 constexpr int kSelBlock = 256;                        // threads per K1 block
 constexpr int kSelTokens = kSelBlock / kSelLanes;     // tokens per K1 block
 constexpr int kSelConvPerThread = 4;                  // multivectors per thread of a conversion workgroup
@@ -68,13 +90,7 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
   }
 
   // ---- rank of every slot among the block's slots of its expert (token order)
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int rank = 0;
-  for (int e = 0; e < E; ++e) {
-    const uint64_t bal = __ballot(my_e == e);
-    if (my_e == e) rank = __popcll(bal & lt_mask);
-    if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
-  }
+  const int rank = rank_in_wave(my_e, E, lane, wave_cnt[wave]);
   __syncthreads();
   if (my_e >= 0) {
     int base = 0;
@@ -85,7 +101,7 @@ __global__ __launch_bounds__(kSelBlock) void route_select(const float* __restric
     int c = 0;
 #pragma unroll
     for (int w = 0; w < kSelBlock / 64; ++w) c += wave_cnt[w][tid];
-    block_hist[(size_t)tid * n_sel + blockIdx.x] = c;  // expert-major: [E][blocks]
+    block_hist[(size_t)tid * hist_stride(n_sel) + blockIdx.x] = c;  // expert-major: [E][blocks]
   }
 }
 
@@ -125,20 +141,35 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
   const int sb0 = f0 < slots ? (int)(f0 / k) / kSelTokens : 0;
   const int sb1 = f0 < slots ? (int)((f1 - 1) / k) / kSelTokens + 1 : 0;
   // Thread (e, part) sums part `part` of expert e's block counts: `parts` threads per
-  // expert (a power of two, so a group is aligned within a wave), every expert at once.
+  // expert (a power of two, so a group is aligned within a wave), every expert at
+  // once; each thread reads its share in 16-byte pieces, every piece in flight before
+  // the first is added (the rows are padded with whole pieces).
   int parts = 1;
   while (parts < 64 && parts * 2 * E <= kPlaceSlots) parts *= 2;
   const int e_me = tid / parts, part = tid % parts;
+  const int hs = hist_stride(nb);
   int pre = 0, all = 0;  // sums of the blocks before sb0, and of every block
   if (e_me < E) {
-    const int32_t* h = block_hist + (size_t)e_me * nb;
-    const int per = (nb + parts - 1) / parts;
-    const int b0 = part * per, b1 = min(nb, b0 + per);
-#pragma unroll 8
-    for (int b = b0; b < b1; ++b) {
-      const int v = h[b];
-      all += v;
-      pre += b < sb0 ? v : 0;
+    const int4* h4 = reinterpret_cast<const int4*>(block_hist + (size_t)e_me * hs);
+    const int n4 = hs >> 2;
+    const int per = (n4 + parts - 1) / parts;
+    const int q0 = part * per, q1 = min(n4, q0 + per);
+    constexpr int kU = 8;
+    for (int qb = q0; qb < q1; qb += kU) {
+      int4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) v[u] = qb + u < q1 ? h4[qb + u] : make_int4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int b0 = 4 * (qb + u);  // padding blocks hold whatever: only blocks below nb count
+        const int c[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int cv_ = b0 + i < nb ? c[i] : 0;
+          all += cv_;
+          pre += b0 + i < sb0 ? cv_ : 0;
+        }
+      }
     }
   }
   for (int o = parts / 2; o > 0; o >>= 1) {
@@ -146,7 +177,7 @@ __global__ __launch_bounds__(kPlaceSlots) void route_scan_place(const int32_t* _
     all += __shfl_xor(all, o);
   }
   if (e_me < E && part == 0) {
-    const int32_t* h = block_hist + (size_t)e_me * nb;
+    const int32_t* h = block_hist + (size_t)e_me * hs;
     s_tot[e_me] = all;
     int run = pre;
 #pragma unroll
@@ -219,7 +250,6 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int j = tid & (kSelLanes - 1);
   const int ngroups = (N + 7) / 8;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   // a real loop (not unrolled): this kernel runs once per layer call, cold, and
   // its instruction fetch, not its arithmetic, sets its latency
 #pragma unroll 1
@@ -234,12 +264,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_small(const float* __rest
     } else {
       select_token<Q>(logits, E, k, t, t < N, j, lane, e, w);
     }
-    int rank = 0;
-    for (int x = 0; x < E; ++x) {
-      const uint64_t bal = __ballot(e == x);
-      if (e == x) rank = __popcll(bal & lt_mask);
-      if (lane == 0) cnt[x][grp] = __popcll(bal);
-    }
+    const int rank = rank_in_wave(e, E, lane, &cnt[0][grp], kSmallGroups);
     if (e >= 0) {  // rank within the group for now; the placement below turns it into the row
       topk_idx[(size_t)t * k + j] = e;
       topk_w[(size_t)t * k + j] = w;
@@ -366,8 +391,8 @@ int launch_route_small(const float* logits, const void* x, int x_dtype, int d, c
 
 YGG_API size_t ygg_route_workspace_bytes(int N, int E, int k) {
   (void)k;
-  const size_t nb = (size_t)(N + kSelTokens - 1) / kSelTokens;
-  return (nb * E * 4 + 255) & ~(size_t)255;
+  const int nb = (N + kSelTokens - 1) / kSelTokens;
+  return ((size_t)hist_stride(nb) * E * 4 + 255) & ~(size_t)255;
 }
 
 YGG_API int ygg_route(const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w, int32_t* counts,
