@@ -239,3 +239,55 @@ def test_layer_formats_against_oracle(fmt):
             e = idx[t, s]
             ref[t] += w[t, s] * moe.clifford_ffn(x[0, t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
     assert normwise_err(out, ref) < TOL_BF16
+
+
+@pytest.mark.parametrize("d_in,d_out,gathered,y_layout", [(64, 96, True, "pauli"), (96, 64, False, "blade"),
+                                                          (256, 1024, True, "pauli"), (1024, 256, False, "blade")])
+def test_pauli_integer_product_exact_with_compact_tiles(d_in, d_out, gathered, y_layout):
+    """Experts whose last row tile holds at most 32 rows run it as a compact tile (half the
+    MFMAs, its rows staged at the token slots of one row block per wave): counts 1, 16, 17,
+    31, 32 and 64 k + those, next to counts of 33, 63, 64 and 65 rows that stay whole, an
+    empty expert, and enough tiles for a half-tile remainder.  Exact integer products, every
+    row, against the float64 dense oracle, in both output layouts."""
+    from oracle import dense
+    ops = _ops()
+    g = np.random.default_rng(d_in * 3 + d_out)
+    counts = np.array([1, 16, 17, 31, 32, 33, 0, 63, 64, 65, 96, 97, 128 + 5, 320 + 32, 2, 200], np.int64)
+    E, P = counts.size, int(counts.sum())
+    N = 700
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    W = g.integers(-2, 3, size=(E, d_out, d_in, 8)).astype(np.float32)
+    x = g.integers(-2, 3, size=(N if gathered else P, d_in, 8)).astype(np.float32)
+    b = g.integers(-3, 4, size=(E, d_out, 8)).astype(np.float32)
+    gather = g.integers(0, N, P).astype(np.int32) if gathered else None
+    say(f"pauli integer product with compact tiles d_in={d_in} d_out={d_out} gathered={gathered} y={y_layout}")
+    xt = ops.pauli_rows_from_blade(torch.from_numpy(x).cuda().bfloat16())
+    y = ops.pauli_grouped_linear(xt, ops.prepare_weights(torch.from_numpy(W).cuda(), "pauli"),
+                                 torch.from_numpy(offsets).cuda(), ops.prepare_bias(torch.from_numpy(b).cuda()),
+                                 "none", x_layout="pauli", gather=None if gather is None else torch.from_numpy(gather).cuda(),
+                                 y_layout=y_layout, out_dtype=torch.float32 if y_layout == "blade" else torch.bfloat16)
+    y = y.float().cpu().numpy()
+    for e in range(E):
+        rows = slice(offsets[e], offsets[e + 1])
+        if counts[e] == 0:
+            continue
+        xe = x[gather[rows]] if gathered else x[rows]
+        ref = dense.linear(xe, W[e], b[e])
+        if y_layout == "pauli":
+            # the exact integer result's Pauli half-rows, rounded to bf16 as the kernel stores them
+            ref = _bf16(_blade_to_pauli_rows(ref))
+        bad = np.nonzero(np.any((y[rows] != ref).reshape(ref.shape[0], -1), axis=-1))
+        assert bad[0].size == 0, (e, int(counts[e]), bad[0][:8])
+
+
+def _blade_to_pauli_rows(y):
+    """(rows, d, 8) blade order -> (rows, 2, d, 4) Pauli half-rows: half b holds column b of each
+    multivector's 2x2 complex matrix as (row 0 re, row 0 im, row 1 re, row 1 im)."""
+    s, v1, v2, v3, b12, b13, b23, t = (y[..., i] for i in range(8))
+    m00 = (s + v3, t + b12)
+    m01 = (v1 - b13, b23 - v2)
+    m10 = (v1 + b13, b23 + v2)
+    m11 = (s - v3, t - b12)
+    h0 = np.stack([m00[0], m00[1], m10[0], m10[1]], axis=-1)
+    h1 = np.stack([m01[0], m01[1], m11[0], m11[1]], axis=-1)
+    return np.stack([h0, h1], axis=1)

@@ -87,6 +87,10 @@ struct PauliTile {
 struct PauliTileInfo {
   int e, row0, row_end, col0;
   int half;  // -1: the whole tile; 0 / 1: only row block `half` of every wave
+  // a compact tile (the last row tile of an expert, at most 32 rows): computed as a
+  // half tile (block 0 of every wave), its rows staged at the token slots that block
+  // covers, 0-15 and 32-47, so wave row group wt holds rows 16 wt .. 16 wt + 15
+  bool compact = false;
 };
 
 // Epilogue of one tile for one wave: the inverse Pauli map, bias, grade-wise
@@ -123,7 +127,7 @@ __device__ __forceinline__ void pauli_tile_epilogue(const pf32x16_t (&acc)[WR][W
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const int rs = ti.row0 + (wt * WR + rbr) * 16 + 4 * q + h;  // row of lanes with g = 0
+          const int rs = ti.row0 + (ti.compact ? wt * 16 : (wt * WR + rbr) * 16) + 4 * q + h;  // row of lanes with g = 0
           if (rs + 2 * g >= ti.row_end) continue;
           const uint32_t s_off = (uint32_t)(rs - row_base) * d_out * MV_BYTES;
           const int v0 = 4 * q + 2 * h;  // b = 0 at v0, b = 1 at v0 + 1
@@ -536,56 +540,90 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   constexpr int NT = C::NT, T = C::T, BN = C::BN, KC = C::KC, WR = C::WR, WC = C::WC, BWT = C::BWT;
   __shared__ __attribute__((aligned(1024))) unsigned char smem[C::LDS];
   __shared__ int s_off[kPauliMaxExperts + 1];   // expert row offsets
-  __shared__ int s_tbeg[kPauliMaxExperts + 1];  // first row tile of each expert
+  __shared__ int s_tbeg[kPauliMaxExperts + 1];  // first whole row tile of each expert
+  __shared__ int s_cbeg[kPauliMaxExperts + 1];  // first compact row tile of each expert
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int i = tid; i <= E; i += NT) s_off[i] = offsets[i];
   __syncthreads();
+  // Two lists of row tiles: every expert's row tiles but a short last one ("whole"
+  // tiles), and the experts' last row tiles of at most T / 2 rows ("compact" tiles,
+  // computed with half the MFMAs).  s_tbeg / s_cbeg: each expert's first whole /
+  // compact row tile.
   if (tid == 0) {
-    int acc = 0;
+    int acc = 0, accc = 0;
     for (int x = 0; x < E; ++x) {
+      const int cnt = s_off[x + 1] - s_off[x];
+      const int nrt = (cnt + T - 1) / T;
+      const int comp = (cnt > 0 && cnt - (nrt - 1) * T <= T / 2) ? 1 : 0;
       s_tbeg[x] = acc;
-      acc += (s_off[x + 1] - s_off[x] + T - 1) / T;
+      s_cbeg[x] = accc;
+      acc += nrt - comp;
+      accc += comp;
     }
     s_tbeg[E] = acc;
+    s_cbeg[E] = accc;
   }
   __syncthreads();
-  // lane x keeps expert x's first row tile and row range: a tile's expert is the
-  // number of experts whose first tile is at or before it, minus one (experts
-  // without rows share their successor's first tile and are never chosen)
+  // lane x keeps expert x's first whole and compact row tile and its row range: a
+  // tile's expert is the number of experts whose first tile of the list is at or
+  // before it, minus one (experts without tiles in a list share their successor's
+  // first tile there and are never chosen)
   const int v_tbeg = lane < E ? s_tbeg[lane] : 0x7fffffff;
+  const int v_cbeg = lane < E ? s_cbeg[lane] : 0x7fffffff;
   const int v_off = s_off[lane < E ? lane : E], v_end = s_off[lane < E ? lane + 1 : E];
   // (LDS values are per lane to the compiler; these are the same in every lane)
   const int n_rows = __builtin_amdgcn_readfirstlane(s_off[E]);
 
-  // the tile stream: as in the register-staged kernel, one contiguous range of
-  // tiles per XCD, whole rounds first, a short remainder cut into half tiles
+  // The tile stream: as in the register-staged kernel, one contiguous range of whole
+  // tiles per XCD, whole rounds first; then items of half the work, dealt round robin
+  // over the XCD's workgroups: the XCD's range of compact tiles, then (when the whole
+  // tiles leave at most half a round) the remaining whole tiles cut into half tiles.
   const int CT = (d_out + BN - 1) / BN;
   const int n_tiles = __builtin_amdgcn_readfirstlane(s_tbeg[E]) * CT;
+  const int n_ctiles = __builtin_amdgcn_readfirstlane(s_cbeg[E]) * CT;
   const int nka = (d_in + 2 * KC - 1) / (2 * KC);  // A chunks per tile
   const int nk = 2 * nka;                          // steps (W chunks) per tile
   const int per_xcd = gridDim.x / n_xcd;
   const int xcd = blockIdx.x % n_xcd, slot = blockIdx.x / n_xcd;
   const int lo = (int)((long long)n_tiles * xcd / n_xcd), hi = (int)((long long)n_tiles * (xcd + 1) / n_xcd);
+  const int clo = (int)((long long)n_ctiles * xcd / n_xcd), chi = (int)((long long)n_ctiles * (xcd + 1) / n_xcd);
   const int R = hi - lo, rounds = R / per_xcd, rem = R - rounds * per_xcd;
   const bool split = rem > 0 && 2 * rem <= per_xcd;
   const int n_full = split ? rounds : (R > slot ? (R - slot + per_xcd - 1) / per_xcd : 0);
-  const int n_mine = n_full + ((split && slot < 2 * rem) ? 1 : 0);
+  const int n_comp = chi - clo;                                // compact items of this XCD
+  const int n_items = n_comp + (split ? 2 * rem : 0);          // half-work items of this XCD
+  const int n_mine = n_full + (n_items > slot ? (n_items - slot + per_xcd - 1) / per_xcd : 0);
   const int total = n_mine * nk, total_a = n_mine * nka;
   if (total == 0) return;
 
   auto decode = [&](int n) __attribute__((always_inline)) {
-    const bool half = n >= n_full;
-    const int L = half ? lo + rounds * per_xcd + (slot >> 1) : lo + slot + n * per_xcd;
+    PauliTileInfo t;
+    const int item = n >= n_full ? slot + (n - n_full) * per_xcd : -1;
+    if (item >= 0 && item < n_comp) {  // a compact tile: an expert's short last row tile
+      const int C = clo + item;
+      const int rt = C / CT, ct = C - rt * CT;
+      const int e = __popcll(__ballot(v_cbeg <= rt)) - 1;
+      const int beg = __builtin_amdgcn_readlane(v_off, e);
+      t.e = e;
+      t.row_end = __builtin_amdgcn_readlane(v_end, e);
+      t.row0 = beg + ((t.row_end - beg - 1) / T) * T;
+      t.col0 = ct * BN;
+      t.compact = true;
+      t.half = 0;
+      return t;
+    }
+    // a whole tile, or half of one
+    const int L = item >= 0 ? lo + rounds * per_xcd + ((item - n_comp) >> 1) : lo + slot + n * per_xcd;
     const int rt = L / CT, ct = L - rt * CT;
     const int e = __popcll(__ballot(v_tbeg <= rt)) - 1;
-    PauliTileInfo t;
     t.e = e;
     t.row0 = __builtin_amdgcn_readlane(v_off, e) + (rt - __builtin_amdgcn_readlane(v_tbeg, e)) * T;
     t.row_end = __builtin_amdgcn_readlane(v_end, e);
     t.col0 = ct * BN;
-    t.half = half ? (slot & 1) : -1;
+    t.compact = false;
+    t.half = item >= 0 ? ((item - n_comp) & 1) : -1;
     return t;
   };
 
@@ -645,9 +683,14 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
       if (gather == nullptr) x_rsrc = rsrc_from(X, x_bytes, (uint64_t)t.row0 * x_row_bytes);
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int r = 8 * (4 * wave + u) + (lane >> 3);  // half-row (token r / 2, b = r % 2)
+        const int r = 8 * (4 * wave + u) + (lane >> 3);  // half-row (token slot r / 2, b = r % 2)
+        // the tile's row at this token slot: the slot itself, or for a compact tile
+        // rows 0-15 at slots 0-15 and rows 16-31 at slots 32-47 (the other slots
+        // repeat them and are not computed)
+        const int ts = r >> 1;
+        const int tr = t.compact ? (ts & 15) | ((ts >> 5) << 4) : ts;
         // the gathered token, or the row relative to the tile's first
-        const int src = gather ? gs[r >> 1] : min(r >> 1, t.row_end - 1 - t.row0);
+        const int src = gather ? gs[tr] : min(tr, t.row_end - 1 - t.row0);
         a_cur[u] = (uint32_t)(2 * src + (r & 1)) * d_in * 8 + a_pc[u];
       }
       if (gather != nullptr && wave == 3 && iam + 1 < n_mine) {
@@ -847,7 +890,6 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
     fkc = last ? 0 : fkc + 1;
     fas = odd ? (fas == C::NA - 1 ? 0 : fas + 1) : fas;
     fws = fws == C::NW - 1 ? 0 : fws + 1;
-    (void)NR;
   };
   int f = 0;
   for (; f < n_full * nk; f += 2) {
