@@ -131,7 +131,39 @@ __global__ __launch_bounds__(256) void dispatch_kernel(const void* __restrict__ 
   }
 }
 
-template <int YT, bool Y_MASK, int OT, bool RESID>
+// Compare-exchange of slots i < j by expert (slot j ends with the larger), as value
+// selects: the slot arrays stay in registers and no lane branches.
+template <int KM>
+__device__ __forceinline__ void slot_cx(int (&ex)[KM], int (&row)[KM], float (&w)[KM], int i, int j) {
+  const bool sw = ex[j] < ex[i];
+  const int e0 = sw ? ex[j] : ex[i], e1 = sw ? ex[i] : ex[j];
+  const int r0 = sw ? row[j] : row[i], r1 = sw ? row[i] : row[j];
+  const float w0 = sw ? w[j] : w[i], w1 = sw ? w[i] : w[j];
+  ex[i] = e0; ex[j] = e1;
+  row[i] = r0; row[j] = r1;
+  w[i] = w0; w[j] = w1;
+}
+// The slots in ascending expert order: sorting networks for 2, 4 and 8 slots (the
+// experts of a token are distinct; unused slots carry the largest key and sort last)
+template <int KM>
+__device__ __forceinline__ void sort_slots(int (&ex)[KM], int (&row)[KM], float (&w)[KM]) {
+  static_assert(KM == 2 || KM == 4 || KM == 8, "slot network");
+  if constexpr (KM == 2) {
+    slot_cx<KM>(ex, row, w, 0, 1);
+  } else if constexpr (KM == 4) {
+    constexpr int net[5][2] = {{0, 1}, {2, 3}, {0, 2}, {1, 3}, {1, 2}};
+#pragma unroll
+    for (int q = 0; q < 5; ++q) slot_cx<KM>(ex, row, w, net[q][0], net[q][1]);
+  } else {  // Batcher's odd-even merge sort of 8
+    constexpr int net[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                                {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int q = 0; q < 19; ++q) slot_cx<KM>(ex, row, w, net[q][0], net[q][1]);
+  }
+}
+
+// KM: the slots a token can have, k <= KM (2, 4 or 8)
+template <int YT, bool Y_MASK, int OT, bool RESID, int KM>
 __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ ys, int N, int k, int d,
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_w,
@@ -142,10 +174,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * kTokPerBlock + (threadIdx.x >> 6);
   if (t >= N) return;
-  int ex[8], row[8];
-  float w[8];
+  int ex[KM], row[KM];
+  float w[KM];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
+  for (int s = 0; s < KM; ++s) {  // unconditional loads (slots past k repeat the last one), then masked
     const size_t f = (size_t)t * k + min(s, k - 1);
     const int e = topk_idx[f], rw = slot_pos[f];
     const float ws = topk_w[f];
@@ -154,25 +186,22 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     row[s] = on ? rw : 0;
     w[s] = on ? ws : 0.f;
   }
-  // ascending expert order (insertion sort over <= 8 slots; distinct experts)
-#pragma unroll
-  for (int a = 1; a < 8; ++a)
-#pragma unroll
-    for (int b = a; b > 0; --b)
-      if (ex[b] < ex[b - 1]) {
-        int te = ex[b]; ex[b] = ex[b - 1]; ex[b - 1] = te;
-        int tr = row[b]; row[b] = row[b - 1]; row[b - 1] = tr;
-        float tw = w[b]; w[b] = w[b - 1]; w[b - 1] = tw;
-      }
-  // k <= 4: the rows of KM slots loaded raw and unconditionally (a slot past k repeats
-  // the last row: a cache hit), all in flight before the first is used -- a load
-  // inside `if (s < k)` is waited for inside its branch, one round trip per slot.
+  sort_slots<KM>(ex, row, w);  // ascending expert order
+  // bf16 rows, KM <= 4: the rows of the KM slots loaded raw and unconditionally (a slot
+  // past k repeats the last row: a cache hit), all in flight before the first is used --
+  // a load inside `if (s < k)` is waited for inside its branch, one round trip per slot.
   // Same products and adds, in the same order, as the loop below.
-  auto rows_raw = [&](auto km_tag) __attribute__((always_inline)) {
-    constexpr int KM = decltype(km_tag)::value;
+  if constexpr (YT == kBF16 && KM <= 4) {  // (fp32 rows: measured no faster, the loop below serves them)
     int rs[KM];
+    const int last = row[0];
 #pragma unroll
-    for (int s = 0; s < KM; ++s) rs[s] = row[s < k ? s : k - 1];
+    for (int s = 0; s < KM; ++s) {
+      int rl = last;  // row[k - 1] without indexing the register array
+#pragma unroll
+      for (int q = 1; q < KM; ++q)
+        if (q == k - 1) rl = row[q];
+      rs[s] = s < k ? row[s] : rl;
+    }
     for (int i = lane; i < d; i += 64) {
       RawMV<YT> y[KM];
 #pragma unroll
@@ -183,17 +212,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
 #pragma unroll
       for (int s = 0; s < KM; ++s) {
         float v[8];
-        if constexpr (YT == kF32) {
-          const uint32_t u[8] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w, y[s].b.x, y[s].b.y, y[s].b.z, y[s].b.w};
+        const uint32_t u[4] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w};
 #pragma unroll
-          for (int c = 0; c < 8; ++c) v[c] = __uint_as_float(u[c]);
-        } else {
-          const uint32_t u[4] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            v[2 * c] = bf16_bits_to_f32((uint16_t)(u[c] & 0xffff));
-            v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(u[c] >> 16));
-          }
+        for (int c = 0; c < 4; ++c) {
+          v[2 * c] = bf16_bits_to_f32((uint16_t)(u[c] & 0xffff));
+          v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(u[c] >> 16));
         }
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc.v[c] = s < k ? acc.v[c] + w[s] * v[c] : acc.v[c];
@@ -210,23 +233,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
       }
       store_mv<OT>(out, (size_t)t * d + i, acc);
     }
-  };
-  if constexpr (YT == kBF16) {  // (fp32 rows: measured no faster, the loop below serves them)
-    if (k <= 2) {
-      rows_raw(std::integral_constant<int, 2>{});
-      return;
-    }
-    if (k <= 4) {
-      rows_raw(std::integral_constant<int, 4>{});
-      return;
-    }
+    return;
   }
   for (int i = lane; i < d; i += 64) {
     MV acc;
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int s = 0; s < KM; ++s) {
       if (s < k) {
         const MV y = load_mv<YT>(ys, (size_t)row[s] * d + i);
 #pragma unroll
@@ -490,15 +504,20 @@ YGG_API int ygg_dispatch(const void* x, int dtype, int N, int k, int d, const in
 template <int YT, int OT>
 static void launch_combine(int grid, hipStream_t st, const void* ys, int N, int k, int d, const int32_t* idx,
                            const float* w, const int32_t* sp, const void* resid, void* out, bool y_mask) {
-#define YGG_C(YM, RS) combine_kernel<YT, YM, OT, RS><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out)
+#define YGG_C1(YM, RS, KM) combine_kernel<YT, YM, OT, RS, KM><<<grid, 256, 0, st>>>(ys, N, k, d, idx, w, sp, resid, out)
+#define YGG_C(YM, RS)                           \
+  if (k <= 2) YGG_C1(YM, RS, 2);               \
+  else if (k <= 4) YGG_C1(YM, RS, 4);          \
+  else YGG_C1(YM, RS, 8)
   if (y_mask) {
-    if (resid) YGG_C(true, true);
-    else YGG_C(true, false);
+    if (resid) { YGG_C(true, true); }
+    else { YGG_C(true, false); }
   } else {
-    if (resid) YGG_C(false, true);
-    else YGG_C(false, false);
+    if (resid) { YGG_C(false, true); }
+    else { YGG_C(false, false); }
   }
 #undef YGG_C
+#undef YGG_C1
 }
 
 template <bool SR>
