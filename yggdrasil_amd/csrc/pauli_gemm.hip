@@ -580,6 +580,8 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   // tiles per XCD, whole rounds first; then items of half the work, dealt round robin
   // over the XCD's workgroups: the XCD's range of compact tiles, then (when the whole
   // tiles leave at most half a round) the remaining whole tiles cut into half tiles.
+  // When the whole tiles end in a partial round, the items go first to the workgroups
+  // that run one whole tile fewer.
   const int CT = (d_out + BN - 1) / BN;
   const int n_tiles = __builtin_amdgcn_readfirstlane(s_tbeg[E]) * CT;
   const int n_ctiles = __builtin_amdgcn_readfirstlane(s_cbeg[E]) * CT;
@@ -594,13 +596,16 @@ __global__ __launch_bounds__(PauliDmaTile::NT) __attribute__((amdgpu_waves_per_e
   const int n_full = split ? rounds : (R > slot ? (R - slot + per_xcd - 1) / per_xcd : 0);
   const int n_comp = chi - clo;                                // compact items of this XCD
   const int n_items = n_comp + (split ? 2 * rem : 0);          // half-work items of this XCD
-  const int n_mine = n_full + (n_items > slot ? (n_items - slot + per_xcd - 1) / per_xcd : 0);
+  // the items are dealt from the first workgroup that runs one whole tile fewer (slot
+  // rem) on, wrapping round: ranks ir
+  const int ir = split ? slot : (slot - rem + per_xcd) % per_xcd;
+  const int n_mine = n_full + (n_items > ir ? (n_items - ir + per_xcd - 1) / per_xcd : 0);
   const int total = n_mine * nk, total_a = n_mine * nka;
   if (total == 0) return;
 
   auto decode = [&](int n) __attribute__((always_inline)) {
     PauliTileInfo t;
-    const int item = n >= n_full ? slot + (n - n_full) * per_xcd : -1;
+    const int item = n >= n_full ? ir + (n - n_full) * per_xcd : -1;
     if (item >= 0 && item < n_comp) {  // a compact tile: an expert's short last row tile
       const int C = clo + item;
       const int rt = C / CT, ct = C - rt * CT;
