@@ -526,7 +526,7 @@ static int combine_planes_t(const float* y_planes, int planes, int P_max, int N,
                             void* out, int out_dtype, hipStream_t stream) {
   if (N == 0) return 0;
   const size_t stride = (size_t)P_max * d;
-  if (planes == 4 || planes == 8) {  // the decode layer's partial planes: the half-multivector kernel
+  if ((planes >= 2 && planes <= 4) || planes == 8) {  // the half-multivector kernel
     const unsigned hgrid = (unsigned)(((size_t)N * d * 2 + 255) / 256);
 #define YGG_CH(OT, RS, PL)                                                                                          \
   combine_planes_half_kernel<OT, RS, PL, SR><<<hgrid, 256, 0, stream>>>(y_planes, N, k, d, topk_idx, topk_w,        \
@@ -535,7 +535,7 @@ static int combine_planes_t(const float* y_planes, int planes, int P_max, int N,
 #define YGG_CH2(PL)                                                                        \
   if (out_dtype == kF32) { if (residual) YGG_CH(kF32, true, PL); else YGG_CH(kF32, false, PL); } \
   else { if (residual) YGG_CH(kBF16, true, PL); else YGG_CH(kBF16, false, PL); }
-    if (planes == 8) { YGG_CH2(8) } else { YGG_CH2(4) }
+    if (planes == 8) { YGG_CH2(8) } else if (planes == 4) { YGG_CH2(4) } else if (planes == 3) { YGG_CH2(3) } else { YGG_CH2(2) }
 #undef YGG_CH2
 #undef YGG_CH
     return check_launch("combine (partial planes)");

@@ -428,9 +428,14 @@ int ygg::pauli_f32_prepare_weights(const float* W, int E, int d_out, int d_in, v
   return check_launch("pauli_f32_prep");
 }
 
+// Contraction splits of the partial-plane product: as many as keep every workgroup of
+// 16-token tiles on a CU of its own (the launch rounds row tiles up to the XCD count)
 int ygg::pauli_f32_splits(int P_max, int E, int d_in, int d_out) {
-  const long long tiles = ((long long)(P_max + kF32Tok - 1) / kF32Tok + E) * ((d_out + kF32Cols - 1) / kF32Cols);
-  long long s = (256 + tiles - 1) / tiles;  // about one workgroup per CU in total
+  const int n_xcd = f32_xcds();
+  long long rts = ((long long)P_max + kF32Tok - 1) / kF32Tok + E;
+  rts = (rts + n_xcd - 1) / n_xcd * n_xcd;
+  const long long tiles = rts * ((d_out + kF32Cols - 1) / kF32Cols);
+  long long s = f32_cus() / tiles;
   s = std::min<long long>(s, std::max(1, d_in / 16));
   return (int)std::max<long long>(s, 1);
 }
