@@ -157,11 +157,12 @@ __global__ __launch_bounds__(256) void dp_prep_kernel(const float* __restrict__ 
 }
 
 // 16-bit fixed point value -> (hi, lo) int8 planes with v = 256 hi + lo, |v| <= 2^14.
-// x scale lies in [-2^14, 2^14] for every finite row; the clamp (NaN to 0) keeps the
-// conversion defined for a non-finite row, whose inverse scale makes its outputs NaN.
+// x scale lies in [-2^14, 2^14] for every finite row; the clamp (fmaxf and fminf return
+// the operand that is not NaN, so NaN lands on -2^14) keeps the conversion defined for a
+// non-finite row, whose inverse scale makes its outputs NaN.
 __device__ inline void dp_split(float x, float scale, int& hi, int& lo) {
   const float t = x * scale;
-  const int v = (int)rintf(t == t ? fminf(fmaxf(t, -16384.f), 16384.f) : 0.f);
+  const int v = (int)rintf(fminf(fmaxf(t, -16384.f), 16384.f));
   hi = (v + 128) >> 8;
   lo = v - (hi << 8);
 }
@@ -519,7 +520,7 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       for (int q = 0; q < 4; ++q) {
         hc0[q] = ok ? hc0[q] : 0.f;
         hc1[q] = ok ? hc1[q] : 0.f;
-        m = fmaxf(m, fmaxf(dc_mag(hc0[q]), dc_mag(hc1[q])));
+        m = fmaxf(m, fmaxf(fabsf(hc0[q]), fabsf(hc1[q])));
       }
       m = dc_row_max(m);  // over the token's 8 channels x 2 rows in this wave
       if (n == 0) s_hmax[rb][wave][g] = m;
@@ -529,7 +530,12 @@ __global__ __launch_bounds__(kDpThreads) void decode_pauli_kernel(
       for (int w = 0; w < kDpWaves; ++w) mx = fmaxf(mx, s_hmax[rb][w][g]);
       const int sh = dc_shift(mx);
       const float hs = ldexpf(1.0f, sh);
-      if (wave == 0 && n == 0) s_hinv[tk] = dc_inv_scale(mx, sh);
+      // a hidden row is non-finite through an infinite entry (its maximum) or through a
+      // non-finite input row (NaN inverse scale: its hidden row is NaN)
+      if (wave == 0 && n == 0) {
+        const float xinv = s_xinv[tk];
+        s_hinv[tk] = xinv == xinv ? dc_inv_scale(mx, sh) : xinv;
+      }
       // lane (jj, a) writes the rows of column b = a: entries (H[0][a].p, H[1][a].p) at
       // K position hidden channel 8 wave + jj (K step wave / 4, lane group wave % 4)
 #pragma unroll
