@@ -280,6 +280,35 @@ def test_pauli_integer_product_exact_with_compact_tiles(d_in, d_out, gathered, y
         assert bad[0].size == 0, (e, int(counts[e]), bad[0][:8])
 
 
+@pytest.mark.parametrize("d_in,d_out", [(128, 512), (512, 128)])
+def test_pauli_integer_product_exact_items_after_partial_round(d_in, d_out):
+    """Config 3's expert-parallel share: 4 experts of about 1930 rows, three of them ending in
+    compact tiles.  The whole tiles end in a partial round that is not cut into halves (up
+    shape, 512 workgroups over 8 XCDs) or fill fewer workgroups than the grid holds (down shape,
+    one XCD range), so the compact items go to the workgroups that run one whole tile fewer.
+    Exact integer products, every row, against the float64 dense oracle."""
+    from oracle import dense
+    ops = _ops()
+    g = np.random.default_rng(d_in + d_out + 7)
+    counts = np.array([1930, 1950, 1900, 1937], np.int64)
+    E, P = counts.size, int(counts.sum())
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    W = g.integers(-2, 3, size=(E, d_out, d_in, 8)).astype(np.float32)
+    x = g.integers(-2, 3, size=(P, d_in, 8)).astype(np.float32)
+    b = g.integers(-3, 4, size=(E, d_out, 8)).astype(np.float32)
+    say(f"pauli integer product, items after a partial round d_in={d_in} d_out={d_out} P={P}")
+    xt = ops.pauli_rows_from_blade(torch.from_numpy(x).cuda().bfloat16())
+    y = ops.pauli_grouped_linear(xt, ops.prepare_weights(torch.from_numpy(W).cuda(), "pauli"),
+                                 torch.from_numpy(offsets).cuda(), ops.prepare_bias(torch.from_numpy(b).cuda()),
+                                 "none", x_layout="pauli", y_layout="blade", out_dtype=torch.float32)
+    y = y.cpu().numpy()
+    for e in range(E):
+        rows = slice(offsets[e], offsets[e + 1])
+        ref = dense.linear(x[rows], W[e], b[e])
+        bad = np.nonzero(np.any(y[rows] != ref, axis=-1))
+        assert bad[0].size == 0, (e, int(counts[e]), bad[0][:8])
+
+
 def _blade_to_pauli_rows(y):
     """(rows, d, 8) blade order -> (rows, 2, d, 4) Pauli half-rows: half b holds column b of each
     multivector's 2x2 complex matrix as (row 0 re, row 0 im, row 1 re, row 1 im)."""
