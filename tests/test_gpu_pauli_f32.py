@@ -160,3 +160,45 @@ def test_layer_pauli_f32_large_down_splits(N, k):
             e = idx[t, s]
             ref[t] += w[t, s] * moe.clifford_ffn(x[0, t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
     assert normwise_err(out, ref) < TOL_F32
+
+
+@pytest.mark.parametrize("N,E,k", [(256, 8, 2), (1, 4, 1), (77, 32, 4), (256, 32, 8), (200, 16, 3), (257, 8, 2)])
+def test_layer_pauli_f32_routed_up_product(N, E, k):
+    """Batches of at most 256 tokens with logits route inside the fp32 up product (no routing launch)
+    and read x's blade rows: the routing arrays equal ygg_route's bit for bit, and the layer matches the
+    float64 oracle.  (257, 8, 2) takes the routing launch instead, for contrast; (200, 16, 3) leaves
+    some experts without tokens (logits shifted away from them); rows 2 and 3 hold ties."""
+    ops = _ops()
+    g = np.random.default_rng(1000 + N + E + k)
+    d, F = 16, 48
+    x = g.standard_normal((N, d, 8), dtype=np.float32)
+    wu = (g.standard_normal((E, F, d, 8), dtype=np.float32) / np.sqrt(8 * d)).astype(np.float32)
+    wd = (g.standard_normal((E, d, F, 8), dtype=np.float32) / np.sqrt(8 * F)).astype(np.float32)
+    bu = (0.1 * g.standard_normal((E, F, 8))).astype(np.float32)
+    bd = (0.1 * g.standard_normal((E, d, 8))).astype(np.float32)
+    logits_np = g.standard_normal((N, E), dtype=np.float32)
+    if N > 3:
+        logits_np[3, :] = 0.25  # a row of ties: the lowest indices win
+        logits_np[2, 1::2] = logits_np[2, 0]  # ties with the row's first logit
+    if N == 200:
+        logits_np[:, [1, 5, 6]] -= 40.0  # experts 1, 5, 6 are never chosen
+    say(f"routed fp32 up product N={N} E={E} k={k}")
+    xt, lt = torch.from_numpy(x).cuda(), torch.from_numpy(logits_np).cuda()
+    pu = ops.prepare_weights(torch.from_numpy(wu).cuda(), "pauli_f32")
+    pd = ops.prepare_weights(torch.from_numpy(wd).cuda(), "pauli_f32")
+    out, r = ops.moe_forward(xt, k, pu, pd, b_up=ops.prepare_bias(torch.from_numpy(bu).cuda()),
+                             b_down=ops.prepare_bias(torch.from_numpy(bd).cuda()), act="gelu", logits=lt)
+    rr = ops.route(lt, k)
+    torch.cuda.synchronize()
+    for key in ("topk_idx", "topk_w", "counts", "offsets"):
+        a, b = r[key].cpu().numpy(), getattr(rr, key).cpu().numpy()
+        assert np.array_equal(a.view(np.int32), b.view(np.int32)), key
+    if N == 200:
+        assert (r["counts"].cpu().numpy()[[1, 5, 6]] == 0).all()
+    idx, w = r["topk_idx"].cpu().numpy(), r["topk_w"].cpu().numpy()
+    ref = np.zeros_like(x)
+    for t in range(N):
+        for s in np.argsort(idx[t]):
+            e = idx[t, s]
+            ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+    assert normwise_err(out.cpu().numpy(), ref) < TOL_F32

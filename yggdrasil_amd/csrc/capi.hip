@@ -198,10 +198,13 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     return combine_planes(static_cast<const float*>(ys), decode_layer_planes(F), (int)P, N, k, d, topk_idx, topk_w,
                           slot_pos, residual, out, dtype, stream);
   }
+  // fp32 Pauli weights, logits given, a batch of at most 256 tokens: the up product
+  // routes the batch itself and reads x's blade rows, so no routing launch runs
+  const bool f32_routed_up = w_format == kWPauliF32 && logits && pauli_f32_route_fusable(N, E, k);
   // the Pauli formats' conversion of x to Pauli rows (into the x_sorted region: N <= P
   // rows) runs as extra workgroups of the routing's first launch
   ygg::RowConvert cv;
-  if (w_format == kWPauli || w_format == kWPauliF32) {
+  if ((w_format == kWPauli || w_format == kWPauliF32) && !f32_routed_up) {
     cv.x = x;
     cv.out = xs;
     cv.n = (long long)N * d;
@@ -216,7 +219,7 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     row_slot = reinterpret_cast<int32_t*>(static_cast<char*>(ys) + align256(ys_bytes(P, E, d, F, dtype, w_format)));
     cv.row_slot = row_slot;
   }
-  if (fused_route) {
+  if (fused_route || f32_routed_up) {
     // routed below
   } else if (!logits) {  // CliffordRouter energy signature, fused into the routing kernel for small N
     if (ygg::route_energy_convert(x, dtype, N, d, router_w, router_b, E, k, topk_idx, topk_w, counts, offsets, perm,
@@ -228,12 +231,19 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
   }
   if (w_format == kWPauliF32) {
     // fp32 Pauli: x's Pauli rows (converted with the routing) are gathered through perm
-    // by the up product; the down product runs in K splits whose partial planes the
-    // combine adds in split order
+    // by the up product, or the routed up product reads x's blade rows itself; the
+    // down product runs in K splits whose partial planes the combine adds in split order
     const int splits = pauli_f32_splits((int)P, E, F, d);
-    if (pauli_f32_linear_save_pre(static_cast<const float*>(xs), perm, (int)P, static_cast<const float*>(w_up), b_up,
-                                  offsets, E, d, F, act, static_cast<float*>(h), h_pre_out, stream))
+    if (f32_routed_up) {
+      if (pauli_f32_up_routed(static_cast<const float*>(x), logits, N, E, k, topk_idx, topk_w, counts, offsets, perm,
+                              slot_pos, row_slot, static_cast<const float*>(w_up), b_up, d, F, act,
+                              static_cast<float*>(h), h_pre_out, stream))
+        return -1;
+    } else if (pauli_f32_linear_save_pre(static_cast<const float*>(xs), perm, (int)P,
+                                         static_cast<const float*>(w_up), b_up, offsets, E, d, F, act,
+                                         static_cast<float*>(h), h_pre_out, stream)) {
       return -1;
+    }
     if (pauli_f32_linear_partial(static_cast<const float*>(h), (int)P, static_cast<const float*>(w_down), b_down,
                                  offsets, E, F, d, splits, static_cast<float*>(ys), stream, row_slot))
       return -1;

@@ -35,8 +35,10 @@
 // were measured 40-80 % slower at the C3 shape.)
 
 #include <algorithm>
+#include <type_traits>
 
 #include "pauli_common.h"
+#include "route_select.h"
 
 namespace ygg {
 
@@ -73,42 +75,86 @@ __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E,
   return false;
 }
 
+// A operands read from blade rows (the routed up product, which has no converted
+// copy of x): the lane of GEMM row (t, b), part k, needs four of an input
+// multivector's eight blade values -- the pair (x0, x1) and the singles x3, x5 for
+// k = 0, the pair (x6, x7) and x2, x4 for k = 1 -- and forms its operand pair
+// (X[0][b], X[1][b]) with the adds of blade_to_pauli: u = pair.x + s1, v = pair.y +
+// s2, the singles negated for b = 1 (x + (-y) is x - y exactly), then (u, v) or
+// (v, u) as k xor b.  The values equal those of the stand-alone conversion.
+struct F32BladeLane {
+  int off_pair, off_s1, off_s2;  // float offsets in a multivector
+  uint32_t neg;                  // sign bit of the singles (b = 1)
+  bool swap;                     // k xor b
+};
+__device__ inline F32BladeLane f32_blade_lane(int b, int k) {
+  F32BladeLane l;
+  l.off_pair = k ? 6 : 0;
+  l.off_s1 = k ? 2 : 3;
+  l.off_s2 = k ? 4 : 5;
+  l.neg = b ? 0x80000000u : 0u;
+  l.swap = (k ^ b) != 0;
+  return l;
+}
+
 // The contraction over inputs [i0, i1) of one wave's WR blocks of 32 GEMM rows x 32
 // columns: operands of input i are x (re, im) of the lane's GEMM row in block r
-// (arow[r] + 8 i) and the eight weight floats of its column (wrow + i w_step), which
-// every row block shares.  Blocks of U inputs are double buffered in registers, so
-// one block's loads are in flight while the previous block's MFMAs run.  i0, i1
-// must be wave-uniform.
-template <int WR>
+// (arow[r] + 8 i; with BLADE, formed from the blade values there as above) and the
+// eight weight floats of its column (wrow + i w_step), which every row block shares.
+// Blocks of U inputs are double buffered in registers, so one block's loads are in
+// flight while the previous block's MFMAs run.  i0, i1 must be wave-uniform.
+template <int WR, bool BLADE = false>
 __device__ inline void f32_kloop(f32x16v_t (&acc)[WR][2][2], const float* const (&arow)[WR],
-                                 const float* __restrict__ wrow, size_t w_step, int i0, int i1) {
+                                 const float* __restrict__ wrow, size_t w_step, int i0, int i1,
+                                 const F32BladeLane bl = F32BladeLane{}) {
   constexpr int U = WR == 1 ? kF32U : kF32U / 2;
+  using XT = std::conditional_t<BLADE, float4, float2>;  // blade: (pair, s1, s2) as loaded
   struct Ops {
-    float2 xa[WR];
+    XT xa[WR];
     float4 w0, w1;
   };
   auto load_op = [&](int i, Ops& o) {
 #pragma unroll
-    for (int r = 0; r < WR; ++r) o.xa[r] = *reinterpret_cast<const float2*>(arow[r] + (size_t)i * 8);
+    for (int r = 0; r < WR; ++r) {
+      if constexpr (BLADE) {
+        const float* mv = arow[r] + (size_t)i * 8;
+        const float2 pr = *reinterpret_cast<const float2*>(mv + bl.off_pair);
+        o.xa[r] = make_float4(pr.x, pr.y, mv[bl.off_s1], mv[bl.off_s2]);
+      } else {
+        o.xa[r] = *reinterpret_cast<const float2*>(arow[r] + (size_t)i * 8);
+      }
+    }
     o.w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
     o.w1 = *reinterpret_cast<const float4*>(wrow + i * w_step + 4);  // c = 1
   };
+  auto a_pair = [&](const XT& q) __attribute__((always_inline)) -> float2 {
+    if constexpr (BLADE) {
+      const float u = q.x + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, q.z) ^ bl.neg);
+      const float v = q.y + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, q.w) ^ bl.neg);
+      return bl.swap ? make_float2(v, u) : make_float2(u, v);
+    } else {
+      return q;
+    }
+  };
   auto mma = [&](const Ops& o) {
+    float2 xa[WR];
+#pragma unroll
+    for (int r = 0; r < WR; ++r) xa[r] = a_pair(o.xa[r]);
 #pragma unroll
     for (int r = 0; r < WR; ++r) {
       f32x16v_t(&a)[2][2] = acc[r];
-      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.x, a[0][0], 0, 0, 0);
-      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.y, a[0][1], 0, 0, 0);
-      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.z, a[1][0], 0, 0, 0);
-      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.w, a[1][1], 0, 0, 0);
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.w, a[1][1], 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < WR; ++r) {
       f32x16v_t(&a)[2][2] = acc[r];
-      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.x, a[0][0], 0, 0, 0);
-      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.y, a[0][1], 0, 0, 0);
-      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.z, a[1][0], 0, 0, 0);
-      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.w, a[1][1], 0, 0, 0);
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.w, a[1][1], 0, 0, 0);
     }
   };
 #pragma unroll
@@ -185,17 +231,40 @@ __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y0
   }
 }
 
-template <int ACT, int OUT, int WR>  // WR row blocks of 16 tokens per wave
+// The routing of a small batch inside the up product (RQ > 0): every workgroup
+// selects the top-k of every token from the logits (the selection of ygg_route,
+// route_select.h), counts each expert's slots, finds its own row tile among the
+// experts' rows and this expert's tokens in ascending order, and writes the routing
+// arrays of its tile's rows (the first column tile) -- the same counts, offsets,
+// permutation and slot positions as ygg_route.  Workgroup 0 writes counts and
+// offsets.  x is then read as blade rows (no converted copy).
+constexpr int kF32FuseTokens = 64 * kF32Waves;           // one token per thread
+constexpr int kF32FuseSlots = kF32FuseTokens * kMaxTopK;
+constexpr int kF32FuseQ = 4;                             // up to 8 RQ logits per token: E <= 32
+struct F32Route {
+  const float* logits = nullptr;
+  int N = 0, k = 0;
+  int32_t* topk_idx = nullptr;
+  float* topk_w = nullptr;
+  int32_t* counts = nullptr;
+  int32_t* offsets = nullptr;
+  int32_t* perm = nullptr;
+  int32_t* slot_pos = nullptr;
+  int32_t* row_slot = nullptr;  // when set: row_slot[row] = the row's slot t k + s
+};
+
+template <int ACT, int OUT, int WR, int RQ = 0>  // WR row blocks of 16 tokens per wave; RQ > 0: routed
 __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(2))) void pauli_f32_kernel(
     const float* __restrict__ X, const int32_t* __restrict__ gather, const float* __restrict__ Wp,
     const float* __restrict__ bias, const int32_t* __restrict__ offsets, int E, int d_in, int d_out, int P_max,
-    float* __restrict__ Y, float* __restrict__ Ypre, const int32_t* __restrict__ row_map, int n_xcd) {
+    float* __restrict__ Y, float* __restrict__ Ypre, const int32_t* __restrict__ row_map, int n_xcd,
+    F32Route route = F32Route{}) {
   constexpr int TOK = kF32Tok * WR;  // tokens per tile
   // the waves' partial sums: one round for WR = 1; for WR = 2 waves 2, 3 hand theirs
   // to waves 0, 1 first, so the buffer holds two waves' tiles
   constexpr int PW = WR == 1 ? kF32Waves : 2;
   __shared__ float4 part[PW][2 * TOK][kF32Cols + 1];  // (a0 re, a0 im, a1 re, a1 im)
-  int e, row0, row_end;
+  int e = 0, row0 = 0, row_end = 0;
   // The column tiles of one row tile run on one XCD, one after the other in
   // dispatch order, so its rows are read once into that XCD's L2: workgroup b runs
   // on XCD b mod n_xcd and takes column tile (b / n_xcd) mod n_ct of row tile
@@ -203,22 +272,136 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
   const int n_ct = (d_out + kF32Cols - 1) / kF32Cols;
   const int xcd = blockIdx.x % n_xcd, q = blockIdx.x / n_xcd;
   const int ct = q % n_ct, rt = (q / n_ct) * n_xcd + xcd;
-  if (!f32_find_tile<TOK>(offsets, E, rt, e, row0, row_end)) return;
-  const int col0 = ct * kF32Cols;
-  const int split = blockIdx.z, splits = gridDim.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the K loop runs on scalars
   const int l32 = lane & 31, k = lane >> 5;
+  // routed: LDS scratch on top of part (free until the partial sums), and the
+  // expert's first row (this expert's tokens are rows_tok[row - row_beg])
+  int row_beg = 0;
+  int32_t* const s_sel = reinterpret_cast<int32_t*>(&part[0][0][0]);
+  float* const s_w = reinterpret_cast<float*>(s_sel + kF32FuseSlots);
+  int32_t* const s_off = reinterpret_cast<int32_t*>(s_w + kF32FuseSlots);  // kMaxExperts + 1
+  int32_t* const s_cnt = s_off + kMaxExperts + 1;                             // kMaxExperts
+  int32_t* const s_wv = s_cnt + kMaxExperts;                                  // kF32Waves
+  int32_t* const rows_tok = s_wv + kF32Waves;                                 // kF32FuseTokens
+  static_assert((2 * kF32FuseSlots + 2 * kMaxExperts + 1 + kF32Waves + kF32FuseTokens) * 4 <= (int)sizeof(part),
+                "routing scratch exceeds the partial-sum buffer");
+  if constexpr (RQ > 0) {
+    const int N = route.N, kk = route.k;
+    // one token per thread: its logits, then its selection (select_one_thread)
+    constexpr int EMAX = kSelLanes * RQ;
+    float lg[EMAX];
+    if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(route.logits) & 15) == 0) {  // the row in 16-byte pieces
+#pragma unroll
+      for (int x = 0; x < EMAX; x += 4) {
+        const float4 v = (tid < N && x < E) ? *reinterpret_cast<const float4*>(route.logits + (size_t)tid * E + x)
+                                            : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        lg[x] = v.x;
+        lg[x + 1] = v.y;
+        lg[x + 2] = v.z;
+        lg[x + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int x = 0; x < EMAX; ++x) lg[x] = (tid < N && x < E) ? route.logits[(size_t)tid * E + x] : -INFINITY;
+    }
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
+    __syncthreads();  // the counters are zero before any thread counts (the logits are in flight)
+    if (tid < N) {
+      int se[kMaxTopK];
+      float sw[kMaxTopK];
+      select_one_thread<EMAX>(lg, E, kk, se, sw);
+#pragma unroll
+      for (int s = 0; s < kMaxTopK; ++s)
+        if (s < kk) {
+          s_sel[tid * kk + s] = se[s];
+          s_w[tid * kk + s] = sw[s];
+          atomicAdd(&s_cnt[se[s]], 1);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the counts over experts (E <= 64: one lane each)
+      const int c = lane < E ? s_cnt[lane] : 0;
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+      }
+      if (lane < E) s_off[lane] = incl - c;
+      if (lane == E - 1) s_off[E] = incl;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && blockIdx.z == 0 && tid <= E) {
+      if (tid < E) route.counts[tid] = s_off[tid + 1] - s_off[tid];
+      route.offsets[tid] = s_off[tid];
+    }
+    // this workgroup's row tile (as f32_find_tile, over the offsets just made)
+    bool found = false;
+    {
+      int acc_t = 0;
+      for (int x = 0; x < E && !found; ++x) {
+        const int beg = s_off[x], end = s_off[x + 1];
+        const int nt = (end - beg + TOK - 1) / TOK;
+        if (rt < acc_t + nt) {
+          e = x;
+          row_beg = beg;
+          row0 = beg + (rt - acc_t) * TOK;
+          row_end = end;
+          found = true;
+        }
+        acc_t += nt;
+      }
+    }
+    if (!found) return;  // uniform
+    // this expert's tokens in ascending order: a ballot per wave, then wave bases
+    bool mine = false;
+    if (tid < N)
+      for (int s = 0; s < kk; ++s) mine |= s_sel[tid * kk + s] == e;
+    const uint64_t bal = __ballot(mine);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    if (lane == 0) s_wv[wave] = __popcll(bal);
+    __syncthreads();
+    if (mine) {
+      int base = 0;
+      for (int w = 0; w < wave; ++w) base += s_wv[w];
+      rows_tok[base + __popcll(bal & lt_mask)] = tid;
+    }
+    __syncthreads();
+    if (ct == 0 && blockIdx.z == 0) {  // the routing arrays of this tile's rows
+      for (int r = row0 + tid; r < min(row0 + TOK, row_end); r += 64 * kF32Waves) {
+        const int t = rows_tok[r - row_beg];
+        int s = 0;
+        while (s_sel[t * kk + s] != e) ++s;
+        const int f = t * kk + s;
+        route.topk_idx[f] = e;
+        route.topk_w[f] = s_w[f];
+        route.slot_pos[f] = r;
+        route.perm[r] = t;
+        if (route.row_slot != nullptr) route.row_slot[r] = f;
+      }
+    }
+  } else {
+    if (!f32_find_tile<TOK>(offsets, E, rt, e, row0, row_end)) return;
+  }
+  const int col0 = ct * kF32Cols;
+  const int split = blockIdx.z, splits = gridDim.z;
 
-  // A operand: GEMM row (t, b) = l32 of row block r, real (k = 0) or imaginary (k = 1) part
+  // A operand: GEMM row (t, b) = l32 of row block r, real (k = 0) or imaginary (k = 1)
+  // part; routed, the token's blade row
   const float* arow[WR];
 #pragma unroll
   for (int r = 0; r < WR; ++r) {
     int m = row0 + r * kF32Tok + (l32 >> 1);
     m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
-    const int src = gather ? gather[m] : m;
-    arow[r] = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
+    if constexpr (RQ > 0) {
+      arow[r] = X + (size_t)rows_tok[m - row_beg] * d_in * 8;
+    } else {
+      const int src = gather ? gather[m] : m;
+      arow[r] = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
+    }
   }
+  if constexpr (RQ > 0) __syncthreads();  // every wave has read rows_tok before any writes part
   // B operand: output column j (clamped: columns past d_out are not stored)
   const int jc = min(col0 + l32, d_out - 1);
   const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
@@ -229,7 +412,7 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
   const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
 
   f32x16v_t acc[WR][2][2];
-  f32_kloop<WR>(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1);
+  f32_kloop<WR, (RQ > 0)>(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1, f32_blade_lane(l32 & 1, k));
   // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4 of each row block
   if constexpr (WR == 2) {
     if (wave >= 2) {
@@ -393,7 +576,7 @@ dim3 f32_grid(int P_max, int E, int d_out, int splits, int n_xcd, int tok) {
 template <int OUT>
 int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const int32_t* gather, const float* W,
                    const float* bias, const int32_t* offsets, int E, int d_in, int d_out, int P_max, float* Y,
-                   float* Ypre = nullptr, const int32_t* row_map = nullptr) {
+                   float* Ypre = nullptr, const int32_t* row_map = nullptr, const F32Route* route = nullptr) {
   const int n_xcd = f32_xcds();
   const dim3 g1 = f32_grid(P_max, E, d_out, splits, n_xcd, kF32Tok);
   const dim3 g2 = f32_grid(P_max, E, d_out, splits, n_xcd, 2 * kF32Tok);
@@ -404,7 +587,22 @@ int launch_f32_act(int act, int splits, hipStream_t st, const float* X, const in
   else two = d_in >= 2 * d_out && n2 >= kF32TwoBlockMinGroups;
   const dim3 grid = two ? g2 : g1;
 #define YGG_F(A)                                                                                              \
-  if (two)                                                                                                    \
+  if (route != nullptr) {                                                                                     \
+    if constexpr (OUT == kF32OutPauliRows) {                                                                  \
+      if (two && E <= kSelLanes)                                                                              \
+        pauli_f32_kernel<A, OUT, 2, 1><<<grid, 64 * kF32Waves, 0, st>>>(                                      \
+            X, nullptr, W, bias, nullptr, E, d_in, d_out, P_max, Y, Ypre, row_map, n_xcd, *route);            \
+      else if (two)                                                                                           \
+        pauli_f32_kernel<A, OUT, 2, kF32FuseQ><<<grid, 64 * kF32Waves, 0, st>>>(                              \
+            X, nullptr, W, bias, nullptr, E, d_in, d_out, P_max, Y, Ypre, row_map, n_xcd, *route);            \
+      else if (E <= kSelLanes)                                                                                \
+        pauli_f32_kernel<A, OUT, 1, 1><<<grid, 64 * kF32Waves, 0, st>>>(                                      \
+            X, nullptr, W, bias, nullptr, E, d_in, d_out, P_max, Y, Ypre, row_map, n_xcd, *route);            \
+      else                                                                                                    \
+        pauli_f32_kernel<A, OUT, 1, kF32FuseQ><<<grid, 64 * kF32Waves, 0, st>>>(                              \
+            X, nullptr, W, bias, nullptr, E, d_in, d_out, P_max, Y, Ypre, row_map, n_xcd, *route);            \
+    }                                                                                                         \
+  } else if (two)                                                                                             \
     pauli_f32_kernel<A, OUT, 2><<<grid, 64 * kF32Waves, 0, st>>>(X, gather, W, bias, offsets, E, d_in, d_out, \
                                                                  P_max, Y, Ypre, row_map, n_xcd);             \
   else                                                                                                        \
@@ -446,6 +644,30 @@ int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, con
   if (P_max == 0) return 0;
   return launch_f32_act<kF32OutPartial>(kActNone, splits, stream, x, nullptr, w, bias, offsets, E, d_in, d_out, P_max,
                                         y_planes, nullptr, row_map);
+}
+
+bool ygg::pauli_f32_route_fusable(int N, int E, int k) {
+  return N >= 1 && N <= kF32FuseTokens && E >= 1 && E <= kSelLanes * kF32FuseQ && k >= 1 && k <= kMaxTopK && k <= E;
+}
+
+int ygg::pauli_f32_up_routed(const float* x, const float* logits, int N, int E, int k, int32_t* topk_idx,
+                             float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_pos,
+                             int32_t* row_slot, const float* w, const float* bias, int d_in, int d_out, int act,
+                             float* y_pauli, float* y_pre, hipStream_t stream) {
+  YGG_CHECK_ARG(pauli_f32_route_fusable(N, E, k), "routed fp32 up product: N=%d E=%d k=%d", N, E, k);
+  F32Route r;
+  r.logits = logits;
+  r.N = N;
+  r.k = k;
+  r.topk_idx = topk_idx;
+  r.topk_w = topk_w;
+  r.counts = counts;
+  r.offsets = offsets;
+  r.perm = perm;
+  r.slot_pos = slot_pos;
+  r.row_slot = row_slot;
+  return launch_f32_act<kF32OutPauliRows>(act, 1, stream, x, nullptr, w, bias, nullptr, E, d_in, d_out, N * k, y_pauli,
+                                          y_pre, nullptr, &r);
 }
 
 int ygg::pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, const float* w,

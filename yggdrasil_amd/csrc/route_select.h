@@ -1,7 +1,8 @@
 // route_select.h -- the per-token routing selection (CliffordRouter's softmax,
 // top-k and renormalisation, clifford_router.py:18-21,54-104), eight lanes per
-// token, shared by the routing kernels (route.hip) and the decode up product
-// that routes inside its own workgroups (clifford_gemm.hip).
+// token (and one token per thread), shared by the routing kernels (route.hip) and
+// the up products that route inside their own workgroups (clifford_gemm.hip,
+// pauli_f32.hip).
 #pragma once
 
 #include "ygg_common.h"
@@ -191,6 +192,78 @@ __device__ inline void select_from_logits(float (&p)[Q], int E, int k, bool acti
   float raw;
   select_topk_raw<Q>(p, E, k, active, j, lane, out_e, raw);
   out_w = renorm_slot(raw, k, j, lane);
+}
+
+// select_from_logits for one token in one thread (its E <= EMAX logits in p): the
+// same operations in the same order -- the row maximum, the exponentials, the sum as
+// the eight-lane tree forms it (E >= 8: accumulator j over elements j, j + 8, ...
+// below E - E % 8, then ((a0 + a1) + (a2 + a3)) + ((a4 + a5) + (a6 + a7)), then the
+// remaining E % 8 elements in order; fewer than 8 elements in order), the
+// probabilities, k rounds of the (probability, lower index) maximum, and the
+// renormalisation from the least probable slot -- so the experts and weights equal
+// the eight-lane version's bit for bit.  Slot s < k -> out_e[s], out_w[s].
+template <int EMAX>
+__device__ inline void select_one_thread(float (&p)[EMAX], int E, int k, int (&out_e)[kMaxTopK],
+                                         float (&out_w)[kMaxTopK]) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) m = e < E ? fmaxf(m, p[e]) : m;
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) p[e] = e < E ? expf(__fsub_rn(p[e], m)) : 0.f;
+  float sum;
+  if (E < 8) {
+    sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < EMAX && e < 8; ++e)
+      if (e < E) sum = __fadd_rn(sum, p[e]);
+  } else {
+    const int E8 = E - (E & 7);
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float r = p[j];
+#pragma unroll
+      for (int e = j + 8; e < EMAX; e += 8)
+        if (e < E8) r = __fadd_rn(r, p[e]);
+      a[j] = r;
+    }
+    sum = __fadd_rn(__fadd_rn(__fadd_rn(a[0], a[1]), __fadd_rn(a[2], a[3])),
+                    __fadd_rn(__fadd_rn(a[4], a[5]), __fadd_rn(a[6], a[7])));
+#pragma unroll
+    for (int e = 8; e < EMAX; ++e)
+      if (e >= E8 && e < E) sum = __fadd_rn(sum, p[e]);
+  }
+  const float denom = __fadd_rn(sum, 1e-12f);
+  uint64_t key[EMAX];  // as in select_topk_raw
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e) {
+    const float pr = __fdiv_rn(p[e], denom);
+    const uint64_t hi = (pr == pr) ? (uint64_t)(__builtin_bit_cast(uint32_t, pr) + 1u) << 32 : 0ull;
+    key[e] = (e < E) ? (hi | (uint64_t)(63 - e)) : 0ull;
+  }
+  float raw[kMaxTopK];
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) {
+    out_e[s] = -1;
+    raw[s] = 0.f;
+    if (s < k) {
+      uint64_t best = key[0];
+#pragma unroll
+      for (int e = 1; e < EMAX; ++e) best = key[e] > best ? key[e] : best;
+      const uint32_t bhi = (uint32_t)(best >> 32);
+      out_e[s] = 63 - (int)(best & 63ull);
+      raw[s] = bhi ? __builtin_bit_cast(float, bhi - 1u) : -1.0f;
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) key[e] = key[e] == best ? 0ull : key[e];
+    }
+  }
+  float ssum = 0.f;
+#pragma unroll
+  for (int s = kMaxTopK - 1; s >= 0; --s)
+    if (s < k) ssum = __fadd_rn(ssum, raw[s]);
+  ssum = __fadd_rn(ssum, 1e-12f);
+#pragma unroll
+  for (int s = 0; s < kMaxTopK; ++s) out_w[s] = s < k ? __fdiv_rn(raw[s], ssum) : 0.f;
 }
 
 template <int Q>

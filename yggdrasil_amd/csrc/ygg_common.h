@@ -168,6 +168,15 @@ int pauli_f32_linear_save_pre(const float* x, const int32_t* gather, int P_max, 
 int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const float* bias, const int32_t* offsets,
                              int E, int d_in, int d_out, int splits, float* y_planes, hipStream_t stream,
                              const int32_t* row_map = nullptr);  // row_map: the planes' row of each product row
+// The up product with the routing of the batch inside it (no routing launch): from
+// the logits and the blade rows of x, the routing arrays of ygg_route (and row_slot,
+// when not NULL) and the Pauli rows of h, as pauli_f32_linear_save_pre writes them.
+// For batches of at most 256 tokens and 32 experts.
+bool pauli_f32_route_fusable(int N, int E, int k);
+int pauli_f32_up_routed(const float* x, const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w,
+                        int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_pos, int32_t* row_slot,
+                        const float* w, const float* bias, int d_in, int d_out, int act, float* y_pauli,
+                        float* y_pre, hipStream_t stream);
 
 // decode-shape int8 products (clifford_gemm.hip): whether (P_max rows, E
 // experts, format) takes the weight-streaming kernel, its number of K splits
