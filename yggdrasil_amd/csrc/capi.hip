@@ -198,9 +198,10 @@ static int moe_forward_impl(const void* x, int dtype, int N, int d, int F, int E
     return combine_planes(static_cast<const float*>(ys), decode_layer_planes(F), (int)P, N, k, d, topk_idx, topk_w,
                           slot_pos, residual, out, dtype, stream);
   }
-  // fp32 Pauli weights, logits given, a batch of at most 256 tokens: the up product
-  // routes the batch itself and reads x's blade rows, so no routing launch runs
-  const bool f32_routed_up = w_format == kWPauliF32 && logits && pauli_f32_route_fusable(N, E, k);
+  // fp32 Pauli weights, logits given, a batch of at most 256 tokens of at most 64
+  // multivectors: the up product routes the batch itself and reads x's blade rows, so
+  // no routing launch runs
+  const bool f32_routed_up = w_format == kWPauliF32 && logits && pauli_f32_route_fusable(N, E, k, d);
   // the Pauli formats' conversion of x to Pauli rows (into the x_sorted region: N <= P
   // rows) runs as extra workgroups of the routing's first launch
   ygg::RowConvert cv;

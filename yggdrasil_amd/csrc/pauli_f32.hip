@@ -35,7 +35,6 @@
 // were measured 40-80 % slower at the C3 shape.)
 
 #include <algorithm>
-#include <type_traits>
 
 #include "pauli_common.h"
 #include "route_select.h"
@@ -75,86 +74,42 @@ __device__ inline bool f32_find_tile(const int32_t* __restrict__ offsets, int E,
   return false;
 }
 
-// A operands read from blade rows (the routed up product, which has no converted
-// copy of x): the lane of GEMM row (t, b), part k, needs four of an input
-// multivector's eight blade values -- the pair (x0, x1) and the singles x3, x5 for
-// k = 0, the pair (x6, x7) and x2, x4 for k = 1 -- and forms its operand pair
-// (X[0][b], X[1][b]) with the adds of blade_to_pauli: u = pair.x + s1, v = pair.y +
-// s2, the singles negated for b = 1 (x + (-y) is x - y exactly), then (u, v) or
-// (v, u) as k xor b.  The values equal those of the stand-alone conversion.
-struct F32BladeLane {
-  int off_pair, off_s1, off_s2;  // float offsets in a multivector
-  uint32_t neg;                  // sign bit of the singles (b = 1)
-  bool swap;                     // k xor b
-};
-__device__ inline F32BladeLane f32_blade_lane(int b, int k) {
-  F32BladeLane l;
-  l.off_pair = k ? 6 : 0;
-  l.off_s1 = k ? 2 : 3;
-  l.off_s2 = k ? 4 : 5;
-  l.neg = b ? 0x80000000u : 0u;
-  l.swap = (k ^ b) != 0;
-  return l;
-}
-
 // The contraction over inputs [i0, i1) of one wave's WR blocks of 32 GEMM rows x 32
 // columns: operands of input i are x (re, im) of the lane's GEMM row in block r
-// (arow[r] + 8 i; with BLADE, formed from the blade values there as above) and the
-// eight weight floats of its column (wrow + i w_step), which every row block shares.
-// Blocks of U inputs are double buffered in registers, so one block's loads are in
-// flight while the previous block's MFMAs run.  i0, i1 must be wave-uniform.
-template <int WR, bool BLADE = false>
+// (arow[r] + 8 i) and the eight weight floats of its column (wrow + i w_step), which
+// every row block shares.  Blocks of U inputs are double buffered in registers, so
+// one block's loads are in flight while the previous block's MFMAs run.  i0, i1
+// must be wave-uniform.
+template <int WR>
 __device__ inline void f32_kloop(f32x16v_t (&acc)[WR][2][2], const float* const (&arow)[WR],
-                                 const float* __restrict__ wrow, size_t w_step, int i0, int i1,
-                                 const F32BladeLane bl = F32BladeLane{}) {
+                                 const float* __restrict__ wrow, size_t w_step, int i0, int i1) {
   constexpr int U = WR == 1 ? kF32U : kF32U / 2;
-  using XT = std::conditional_t<BLADE, float4, float2>;  // blade: (pair, s1, s2) as loaded
   struct Ops {
-    XT xa[WR];
+    float2 xa[WR];
     float4 w0, w1;
   };
   auto load_op = [&](int i, Ops& o) {
 #pragma unroll
-    for (int r = 0; r < WR; ++r) {
-      if constexpr (BLADE) {
-        const float* mv = arow[r] + (size_t)i * 8;
-        const float2 pr = *reinterpret_cast<const float2*>(mv + bl.off_pair);
-        o.xa[r] = make_float4(pr.x, pr.y, mv[bl.off_s1], mv[bl.off_s2]);
-      } else {
-        o.xa[r] = *reinterpret_cast<const float2*>(arow[r] + (size_t)i * 8);
-      }
-    }
+    for (int r = 0; r < WR; ++r) o.xa[r] = *reinterpret_cast<const float2*>(arow[r] + (size_t)i * 8);
     o.w0 = *reinterpret_cast<const float4*>(wrow + i * w_step);      // c = 0
     o.w1 = *reinterpret_cast<const float4*>(wrow + i * w_step + 4);  // c = 1
   };
-  auto a_pair = [&](const XT& q) __attribute__((always_inline)) -> float2 {
-    if constexpr (BLADE) {
-      const float u = q.x + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, q.z) ^ bl.neg);
-      const float v = q.y + __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, q.w) ^ bl.neg);
-      return bl.swap ? make_float2(v, u) : make_float2(u, v);
-    } else {
-      return q;
-    }
-  };
   auto mma = [&](const Ops& o) {
-    float2 xa[WR];
-#pragma unroll
-    for (int r = 0; r < WR; ++r) xa[r] = a_pair(o.xa[r]);
 #pragma unroll
     for (int r = 0; r < WR; ++r) {
       f32x16v_t(&a)[2][2] = acc[r];
-      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.x, a[0][0], 0, 0, 0);
-      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.y, a[0][1], 0, 0, 0);
-      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.z, a[1][0], 0, 0, 0);
-      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].x, o.w0.w, a[1][1], 0, 0, 0);
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].x, o.w0.w, a[1][1], 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < WR; ++r) {
       f32x16v_t(&a)[2][2] = acc[r];
-      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.x, a[0][0], 0, 0, 0);
-      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.y, a[0][1], 0, 0, 0);
-      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.z, a[1][0], 0, 0, 0);
-      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[r].y, o.w1.w, a[1][1], 0, 0, 0);
+      a[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.x, a[0][0], 0, 0, 0);
+      a[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.y, a[0][1], 0, 0, 0);
+      a[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.z, a[1][0], 0, 0, 0);
+      a[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.xa[r].y, o.w1.w, a[1][1], 0, 0, 0);
     }
   };
 #pragma unroll
@@ -237,10 +192,12 @@ __device__ inline void f32_store_mv(float y00r, float y00i, float y01r, float y0
 // experts' rows and this expert's tokens in ascending order, and writes the routing
 // arrays of its tile's rows (the first column tile) -- the same counts, offsets,
 // permutation and slot positions as ygg_route.  Workgroup 0 writes counts and
-// offsets.  x is then read as blade rows (no converted copy).
+// offsets.  The tile's rows of x are then read as blade rows and staged in LDS as
+// Pauli rows (no converted copy of x in memory).
 constexpr int kF32FuseTokens = 64 * kF32Waves;           // one token per thread
 constexpr int kF32FuseSlots = kF32FuseTokens * kMaxTopK;
 constexpr int kF32FuseQ = 4;                             // up to 8 RQ logits per token: E <= 32
+constexpr int kF32FuseMaxD = 64;                         // d_in of a routed product: the staged tile fits part
 struct F32Route {
   const float* logits = nullptr;
   int N = 0, k = 0;
@@ -286,6 +243,7 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
   int32_t* const rows_tok = s_wv + kF32Waves;                                 // kF32FuseTokens
   static_assert((2 * kF32FuseSlots + 2 * kMaxExperts + 1 + kF32Waves + kF32FuseTokens) * 4 <= (int)sizeof(part),
                 "routing scratch exceeds the partial-sum buffer");
+  static_assert(RQ == 0 || TOK * (kF32FuseMaxD + 1) * 32 <= (int)sizeof(part), "staged tile exceeds part");
   if constexpr (RQ > 0) {
     const int N = route.N, kk = route.k;
     // one token per thread: its logits, then its selection (select_one_thread)
@@ -388,20 +346,49 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
   const int split = blockIdx.z, splits = gridDim.z;
 
   // A operand: GEMM row (t, b) = l32 of row block r, real (k = 0) or imaginary (k = 1)
-  // part; routed, the token's blade row
+  // part.  Routed: the tile's rows of x, blade to Pauli rows (the conversion's adds),
+  // staged in LDS over part -- every thread issues the loads of its share at once --
+  // with rows padded by one multivector, so that a wave's 16 rows spread over the banks.
   const float* arow[WR];
+  if constexpr (RQ > 0) {
+    float* const xs = reinterpret_cast<float*>(&part[0][0][0]);
+    const int rs = (d_in + 1) * 8;  // floats per staged row
+    const int nq = TOK * d_in;      // multivectors of the tile
+    constexpr int kStage = 2 * kF32Tok * kF32FuseMaxD / (64 * kF32Waves);
+    float4 v[kStage][2];
 #pragma unroll
-  for (int r = 0; r < WR; ++r) {
-    int m = row0 + r * kF32Tok + (l32 >> 1);
-    m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
-    if constexpr (RQ > 0) {
-      arow[r] = X + (size_t)rows_tok[m - row_beg] * d_in * 8;
-    } else {
+    for (int u = 0; u < kStage; ++u) {
+      const int q = tid + u * 64 * kF32Waves;
+      if (q < nq) {
+        const int r = q / d_in, i = q - r * d_in;
+        const int m = min(row0 + r, row_end - 1);  // rows past the expert's range: computed, not stored
+        const float4* src = reinterpret_cast<const float4*>(X + ((size_t)rows_tok[m - row_beg] * d_in + i) * 8);
+        v[u][0] = src[0];
+        v[u][1] = src[1];
+      }
+    }
+    __syncthreads();  // the routing scratch is read: the staged rows may overwrite it
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+      const int q = tid + u * 64 * kF32Waves;
+      if (q < nq) {
+        const int r = q / d_in, i = q - r * d_in;
+        const float b[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w, v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+        store_pauli_f32(xs + r * rs + i * 8, b);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < WR; ++r) arow[r] = xs + (r * kF32Tok + (l32 >> 1)) * rs + ((l32 & 1) * 2 + k) * 2;
+  } else {
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      int m = row0 + r * kF32Tok + (l32 >> 1);
+      m = m < row_end ? m : row_end - 1;  // rows past the expert's range are computed, not stored
       const int src = gather ? gather[m] : m;
       arow[r] = X + (size_t)src * d_in * 8 + ((l32 & 1) * 2 + k) * 2;
     }
   }
-  if constexpr (RQ > 0) __syncthreads();  // every wave has read rows_tok before any writes part
   // B operand: output column j (clamped: columns past d_out are not stored)
   const int jc = min(col0 + l32, d_out - 1);
   const float* wrow = Wp + (((size_t)e * d_in * 2 + k) * d_out + jc) * 8;
@@ -412,7 +399,8 @@ __global__ __launch_bounds__(64 * kF32Waves) __attribute__((amdgpu_waves_per_eu(
   const int i0 = is0 + wave * per_wave, i1 = min(is1, i0 + per_wave);
 
   f32x16v_t acc[WR][2][2];
-  f32_kloop<WR, (RQ > 0)>(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1, f32_blade_lane(l32 & 1, k));
+  f32_kloop<WR>(acc, arow, wrow, (size_t)2 * d_out * 8, i0, i1);
+  if constexpr (RQ > 0) __syncthreads();  // every wave has read the staged rows before part is written
   // lane holds column l32, GEMM rows 8 (v / 4) + 4 k + v % 4 of each row block
   if constexpr (WR == 2) {
     if (wave >= 2) {
@@ -646,15 +634,17 @@ int ygg::pauli_f32_linear_partial(const float* x, int P_max, const float* w, con
                                         y_planes, nullptr, row_map);
 }
 
-bool ygg::pauli_f32_route_fusable(int N, int E, int k) {
-  return N >= 1 && N <= kF32FuseTokens && E >= 1 && E <= kSelLanes * kF32FuseQ && k >= 1 && k <= kMaxTopK && k <= E;
+bool ygg::pauli_f32_route_fusable(int N, int E, int k, int d_in) {
+  return N >= 1 && N <= kF32FuseTokens && E >= 1 && E <= kSelLanes * kF32FuseQ && k >= 1 && k <= kMaxTopK &&
+         k <= E && d_in >= 1 && d_in <= kF32FuseMaxD;
 }
 
 int ygg::pauli_f32_up_routed(const float* x, const float* logits, int N, int E, int k, int32_t* topk_idx,
                              float* topk_w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_pos,
                              int32_t* row_slot, const float* w, const float* bias, int d_in, int d_out, int act,
                              float* y_pauli, float* y_pre, hipStream_t stream) {
-  YGG_CHECK_ARG(pauli_f32_route_fusable(N, E, k), "routed fp32 up product: N=%d E=%d k=%d", N, E, k);
+  YGG_CHECK_ARG(pauli_f32_route_fusable(N, E, k, d_in), "routed fp32 up product: N=%d E=%d k=%d d_in=%d", N, E, k,
+                d_in);
   F32Route r;
   r.logits = logits;
   r.N = N;

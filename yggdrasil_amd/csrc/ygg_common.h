@@ -171,8 +171,8 @@ int pauli_f32_linear_partial(const float* x, int P_max, const float* w, const fl
 // The up product with the routing of the batch inside it (no routing launch): from
 // the logits and the blade rows of x, the routing arrays of ygg_route (and row_slot,
 // when not NULL) and the Pauli rows of h, as pauli_f32_linear_save_pre writes them.
-// For batches of at most 256 tokens and 32 experts.
-bool pauli_f32_route_fusable(int N, int E, int k);
+// For batches of at most 256 tokens, 32 experts and 64 input multivectors.
+bool pauli_f32_route_fusable(int N, int E, int k, int d_in);
 int pauli_f32_up_routed(const float* x, const float* logits, int N, int E, int k, int32_t* topk_idx, float* topk_w,
                         int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_pos, int32_t* row_slot,
                         const float* w, const float* bias, int d_in, int d_out, int act, float* y_pauli,
