@@ -202,36 +202,49 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         if (q == k - 1) rl = row[q];
       rs[s] = s < k ? row[s] : rl;
     }
-    for (int i = lane; i < d; i += 64) {
-      RawMV<YT> y[KM];
-#pragma unroll
-      for (int s = 0; s < KM; ++s) y[s] = load_raw<YT, false>(ys, (size_t)rs[s] * d + i);
-      MV acc;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
+    // two multivectors per lane per round (i and i + 64): every row load of both is in
+    // flight before the first is used (past d the second repeats the first, not stored)
+    for (int i0 = lane; i0 < d; i0 += 128) {
+      const int i1 = i0 + 64 < d ? i0 + 64 : i0;
+      RawMV<YT> y[2][KM];
 #pragma unroll
       for (int s = 0; s < KM; ++s) {
-        float v[8];
-        const uint32_t u[4] = {y[s].a.x, y[s].a.y, y[s].a.z, y[s].a.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          v[2 * c] = bf16_bits_to_f32((uint16_t)(u[c] & 0xffff));
-          v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(u[c] >> 16));
-        }
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc.v[c] = s < k ? acc.v[c] + w[s] * v[c] : acc.v[c];
+        y[0][s] = load_raw<YT, false>(ys, (size_t)rs[s] * d + i0);
+        y[1][s] = load_raw<YT, false>(ys, (size_t)rs[s] * d + i1);
       }
-      if constexpr (Y_MASK) {  // back to blade order
-        const float t3 = acc.v[3];
-        acc.v[3] = acc.v[4];
-        acc.v[4] = t3;
-      }
+      MV r[2];
       if constexpr (RESID) {
-        const MV r = load_mv<OT>(resid, (size_t)t * d + i);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) acc.v[c] = r.v[c] + acc.v[c];
+        r[0] = load_mv<OT>(resid, (size_t)t * d + i0);
+        r[1] = load_mv<OT>(resid, (size_t)t * d + i1);
       }
-      store_mv<OT>(out, (size_t)t * d + i, acc);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        MV acc;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc.v[c] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KM; ++s) {
+          float v[8];
+          const uint32_t u[4] = {y[h][s].a.x, y[h][s].a.y, y[h][s].a.z, y[h][s].a.w};
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v[2 * c] = bf16_bits_to_f32((uint16_t)(u[c] & 0xffff));
+            v[2 * c + 1] = bf16_bits_to_f32((uint16_t)(u[c] >> 16));
+          }
+#pragma unroll
+          for (int c = 0; c < 8; ++c) acc.v[c] = s < k ? acc.v[c] + w[s] * v[c] : acc.v[c];
+        }
+        if constexpr (Y_MASK) {  // back to blade order
+          const float t3 = acc.v[3];
+          acc.v[3] = acc.v[4];
+          acc.v[4] = t3;
+        }
+        if constexpr (RESID) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) acc.v[c] = r[h].v[c] + acc.v[c];
+        }
+        if (h == 0 || i1 != i0) store_mv<OT>(out, (size_t)t * d + (h ? i1 : i0), acc);
+      }
     }
     return;
   }
