@@ -64,6 +64,7 @@ CASES = [
     ("int8 Pauli decode, grade-energy router", torch.bfloat16, "int8_pauli", 48, 20, 64, 128, 8, 2, "energy", True),
     ("bf16 Pauli", torch.bfloat16, "pauli", 512, 96, 32, 64, 8, 2, "logits", True),
     ("fp32 Pauli, grade-energy router", torch.float32, "pauli_f32", 300, 33, 16, 32, 6, 2, "energy", False),
+    ("fp32 Pauli, routed in the up product", torch.float32, "pauli_f32", 200, 37, 32, 64, 8, 2, "logits", True),
     ("bf16 L(w) blocks", torch.bfloat16, "bf16", 200, 40, 16, 32, 4, 3, "logits", False),
 ]
 
