@@ -478,8 +478,10 @@ int ygg::route_convert(const float* logits, int N, int E, int k, int32_t* topk_i
 // One wave per token.  The per-i products are independent: lane i computes them
 // for 64 input multivectors at a time (x and W rows read as contiguous 2 KiB runs
 // across the wave) into LDS, then lane e adds its expert's 64 products in i order
-// to its running sum.  Experts beyond 64 take further passes.
-constexpr int kHeadWaves = 4;
+// to its running sum.  Experts beyond 64 take further passes.  One wave per
+// workgroup: a C1-sized batch (256 tokens) spreads over 256 CUs rather than 64
+// (C1 step 41.4-42.0 -> 41.1-41.3 us).
+constexpr int kHeadWaves = 1;
 
 template <typename XT>
 __global__ __launch_bounds__(64 * kHeadWaves) void router_head_logits_kernel(const XT* __restrict__ x, int N, int d,
