@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import _inputs
-from _gpu_helpers import TOL_BF16, normwise_err, say
+from _gpu_helpers import TOL_BF16, moe_reference, normwise_err, say
 from oracle import moe
 
 pytestmark = pytest.mark.gpu
@@ -67,14 +67,8 @@ def test_prepare_int8_pauli_weights_bit_exact(E, d_out, d_in):
 
 
 def _layer_ref(x, idx, w, wu, bu, wd, bd, act):
-    N = x.shape[0]
-    ref = np.zeros(x.shape, np.float64)
-    for t in range(N):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu[e].astype(np.float32), bu[e],
-                                                 wd[e].astype(np.float32), bd[e], act)[0]
-    return ref
+    return moe_reference(x, idx, w, wu.astype(np.float32), bu, wd.astype(np.float32), bd, act,
+                         acc_dtype=np.float64)
 
 
 @pytest.mark.parametrize("N,d,F,E,k,act", [(64, 128, 512, 32, 2, "gelu"), (1, 16, 32, 4, 1, "relu"),

@@ -11,7 +11,7 @@ import torch
 
 import _inputs
 from _fixtures import LAYER_CASES, load_case
-from _gpu_helpers import TOL_BF16, TOL_F32, normwise_err, say
+from _gpu_helpers import TOL_BF16, TOL_F32, moe_reference, normwise_err, say
 from oracle import moe
 
 pytestmark = pytest.mark.gpu
@@ -232,11 +232,7 @@ def test_decode_int8_skewed_layer():
     assert np.array_equal(idx, idx_o)
     wu_q = moe.dequantize_int8(*moe.quantize_int8(wu))
     wd_q = moe.dequantize_int8(*moe.quantize_int8(wd))
-    ref = np.zeros((N, d, 8), np.float32)
-    for t in range(N):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w_o[t, s] * moe.clifford_ffn(x[t][None], wu_q[e], bu[e], wd_q[e], bd[e], "gelu")[0]
+    ref = moe_reference(x.reshape(N, d, 8), idx, w_o, wu_q, bu, wd_q, bd, "gelu")
     assert normwise_err(y, ref) < TOL_BF16
 
 
@@ -273,11 +269,7 @@ def test_decode_routing_inside_up_product(N, d, F, E, k, act):
     idx, w = r.topk_idx.cpu().numpy(), r.topk_w.cpu().numpy()
     wu_q = moe.dequantize_int8(*moe.quantize_int8(wu))
     wd_q = moe.dequantize_int8(*moe.quantize_int8(wd))
-    ref = np.zeros((N, d, 8), np.float32)
-    for t in range(N):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu_q[e], bu[e], wd_q[e], bd[e], act)[0]
+    ref = moe_reference(x.reshape(N, d, 8), idx, w, wu_q, bu, wd_q, bd, act)
     assert normwise_err(y, ref) < TOL_BF16
 
 

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 import _inputs
-from _gpu_helpers import TOL_BF16, normwise_err, say
+from _gpu_helpers import TOL_BF16, moe_reference, normwise_err, say
 from oracle import moe
 
 pytestmark = pytest.mark.gpu
@@ -233,11 +233,7 @@ def test_layer_formats_against_oracle(fmt):
     idx = layer.last_routing["topk_idx"].cpu().numpy()
     idx_o, w = moe.route_topk(moe.softmax(logits_np), k)
     assert np.array_equal(idx, idx_o)
-    ref = np.zeros((N, d, 8), np.float32)
-    for t in range(N):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w[t, s] * moe.clifford_ffn(x[0, t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+    ref = moe_reference(x[0], idx, w, wu, bu, wd, bd, "gelu")
     assert normwise_err(out, ref) < TOL_BF16
 
 

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from _fixtures import load_case
-from _gpu_helpers import TOL_F32, normwise_err, say
+from _gpu_helpers import TOL_F32, moe_reference, normwise_err, say
 from oracle import moe
 
 pytestmark = pytest.mark.gpu
@@ -154,11 +154,7 @@ def test_layer_pauli_f32_large_down_splits(N, k):
     idx = layer.last_routing["topk_idx"].cpu().numpy()
     idx_o, w = moe.route_topk(moe.softmax(logits_np), k)
     assert np.array_equal(idx, idx_o)
-    ref = x[0].copy()
-    for t in range(N):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w[t, s] * moe.clifford_ffn(x[0, t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+    ref = moe_reference(x[0], idx, w, wu, bu, wd, bd, "gelu", base=x[0])
     assert normwise_err(out, ref) < TOL_F32
 
 
@@ -203,9 +199,5 @@ def test_layer_pauli_f32_routed_up_product(N, E, k, d):
     if N == 200:
         assert (r["counts"].cpu().numpy()[[1, 5, 6]] == 0).all()
     idx, w = r["topk_idx"].cpu().numpy(), r["topk_w"].cpu().numpy()
-    ref = np.zeros_like(x)
-    for t in np.flatnonzero(keep):
-        for s in np.argsort(idx[t]):
-            e = idx[t, s]
-            ref[t] += w[t, s] * moe.clifford_ffn(x[t][None], wu[e], bu[e], wd[e], bd[e], "gelu")[0]
+    ref = moe_reference(x, idx, w, wu, bu, wd, bd, "gelu")
     assert normwise_err(out.cpu().numpy()[keep], ref[keep]) < TOL_F32
