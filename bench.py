@@ -225,6 +225,20 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
     rot = c.get("rotate", 0)
     x, layers = make_inputs(torch, dict(c, layers=rot) if rot else c, seed=SEEDS[name])
     N, d, E, k, F = c["N"], c["d"], c["E"], c["k"], c["F"]
+    qerr = None
+    if rot and c["fmt"] in ("int8", "int8_pauli"):
+        # the int8 formats' error against the fp32 masters they are quantized from, on weight set 0:
+        # the same layer with fp32 activations and the master weights (format 4) as the reference
+        L0 = layers[0]
+        ref, _ = ops.moe_forward(x.float(), k, ops.prepare_weights(L0["w_up"], "pauli_f32"),
+                                 ops.prepare_weights(L0["w_down"], "pauli_f32"), None, None, "gelu",
+                                 logits=L0["logits"])
+        qerr = {}
+        for f in ("int8", "int8_pauli"):
+            o, _ = ops.moe_forward(x, k, ops.prepare_weights(L0["w_up"], f), ops.prepare_weights(L0["w_down"], f),
+                                   None, None, "gelu", logits=L0["logits"])
+            qerr[f] = float(((o.float() - ref).abs().max() / ref.abs().max()).item())
+        del ref, o
     prepared = []
     for L in layers:
         prepared.append(dict(
@@ -312,6 +326,11 @@ def run_layer_config(torch, ops, name, c, steps, warmup):
                    ms_per_step_warm=ms_warm, decode_hbm_frac_warm=moved / (ms_warm * 1e-3) / PEAK_HBM,
                    # the same steps launched one by one from Python (host-bound at this size)
                    ms_per_step_eager=info["ms_eager"])
+        if qerr is not None:
+            res.update(quant_error_vs_fp32=dict(
+                qerr, measured=c["fmt"],
+                basis="max |y_int8 - y_fp32| / max |y_fp32| over the layer's output, weight set 0; y_fp32 the "
+                      "same layer with fp32 activations and the fp32 master weights (format 4)"))
         return res
     # the dominant kernel: both grouped expert products of layer 0, timed alone
     P0 = prepared[0]

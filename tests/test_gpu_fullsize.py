@@ -172,6 +172,38 @@ def test_c4_decode_every_token(fmt):
     assert err.max() < TOL_BF16, (int(err.argmax()), float(err.max()))
 
 
+def test_c4_quantization_error_against_fp32_masters():
+    """BASELINE config 4 quantizes its expert weights to int8 from fp32 masters.  Both int8 formats run
+    the full layer and are compared with the float64 layer on those masters, so the error includes the
+    quantization itself.  Format 2 holds per-output-channel codes of the blade coefficients (the
+    reference quantizer's scheme, bifrost/quantization/grade_quantize.py); format 5 holds codes of the
+    Pauli matrix entries, sums of two blade coefficients, whose per-coefficient bound is about sqrt(2)
+    coarser.  At the layer's output the two measure alike (the float64 oracle on the dequantized weights
+    gives 1.2 % RMS for both at this shape); the bounds: normwise 2e-2, per token 3e-2, and format 5
+    within 1.5 times format 2."""
+    N, d, E, k, F = 64, 128, 32, 2, 512
+    ops = _ops()
+    g = np.random.default_rng(4040)
+    logits = g.standard_normal((N, E), dtype=np.float32)
+    x = _bf16(g.standard_normal((N, d, 8), dtype=np.float32))
+    dev, host = _device_weights(4041, E, d, F, torch.float32)
+    idx, w = moe.route_topk(moe.softmax(logits), k)
+    ref = dense.moe_layer(x, idx, w, host["w_up"], host["b_up"], host["w_down"], host["b_down"], "gelu")
+    errs = {}
+    for fmt in ("int8", "int8_pauli"):
+        P = _layer(ops, dev, fmt)
+        say(f"c4 {fmt} against the fp32 masters, N={N}")
+        out, rt = ops.moe_forward(torch.from_numpy(x).cuda().bfloat16(), k, P["w_up"], P["w_down"], P["b_up"],
+                                  P["b_down"], "gelu", logits=torch.from_numpy(logits).cuda())
+        _check_routing(rt, logits, k)
+        got = out.float().cpu().numpy()
+        errs[fmt] = (normwise_err(got, ref), float(_per_token_err(got, ref).max()))
+        say(f"c4 {fmt}: normwise {errs[fmt][0]:.3e}, worst token {errs[fmt][1]:.3e} against the fp32 masters")
+    for fmt, (nw, tok) in errs.items():
+        assert nw < 2e-2 and tok < 3e-2, (fmt, nw, tok)
+    assert errs["int8_pauli"][0] < 1.5 * errs["int8"][0], errs
+
+
 # ---- config 5: one layer, every token; the 12-layer stack ---------------------------------
 
 
